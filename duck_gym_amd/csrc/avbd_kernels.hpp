@@ -1,0 +1,882 @@
+// gfx950 kernels of the batched AVBD environment step.
+#pragma once
+#include "avbd_step.hpp"
+
+namespace duckhip {
+
+template <int L, class T> __device__ __forceinline__ T groupMax(T v) {
+#pragma unroll
+  for (int o = L / 2; o > 0; o /= 2) {
+    T u = __shfl_xor(v, o, L);
+    v = v > u ? v : u;
+  }
+  return v;
+}
+template <int L> __device__ __forceinline__ int groupOr(int v) {
+#pragma unroll
+  for (int o = L / 2; o > 0; o /= 2)
+    v |= __shfl_xor(v, o, L);
+  return v;
+}
+__device__ __forceinline__ int waveMaxInt(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o /= 2) {
+    int u = __shfl_xor(v, o, 64);
+    v = v > u ? v : u;
+  }
+  return v;
+}
+
+template <class S> __device__ __forceinline__ S &blobAt(unsigned char *base, long long bytes, int e) {
+  return *reinterpret_cast<S *>(base + bytes * e);
+}
+
+// Copy one environment's blob (header + live contacts) between HBM and LDS
+// with the L lanes of its group.
+template <class S>
+__device__ void copyEnv(unsigned *dst, const unsigned *src, int lane, int L, int ngc, int nsc) {
+  constexpr int header = int(headerBytes<S>() / 4);
+  constexpr int CGcap = int(sizeof(S::gc) / sizeof(S::gc[0]));
+  constexpr int CScap = int(sizeof(S::sc) / sizeof(S::sc[0]));
+  ngc = ngc < 0 ? 0 : (ngc > CGcap ? CGcap : ngc);
+  nsc = nsc < 0 ? 0 : (nsc > CScap ? CScap : nsc);
+  for (int i = lane; i < header; i += L)
+    dst[i] = src[i];
+  constexpr int gcWords = int(sizeof(decltype(S::gc[0])) / 4);
+  const int gcStart = header, gcEnd = header + ngc * gcWords;
+  for (int i = gcStart + lane; i < gcEnd; i += L)
+    dst[i] = src[i];
+  constexpr int scStart = int(offsetof(S, sc) / 4);
+  constexpr int scWords = int(sizeof(decltype(S::sc[0])) / 4);
+  const int scEnd = scStart + nsc * scWords;
+  for (int i = scStart + lane; i < scEnd; i += L)
+    dst[i] = src[i];
+}
+
+// MPR narrow phase between two shapes (convex.cuh:124-217), one lane.
+template <class R> struct MprQuery {
+  const DeviceModel<R> &M;
+  const V3<R> *points;
+  int sa, sb;
+  V3<R> xa, xb;
+  Q4<R> qa, qb;
+  R inflation;
+  DUCK_HD V3<R> support1(int s, V3<R> x, Q4<R> q, V3<R> dir, R infl) const {
+    V3<R> ld = rotate(conj(q), dir), local;
+    int type = M.stype[s];
+    V3<R> c{M.center[0][s], M.center[1][s], M.center[2][s]};
+    if (type == 0 || type == 2) {
+      local = c + unitOrNan(ld) * M.size[0][s];
+      if (type == 2) {
+        Q4<R> sq{M.sq[0][s], M.sq[1][s], M.sq[2][s], M.sq[3][s]};
+        V3<R> axis = rotate(sq, V3<R>{0, 0, 1});
+        local = local + axis * (dot(axis, ld) >= 0 ? M.size[1][s] : -M.size[1][s]);
+      }
+    } else {
+      int best = -1, off = M.soffset[s], n = M.scount[s];
+      R value = R(-INFINITY);
+      for (int i = 0; i < n; ++i) {
+        R cand = dot(points[off + i], ld);
+        if (cand > value) {
+          best = i;
+          value = cand;
+        }
+      }
+      local = points[off + (best < 0 ? 0 : best)];
+    }
+    return (x + rotate(q, local)) + dir * infl;
+  }
+  struct SP {
+    V3<R> v, a, b;
+  };
+  DUCK_HD SP support(V3<R> dir) const {
+    SP p;
+    p.a = support1(sa, xa, qa, dir, inflation / R(2));
+    p.b = support1(sb, xb, qb, -dir, inflation / R(2));
+    p.v = p.a - p.b;
+    return p;
+  }
+};
+
+template <class R> struct MprHit {
+  int status;
+  V3<R> normal, position;
+  R depth;
+};
+
+template <class R> DUCK_HD V3<R> closestToOrigin(V3<R> a, V3<R> b, V3<R> c) {
+  V3<R> best = a;
+  R dist = dot(a, a);
+  V3<R> v[3] = {a, b, c};
+  for (int i = 0; i < 3; ++i) {
+    V3<R> start = v[i], edge = v[(i + 1) % 3] - start;
+    R sq = dot(edge, edge);
+    V3<R> p = start + edge * (sq > 0 ? clampv(-dot(start, edge) / sq, R(0), R(1)) : R(0));
+    if (dot(p, p) < dist) {
+      dist = dot(p, p);
+      best = p;
+    }
+  }
+  V3<R> ab = b - a, ac = c - a, n = cross(ab, ac);
+  R nn = dot(n, n);
+  if (nn > 0) {
+    V3<R> p = n * (dot(n, a) / nn);
+    R u = dot(cross(b - p, c - p), n) / nn;
+    R w = dot(cross(c - p, a - p), n) / nn;
+    if (u >= 0 && w >= 0 && u + w <= 1 && dot(p, p) < dist)
+      best = p;
+  }
+  return best;
+}
+
+template <class R> DUCK_HD MprHit<R> mprContact(const MprQuery<R> &Qy, R tolerance) {
+  using SP = typename MprQuery<R>::SP;
+  MprHit<R> hit{0, {0, 0, 0}, {0, 0, 0}, 0};
+  SP p[4];
+  const auto &M = Qy.M;
+  V3<R> ia{M.interior[0][Qy.sa], M.interior[1][Qy.sa], M.interior[2][Qy.sa]};
+  V3<R> ib{M.interior[0][Qy.sb], M.interior[1][Qy.sb], M.interior[2][Qy.sb]};
+  p[0].a = Qy.xa + rotate(Qy.qa, ia);
+  p[0].b = Qy.xb + rotate(Qy.qb, ib);
+  p[0].v = p[0].a - p[0].b;
+  R size = mx(R(0.001), M.radius[Qy.sa] + M.radius[Qy.sb]);
+  R eps = tolerance * R(0.01);
+  if (norm(p[0].v) < eps)
+    p[0].v.x += eps * R(10);
+  V3<R> dir = unitOrNan(-p[0].v);
+  p[1] = Qy.support(dir);
+  if (dot(p[1].v, dir) <= 0)
+    return hit;
+  dir = cross(p[0].v, p[1].v);
+  if (norm(dir) <= eps * size) {
+    hit.status = 1;
+    hit.depth = norm(p[1].v);
+    hit.normal = hit.depth > eps ? -unitOrNan(p[1].v) : unitOrNan(p[0].v);
+    hit.position = divide(p[1].a + p[1].b, R(2));
+    return hit;
+  }
+  dir = unitOrNan(dir);
+  p[2] = Qy.support(dir);
+  if (dot(p[2].v, dir) <= 0)
+    return hit;
+  dir = unitOrNan(cross(p[1].v - p[0].v, p[2].v - p[0].v));
+  if (dot(dir, p[0].v) > 0) {
+    SP t = p[1];
+    p[1] = p[2];
+    p[2] = t;
+    dir = -dir;
+  }
+  bool discovered = false;
+  for (int it = 0; it < 128; ++it) {
+    if (!mfinite(dir.x))
+      break;
+    p[3] = Qy.support(dir);
+    if (dot(p[3].v, dir) <= 0)
+      return hit;
+    if (dot(cross(p[1].v, p[3].v), p[0].v) < -eps * size * size) {
+      p[2] = p[3];
+    } else if (dot(cross(p[3].v, p[2].v), p[0].v) < -eps * size * size) {
+      p[1] = p[3];
+    } else {
+      discovered = true;
+      break;
+    }
+    dir = unitOrNan(cross(p[1].v - p[0].v, p[2].v - p[0].v));
+  }
+  if (!discovered) {
+    hit.status = -1;
+    return hit;
+  }
+  auto portalDir = [&]() { return unitOrNan(cross(p[2].v - p[1].v, p[3].v - p[1].v)); };
+  auto advanceOf = [&](const SP &s, V3<R> d) {
+    return dot(s.v, d) - mx(dot(p[1].v, d), mx(dot(p[2].v, d), dot(p[3].v, d)));
+  };
+  auto expand = [&](const SP &v) {
+    V3<R> c = cross(v.v, p[0].v);
+    if (dot(p[1].v, c) > 0) {
+      if (dot(p[2].v, c) > 0)
+        p[1] = v;
+      else
+        p[3] = v;
+    } else if (dot(p[3].v, c) > 0) {
+      p[2] = v;
+    } else {
+      p[1] = v;
+    }
+  };
+  bool inside = false;
+  for (int it = 0; it < 128; ++it) {
+    dir = portalDir();
+    if (!mfinite(dir.x))
+      break;
+    if (dot(dir, p[1].v) >= -eps) {
+      inside = true;
+      break;
+    }
+    SP s = Qy.support(dir);
+    if (dot(s.v, dir) < 0 || advanceOf(s, dir) <= tolerance)
+      return hit;
+    expand(s);
+  }
+  if (!inside) {
+    hit.status = -1;
+    return hit;
+  }
+  for (int it = 0; it < 256; ++it) {
+    dir = portalDir();
+    if (!mfinite(dir.x))
+      break;
+    SP s = Qy.support(dir);
+    if (advanceOf(s, dir) <= tolerance) {
+      V3<R> closest = closestToOrigin(p[1].v, p[2].v, p[3].v);
+      hit.depth = norm(closest);
+      hit.normal = hit.depth > eps ? -divide(closest, hit.depth) : -dir;
+      // Barycentric position on the portal (convex.cuh:105-123).
+      R w[4] = {dot(cross(p[1].v, p[2].v), p[3].v), dot(cross(p[3].v, p[2].v), p[0].v),
+                dot(cross(p[0].v, p[1].v), p[3].v), dot(cross(p[2].v, p[1].v), p[0].v)};
+      R sum = w[0] + w[1] + w[2] + w[3];
+      if (!(sum > 0)) {
+        w[0] = 0;
+        w[1] = dot(cross(p[2].v, p[3].v), dir);
+        w[2] = dot(cross(p[3].v, p[1].v), dir);
+        w[3] = dot(cross(p[1].v, p[2].v), dir);
+        sum = w[1] + w[2] + w[3];
+      }
+      if (!(sum > 0)) {
+        hit.position = {R(NAN), R(NAN), R(NAN)};
+      } else {
+        V3<R> pos{0, 0, 0};
+        for (int i = 0; i < 4; ++i)
+          pos = pos + (p[i].a + p[i].b) * (w[i] / (R(2) * sum));
+        hit.position = pos;
+      }
+      hit.status = mfinite(hit.position.x) ? 1 : -1;
+      return hit;
+    }
+    expand(s);
+  }
+  hit.status = -1;
+  return hit;
+}
+
+// Per-launch kernel: controls, `substeps` physics steps, write-back.
+template <class R, int B, int J, int CG, int CS, int L>
+__global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
+  constexpr int G = 64 / L;
+  constexpr int PPL = (CS + L - 1) / L; // pairs per lane (pairs <= CS)
+  constexpr int SPL = (B + L - 1) / L;  // shapes per lane (shapes <= B)
+  using Env = EnvLds<R, B, J, CG, CS>;
+  using State = EnvState<R, B, J, CG, CS>;
+  __shared__ Frames<R, B, J> F;
+  __shared__ Env envs[G];
+
+  const DeviceModel<R> &M = *static_cast<const DeviceModel<R> *>(args.model);
+  const V3<R> *points = static_cast<const V3<R> *>(args.points);
+  const int t = threadIdx.x, lane = t % L, g = t / L;
+  const int e = blockIdx.x * G + g;
+  const bool valid = e < args.count;
+  Env &E = envs[g];
+  const int nb = M.nb, nj = M.nj, ns = M.ns, np = M.np;
+
+  // Stage the joint model (all 64 lanes).
+  for (int j = t; j < nj; j += 64) {
+    F.a[j] = M.ja[j];
+    F.b[j] = M.jb[j];
+    F.limited[j] = M.limited[j];
+    for (int k = 0; k < 3; ++k) {
+      F.ra[k][j] = M.ra[k][j];
+      F.rb[k][j] = M.rb[k][j];
+      F.axisA[k][j] = M.axisA[k][j];
+      F.axisB[k][j] = M.axisB[k][j];
+      F.tangentA[k][j] = M.tangentA[k][j];
+      F.tangentB[k][j] = M.tangentB[k][j];
+    }
+    F.lo[j] = M.lo[j];
+    F.hi[j] = M.hi[j];
+    F.armature[j] = M.armature[j];
+  }
+  for (int i = t; i <= nb; i += 64)
+    F.adjStart[i] = M.adjStart[i];
+  for (int i = t; i < 2 * nj; i += 64)
+    F.adj[i] = M.adj[i];
+  for (int i = t; i < ns; i += 64)
+    F.shapeFriction[i] = M.sfriction[i];
+
+  State *gs = valid ? &blobAt<State>(args.states, args.blobBytes, e) : nullptr;
+  if (valid)
+    copyEnv<State>(reinterpret_cast<unsigned *>(&E.s), reinterpret_cast<const unsigned *>(gs), lane,
+                   L, gs->ngc, gs->nsc);
+  __syncthreads();
+
+  // ---- controls (extension.cu:87-110 / kernel.cuh:448-466) ----
+  int bad = 0;
+  if (valid) {
+    if (args.motorMode) {
+      const R *motor = static_cast<const R *>(args.motor) + size_t(e) * nj * 3;
+      for (int j = lane; j < nj; j += L) {
+        R m0 = motor[3 * j], m1 = motor[3 * j + 1], m2 = motor[3 * j + 2];
+        if (!mfinite(m0) || !mfinite(m1) || !mfinite(m2) || m1 < 0 || m2 < 0)
+          bad = 1;
+      }
+    } else {
+      const R *target = static_cast<const R *>(args.targets) + size_t(e) * nj;
+      for (int j = lane; j < nj; j += L)
+        if (!mfinite(target[j]))
+          bad = 1;
+    }
+    const R *force = static_cast<const R *>(args.forces) + size_t(e) * 3;
+    if (lane < 3 && !mfinite(force[lane]))
+      bad = 1;
+  }
+  bad = groupOr<L>(bad);
+  __syncthreads();
+  bool active = false;
+  if (valid) {
+    const R *force = static_cast<const R *>(args.forces) + size_t(e) * 3;
+    if (args.motorMode) {
+      // setMotor applies the channels even when they are invalid.
+      const R *motor = static_cast<const R *>(args.motor) + size_t(e) * nj * 3;
+      for (int j = lane; j < nj; j += L) {
+        E.s.kp[j] = 0;
+        E.s.maxTorque[j] = 0;
+        E.s.torque[j] = motor[3 * j];
+        E.s.frictionloss[j] = motor[3 * j + 1];
+        E.s.damping[j] = motor[3 * j + 2];
+      }
+      if (lane < 3)
+        E.s.force[lane] = force[lane];
+      if (bad && lane == 0)
+        E.s.failed = 1;
+      active = !E.s.failed && !bad;
+    } else if (!E.s.failed && !bad) {
+      const R *target = static_cast<const R *>(args.targets) + size_t(e) * nj;
+      for (int j = lane; j < nj; j += L) {
+        E.s.target[j] = target[j];
+        E.s.kp[j] = R(args.kp);
+        E.s.maxTorque[j] = R(args.limit);
+        E.s.torque[j] = M.torque[j];
+        E.s.frictionloss[j] = M.frictionloss[j];
+        E.s.damping[j] = M.damping[j];
+      }
+      if (lane < 3)
+        E.s.force[lane] = force[lane];
+      active = true;
+    } else {
+      if (lane == 0)
+        E.s.failed = 1;
+    }
+  }
+  const bool ran = active;
+  if (ran && lane == 0) {
+    for (int k = 0; k < 8; ++k)
+      E.stepDiag[k] = 0;
+    E.s.diag[kJointError] = 0;
+    E.s.diag[kAxisError] = 0;
+    E.s.diag[kPenetration] = 0;
+    E.s.diag[kContacts] = 0;
+    E.s.diag[kConverged] = 1;
+    E.s.diag[kIterations] = 0;
+  }
+  __syncthreads();
+
+  Stepper<R, B, J, CG, CS, L> stp{M, points, F, E, lane};
+  const R h = M.dt, alpha = M.alpha, gamma = M.gamma, ag = alpha * gamma;
+
+  for (int sub = 0; sub < args.substeps; ++sub) {
+    if (!__any(active))
+      break;
+    // ---------------- detection: ground manifolds (kernel.cuh:601-653) ----
+    int picks[SPL][4], npick[SPL], src[SPL][4];
+    V3<R> pickLocal[SPL][4];
+#pragma unroll
+    for (int r = 0; r < SPL; ++r) {
+      npick[r] = 0;
+      const int si = lane + r * L;
+      if (!active || si >= ns)
+        continue;
+      const int b = M.sbody[si];
+      const R mass = E.s.mass[b];
+      if (!M.ground || !M.sground[si] || mass == 0) {
+        E.shapeCount[si] = 0;
+        continue;
+      }
+      V3<R> x = stp.X(b), v = stp.Vel(b), w = stp.Omega(b);
+      Q4<R> q = stp.Q(b);
+      const R gz = M.gravity[2] + stp.forceZ(b) / mass;
+      R low = mn(x.z, x.z + h * v.z + h * h * gz);
+      if (double(low - M.radius[si] * (R(1) + h * norm(w))) >= .003) {
+        E.shapeCount[si] = 0;
+        continue;
+      }
+      const int type = M.stype[si], count = M.scount[si], off = M.soffset[si];
+      V3<R> c{M.center[0][si], M.center[1][si], M.center[2][si]};
+      auto pointOf = [&](int k) {
+        if (type == 1 || type == 3)
+          return points[off + k];
+        V3<R> down = rotate(conj(q), V3<R>{0, 0, -M.size[0][si]});
+        if (type == 0)
+          return c + down;
+        Q4<R> sq{M.sq[0][si], M.sq[1][si], M.sq[2][si], M.sq[3][si]};
+        return (c + rotate(sq, V3<R>{0, 0, (k ? R(1) : R(-1)) * M.size[1][si]})) + down;
+      };
+      V3<R> chosen[4];
+      int n = 0;
+#pragma unroll
+      for (int pk = 0; pk < 4; ++pk) {
+        if (n < pk)
+          break;
+        int best = -1;
+        R lowest = R(INFINITY);
+        V3<R> bestLocal{0, 0, 0}, bestWorld{0, 0, 0};
+        for (int k = 0; k < count; ++k) {
+          V3<R> local = pointOf(k), world = x + rotate(q, local);
+          V3<R> vel = v + cross(w, world - x);
+          R z = mn(world.z, world.z + h * vel.z + h * h * gz);
+          if (double(z) >= .003 || z >= lowest)
+            continue;
+          bool dup = false;
+#pragma unroll
+          for (int cc = 0; cc < 4; ++cc)
+            if (cc < pk && double(mhypot(chosen[cc].x - world.x, chosen[cc].y - world.y)) < .005)
+              dup = true;
+          if (dup)
+            continue;
+          best = k;
+          lowest = z;
+          bestLocal = local;
+          bestWorld = world;
+        }
+        if (best >= 0) {
+          picks[r][pk] = best;
+          pickLocal[r][pk] = bestLocal;
+          chosen[pk] = bestWorld;
+          n = pk + 1;
+        }
+      }
+      npick[r] = n;
+      E.shapeCount[si] = n;
+      // Warm-start source in the previous list (still in LDS).
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        src[r][p] = -1;
+        if (p >= n)
+          continue;
+        for (int i = 0; i < E.s.ngc; ++i) {
+          int id = E.s.gc[i].id;
+          if (gcShape(id) == si && gcFeature(id) == picks[r][p]) {
+            src[r][p] = i;
+            break;
+          }
+        }
+      }
+    }
+    // ---------------- detection: body-body pairs (kernel.cuh:656-722) ----
+    struct PairGeom {
+      V3<R> n, t1, t2, local, localB;
+      R c0;
+      int src;
+    };
+    PairGeom pg[PPL];
+#pragma unroll
+    for (int r = 0; r < PPL; ++r) {
+      const int pi = lane + r * L;
+      if (!active || pi >= np)
+        continue;
+      E.pairHit[pi] = 0;
+      const int sa = M.pa[pi], sb = M.pb[pi], A = M.sbody[sa], Bb = M.sbody[sb];
+      if (E.s.mass[A] == 0 && E.s.mass[Bb] == 0)
+        continue;
+      V3<R> xa = stp.X(A), xb = stp.X(Bb);
+      Q4<R> qa = stp.Q(A), qb = stp.Q(Bb);
+      R skin = R(.003) + h * (norm(stp.Vel(A) - stp.Vel(Bb)) + norm(stp.Omega(A)) * M.radius[sa] +
+                              norm(stp.Omega(Bb)) * M.radius[sb]);
+      if (norm(xa - xb) > M.radius[sa] + M.radius[sb] + skin)
+        continue;
+      MprQuery<R> qy{M, points, sa, sb, xa, xb, qa, qb, skin};
+      MprHit<R> hit = mprContact(qy, mx(R(1e-8), M.tolerance * R(.1)));
+      if (hit.status < 0) {
+        E.s.failed = 1;
+        continue;
+      }
+      if (hit.status == 0)
+        continue;
+      PairGeom &o = pg[r];
+      o.n = hit.normal;
+      o.t1 = unitOrNan(cross(mabs(o.n.x) < R(.8) ? V3<R>{1, 0, 0} : V3<R>{0, 1, 0}, o.n));
+      o.t2 = cross(o.n, o.t1);
+      R gap = skin - hit.depth;
+      o.local = rotate(conj(qa), (hit.position + o.n * (gap / R(2))) - xa);
+      o.localB = rotate(conj(qb), (hit.position - o.n * (gap / R(2))) - xb);
+      o.c0 = mn(gap, R(0));
+      o.src = -1;
+      for (int i = 0; i < E.s.nsc; ++i) {
+        const SelfContact<R> &old = E.s.sc[i];
+        V3<R> on{old.n[0], old.n[1], old.n[2]};
+        V3<R> ol{old.local[0], old.local[1], old.local[2]},
+            olb{old.localB[0], old.localB[1], old.localB[2]};
+        if (scShape(old.id) == sa && scOtherShape(old.id) == sb && dot(on, o.n) > R(.95) &&
+            norm(rotate(qa, ol - o.local)) < R(.005) && norm(rotate(qb, olb - o.localB)) < R(.005)) {
+          o.src = i;
+          break;
+        }
+      }
+      E.pairHit[pi] = 1;
+    }
+    __syncthreads();
+    // ---------------- compaction + warm start ----------------------------
+    if (active) {
+      int total = 0;
+      for (int si = 0; si < ns; ++si)
+        total += E.shapeCount[si];
+      if (total > CG && lane == 0)
+        E.s.failed = 1;
+#pragma unroll
+      for (int r = 0; r < SPL; ++r) {
+        const int si = lane + r * L;
+        if (si >= ns || npick[r] == 0)
+          continue;
+        int offset = 0;
+        for (int k = 0; k < si; ++k)
+          offset += E.shapeCount[k];
+        const int b = M.sbody[si];
+        V3<R> x = stp.X(b);
+        Q4<R> q = stp.Q(b);
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+          if (p >= npick[r] || offset + p >= CG)
+            break;
+          GroundContact<R> c;
+          V3<R> local = pickLocal[r][p], world = x + rotate(q, local);
+          R lam[3] = {0, 0, 0}, pen[3] = {1000, 1000, 1000};
+          R anchor[2] = {world.x, world.y};
+          if (src[r][p] >= 0) {
+            const GroundContact<R> &old = gs->gc[src[r][p]];
+            for (int d = 0; d < 3; ++d) {
+              lam[d] = old.lambda[d];
+              pen[d] = old.penalty[d];
+            }
+            if (gcStick(old.id)) {
+              local = {old.local[0], old.local[1], old.local[2]};
+              anchor[0] = old.anchor[0];
+              anchor[1] = old.anchor[1];
+            }
+          }
+          c.id = gcPack(si, b, picks[r][p], false);
+          c.local[0] = local.x;
+          c.local[1] = local.y;
+          c.local[2] = local.z;
+          c.anchor[0] = anchor[0];
+          c.anchor[1] = anchor[1];
+          c.c0 = mn((x + rotate(q, local)).z, R(0));
+          for (int d = 0; d < 3; ++d) {
+            c.lambda[d] = lam[d] * ag;
+            c.penalty[d] = clampv(pen[d] * gamma, R(1000), R(1e9));
+          }
+          E.s.gc[offset + p] = c;
+        }
+      }
+      if (lane == 0)
+        E.s.ngc = total > CG ? CG : total;
+#pragma unroll
+      for (int r = 0; r < PPL; ++r) {
+        const int pi = lane + r * L;
+        if (pi >= np || !E.pairHit[pi])
+          continue;
+        int slot = 0;
+        for (int k = 0; k < pi; ++k)
+          slot += E.pairHit[k];
+        if (slot >= CS) {
+          E.s.failed = 1;
+          continue;
+        }
+        const PairGeom &o = pg[r];
+        const int sa = M.pa[pi], sb = M.pb[pi];
+        SelfContact<R> c;
+        c.id = scPack(M.sbody[sa], M.sbody[sb], sa, sb, false);
+        R lam[3] = {0, 0, 0}, pen[3] = {1000, 1000, 1000};
+        if (o.src >= 0) {
+          const SelfContact<R> &old = gs->sc[o.src];
+          V3<R> f = ((V3<R>{old.t1[0], old.t1[1], old.t1[2]} * old.lambda[0]) +
+                     (V3<R>{old.t2[0], old.t2[1], old.t2[2]} * old.lambda[1])) +
+                    (V3<R>{old.n[0], old.n[1], old.n[2]} * old.lambda[2]);
+          lam[0] = dot(f, o.t1);
+          lam[1] = dot(f, o.t2);
+          lam[2] = dot(f, o.n);
+          for (int d = 0; d < 3; ++d)
+            pen[d] = old.penalty[d];
+        }
+        V3<R> vs[5] = {o.local, o.localB, o.t1, o.t2, o.n};
+        R *dst[5] = {c.local, c.localB, c.t1, c.t2, c.n};
+        for (int v = 0; v < 5; ++v) {
+          dst[v][0] = vs[v].x;
+          dst[v][1] = vs[v].y;
+          dst[v][2] = vs[v].z;
+        }
+        c.c0 = o.c0;
+        c.friction = M.pfriction[pi];
+        for (int d = 0; d < 3; ++d) {
+          c.lambda[d] = lam[d] * ag;
+          c.penalty[d] = clampv(pen[d] * gamma, R(1000), R(1e9));
+        }
+        E.s.sc[slot] = c;
+      }
+    }
+    __syncthreads();
+    // ---------------- colours (kernel.cuh:596-598, 717-720) -------------
+    if (active && lane == 0) {
+      int nsc = 0;
+      for (int pi = 0; pi < np; ++pi)
+        nsc += E.pairHit[pi];
+      E.s.nsc = nsc < CS ? nsc : CS;
+      for (int b = 0; b < nb; ++b)
+        E.s.colors[b] = M.colors[b];
+      int cc = 2;
+      for (int i = 0; i < E.s.nsc; ++i) {
+        int a = scBody(E.s.sc[i].id), b = scOther(E.s.sc[i].id);
+        if (E.s.mass[a] > 0 && E.s.mass[b] > 0 && E.s.colors[a] == E.s.colors[b])
+          E.s.colors[b] = cc++;
+      }
+      E.s.colorCount = cc;
+      for (int c = 0; c <= cc; ++c)
+        E.colorStart[c] = 0;
+      for (int b = 0; b < nb; ++b)
+        if (E.s.mass[b] > 0)
+          E.colorStart[E.s.colors[b] + 1] += 1;
+      for (int c = 0; c < cc; ++c)
+        E.colorStart[c + 1] += E.colorStart[c];
+      int pos = 0;
+      for (int c = 0; c < cc; ++c)
+        for (int b = 0; b < nb; ++b)
+          if (E.s.mass[b] > 0 && E.s.colors[b] == c)
+            E.order[pos++] = b;
+      E.done = 0;
+      for (int k = 0; k < 8; ++k)
+        E.stepDiag[k] = 0;
+    }
+    __syncthreads();
+    if (active && E.s.failed)
+      active = false; // detection failure ends this env's launch
+    // ---------------- warm start, predictor, contact masks ---------------
+    if (active) {
+      for (int ji = lane; ji < nj; ji += L) {
+        auto je = stp.evalJoint(ji);
+        for (int k = 0; k < 7; ++k)
+          E.c0[k][ji] = je.C[k];
+        E.angle0[ji] = je.angle;
+        E.s.lambdaF[ji] *= ag;
+        E.s.penaltyF[ji] = clampv(E.s.penaltyF[ji] * gamma, R(1), R(1e7));
+        const int a = F.a[ji], b = F.b[ji];
+        E.velocity0[ji] = dot(stp.Omega(b) - stp.Omega(a), je.axis);
+        for (int k = 0; k < 7; ++k) {
+          E.s.lambda[k][ji] *= ag;
+          E.s.penalty[k][ji] =
+              clampv(E.s.penalty[k][ji] * gamma, k < 3 ? R(1000) : R(1), k < 3 ? R(1e9) : R(1e7));
+        }
+      }
+    }
+    __syncthreads(); // joint warm start reads the poses the predictor overwrites
+    if (active) {
+      for (int b = lane; b < nb; b += L) {
+        V3<R> x = stp.X(b);
+        Q4<R> q = stp.Q(b);
+        for (int k = 0; k < 3; ++k)
+          E.x0[k][b] = comp(x, k);
+        E.q0[0][b] = q.w;
+        E.q0[1][b] = q.x;
+        E.q0[2][b] = q.y;
+        E.q0[3][b] = q.z;
+        uint64_t gm = 0;
+        for (int i = 0; i < E.s.ngc; ++i)
+          if (gcBody(E.s.gc[i].id) == b)
+            gm |= uint64_t(1) << i;
+        uint32_t sm = 0;
+        for (int i = 0; i < E.s.nsc; ++i) {
+          int id = E.s.sc[i].id;
+          if (scBody(id) == b || scOther(id) == b)
+            sm |= 1u << i;
+        }
+        E.gmask[b] = gm;
+        E.smask[b] = sm;
+        const R mass = E.s.mass[b];
+        if (mass == 0)
+          continue;
+        V3<R> v = stp.Vel(b), w = stp.Omega(b), I = stp.Inertia(b);
+        V3<R> xp = (x + h * v) + (h * h) * (V3<R>{M.gravity[0], M.gravity[1], M.gravity[2]} +
+                                            divide(stp.force(b), mass));
+        V3<R> spin = -cross(w, stp.inertiaApply(q, I, w, false));
+        V3<R> wp = w + h * stp.inertiaApply(q, I, spin, true);
+        Q4<R> qp = expmap(h * wp) * q;
+        for (int k = 0; k < 3; ++k)
+          E.xp[k][b] = comp(xp, k);
+        E.qp[0][b] = qp.w;
+        E.qp[1][b] = qp.x;
+        E.qp[2][b] = qp.y;
+        E.qp[3][b] = qp.z;
+        stp.setX(b, xp);
+        stp.setQ(b, qp);
+      }
+    }
+    int colours = waveMaxInt(active ? E.s.colorCount : 0);
+    __syncthreads();
+    // ---------------- AVBD iterations (kernel.cuh:979-1063) ---------------
+    for (int it = 0; it < M.iterations; ++it) {
+      const bool work = active && !E.done;
+      if (!__any(work))
+        break;
+      R maxUpdate = 0;
+      for (int c = 0; c < colours; ++c) {
+        if (work && c < E.s.colorCount)
+          for (int k = E.colorStart[c] + lane; k < E.colorStart[c + 1]; k += L)
+            maxUpdate = mx(maxUpdate, stp.updateBody(E.order[k], true));
+        __syncthreads();
+      }
+      maxUpdate = groupMax<L>(maxUpdate);
+      R error = 0;
+      if (work) {
+        for (int ji = lane; ji < nj; ji += L) {
+          auto je = stp.evalJoint(ji);
+          const int rows = F.limited[ji] ? 7 : 5;
+          for (int k = 0; k < rows; ++k) {
+            R c0 = E.c0[k][ji];
+            R c = je.C[k] - alpha * (k < 5 ? c0 : mn(c0, R(0)));
+            R f = E.s.lambda[k][ji] + E.s.penalty[k][ji] * c;
+            E.s.lambda[k][ji] = k >= 5 ? mn(f, R(0)) : f;
+            if (k < 5 || f < 0)
+              E.s.penalty[k][ji] =
+                  mn(E.s.penalty[k][ji] + (k < 3 ? M.betaLinear : M.betaAngular) * mabs(c),
+                     k < 3 ? R(1e9) : R(1e7));
+            error = mx(error, k < 5 ? mabs(c) : mx(R(0), -c));
+          }
+          const R fl = E.s.frictionloss[ji];
+          if (fl > 0) {
+            R delta = wrapAngle(je.angle - E.angle0[ji]);
+            R trial = E.s.lambdaF[ji] + E.s.penaltyF[ji] * delta;
+            E.s.lambdaF[ji] = clampv(trial, -fl, fl);
+            if (mabs(trial) < fl)
+              E.s.penaltyF[ji] = mn(E.s.penaltyF[ji] + M.betaAngular * mabs(delta), R(1e7));
+            R residual = E.s.lambdaF[ji] + E.s.penaltyF[ji] * delta;
+            error = mx(error, mabs(E.s.lambdaF[ji] - clampv(residual, -fl, fl)) / E.s.penaltyF[ji]);
+          }
+        }
+        for (int i = lane; i < E.s.ngc; i += L) {
+          GroundContact<R> &c = E.s.gc[i];
+          V3<R> ra;
+          V3<R> C = stp.groundC(c, ra);
+          const R mu = stp.groundFriction(gcShape(c.id));
+          V3<R> f = contactForce(C, c.lambda, c.penalty, mu);
+          R trial = mhypot(c.lambda[0] + c.penalty[0] * C.x, c.lambda[1] + c.penalty[1] * C.y);
+          bool stick = trial <= -mu * f.z && double(mhypot(C.x, C.y)) < 1e-5;
+          c.id = (c.id & 0x7fffffff) | (stick ? int(0x80000000u) : 0);
+          R fk[3] = {f.x, f.y, f.z}, Ck[3] = {C.x, C.y, C.z};
+          for (int k = 0; k < 3; ++k) {
+            c.lambda[k] = fk[k];
+            if (f.z < 0 && (k == 2 || trial <= -mu * f.z))
+              c.penalty[k] = mn(c.penalty[k] + M.betaLinear * mabs(Ck[k]), R(1e9));
+          }
+          error = mx(error, mx(R(0), -C.z));
+        }
+        for (int i = lane; i < E.s.nsc; i += L) {
+          SelfContact<R> &c = E.s.sc[i];
+          V3<R> ra, rb;
+          V3<R> C = stp.selfC(c, ra, rb);
+          V3<R> f = contactForce(C, c.lambda, c.penalty, c.friction);
+          R trial = mhypot(c.lambda[0] + c.penalty[0] * C.x, c.lambda[1] + c.penalty[1] * C.y);
+          bool stick = trial <= -c.friction * f.z && double(mhypot(C.x, C.y)) < 1e-5;
+          c.id = (c.id & 0x7fffffff) | (stick ? int(0x80000000u) : 0);
+          R fk[3] = {f.x, f.y, f.z}, Ck[3] = {C.x, C.y, C.z};
+          for (int k = 0; k < 3; ++k) {
+            c.lambda[k] = fk[k];
+            if (f.z < 0 && (k == 2 || trial <= -c.friction * f.z))
+              c.penalty[k] = mn(c.penalty[k] + M.betaLinear * mabs(Ck[k]), R(1e9));
+          }
+          error = mx(error, mx(R(0), -C.z));
+        }
+      }
+      error = groupMax<L>(error);
+      if (work && lane == 0) {
+        E.stepDiag[kIterations] = R(it + 1);
+        const bool conv = maxUpdate < M.tolerance && error < M.tolerance;
+        E.stepDiag[kConverged] = conv ? R(1) : R(0);
+        if (conv)
+          E.done = 1;
+      }
+      __syncthreads();
+    }
+    // ---------------- velocity recovery (kernel.cuh:1064-1073) ------------
+    if (active) {
+      const R invh = R(1) / h;
+      for (int b = lane; b < nb; b += L) {
+        if (E.s.mass[b] == 0)
+          continue;
+        V3<R> x = stp.X(b), x0{E.x0[0][b], E.x0[1][b], E.x0[2][b]};
+        V3<R> v = (x - x0) * invh;
+        V3<R> w = logmap(stp.Q(b) * conj(stp.Q0(b))) * invh;
+        for (int k = 0; k < 3; ++k) {
+          E.s.v[k][b] = comp(v, k);
+          E.s.w[k][b] = comp(w, k);
+        }
+        if (!mfinite(norm(x) + norm(v) + norm(w)))
+          E.s.failed = 1;
+      }
+    }
+    __syncthreads();
+    if (active && E.s.failed)
+      active = false;
+    // ---------------- diagnostics and substep summary ---------------------
+    R jointErr = 0, axisErr = 0, pen = 0;
+    if (active) {
+      for (int ji = lane; ji < nj; ji += L) {
+        auto je = stp.evalJoint(ji);
+        for (int k = 0; k < 3; ++k)
+          jointErr = mx(jointErr, mabs(je.C[k]));
+        for (int k = 3; k < 5; ++k)
+          axisErr = mx(axisErr, mabs(je.C[k]));
+      }
+      for (int i = lane; i < E.s.ngc; i += L) {
+        V3<R> ra;
+        V3<R> C = stp.groundC(E.s.gc[i], ra);
+        pen = mx(pen, mx(R(0), -(C.z + alpha * E.s.gc[i].c0)));
+      }
+      for (int i = lane; i < E.s.nsc; i += L) {
+        V3<R> ra, rb;
+        V3<R> C = stp.selfC(E.s.sc[i], ra, rb);
+        pen = mx(pen, mx(R(0), -(C.z + alpha * E.s.sc[i].c0)));
+      }
+    }
+    jointErr = groupMax<L>(jointErr);
+    axisErr = groupMax<L>(axisErr);
+    pen = groupMax<L>(pen);
+    if (active && lane == 0) {
+      R *d = E.s.diag;
+      d[kJointError] = mx(d[kJointError], jointErr);
+      d[kAxisError] = mx(d[kAxisError], axisErr);
+      d[kPenetration] = mx(d[kPenetration], pen);
+      d[kContacts] = mx(d[kContacts], R(E.s.ngc + E.s.nsc));
+      d[kConverged] = (d[kConverged] != 0 && E.stepDiag[kConverged] != 0) ? R(1) : R(0);
+      d[kIterations] += E.stepDiag[kIterations];
+    }
+    __syncthreads();
+    // The next substep warm-starts from the HBM copy of this contact list.
+    if (active && sub + 1 < args.substeps) {
+      constexpr int header = int(headerBytes<State>() / 4);
+      constexpr int gcWords = int(sizeof(GroundContact<R>) / 4);
+      constexpr int scStart = int(offsetof(State, sc) / 4), scWords = int(sizeof(SelfContact<R>) / 4);
+      const unsigned *s = reinterpret_cast<const unsigned *>(&E.s);
+      unsigned *d = reinterpret_cast<unsigned *>(gs);
+      for (int i = header + lane; i < header + E.s.ngc * gcWords; i += L)
+        d[i] = s[i];
+      for (int i = scStart + lane; i < scStart + E.s.nsc * scWords; i += L)
+        d[i] = s[i];
+      if (lane == 0) {
+        gs->ngc = E.s.ngc;
+        gs->nsc = E.s.nsc;
+      }
+    }
+    __syncthreads();
+  }
+  if (valid)
+    copyEnv<State>(reinterpret_cast<unsigned *>(gs), reinterpret_cast<const unsigned *>(&E.s), lane,
+                   L, E.s.ngc, E.s.nsc);
+}
+
+} // namespace duckhip

@@ -1,0 +1,119 @@
+// Small-vector, quaternion and SO(3) math for the AVBD step, usable on the
+// host and on gfx950.  The arithmetic order of every expression follows the
+// reference core (src/cuda/kernel.cuh:86-228) so that float32 and float64
+// results track the reference's CPU build to rounding; in the float build the
+// reference evaluates a few expressions in double (its literals are double),
+// and the same expressions are evaluated in double here (marked [double]).
+// Vector division multiplies by the reciprocal, as kernel.cuh:100 does.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+
+#define DUCK_HD __host__ __device__ __forceinline__
+
+namespace duckhip {
+
+// Precision-explicit libm / OCML entry points.
+DUCK_HD float msqrt(float x) { return sqrtf(x); }
+DUCK_HD double msqrt(double x) { return sqrt(x); }
+DUCK_HD float msin(float x) { return sinf(x); }
+DUCK_HD double msin(double x) { return sin(x); }
+DUCK_HD float mcos(float x) { return cosf(x); }
+DUCK_HD double mcos(double x) { return cos(x); }
+DUCK_HD float matan2(float y, float x) { return atan2f(y, x); }
+DUCK_HD double matan2(double y, double x) { return atan2(y, x); }
+DUCK_HD float mhypot(float x, float y) { return hypotf(x, y); }
+DUCK_HD double mhypot(double x, double y) { return hypot(x, y); }
+DUCK_HD float mabs(float x) { return fabsf(x); }
+DUCK_HD double mabs(double x) { return fabs(x); }
+DUCK_HD bool mfinite(float x) { return isfinite(x); }
+DUCK_HD bool mfinite(double x) { return isfinite(x); }
+
+template <class R> struct V3 {
+  R x, y, z;
+};
+template <class R> struct Q4 {
+  R w, x, y, z;
+};
+
+template <class R> DUCK_HD V3<R> v3(R x, R y, R z) { return V3<R>{x, y, z}; }
+template <class R> DUCK_HD V3<R> operator+(V3<R> a, V3<R> b) { return {a.x + b.x, a.y + b.y, a.z + b.z}; }
+template <class R> DUCK_HD V3<R> operator-(V3<R> a, V3<R> b) { return {a.x - b.x, a.y - b.y, a.z - b.z}; }
+template <class R> DUCK_HD V3<R> operator-(V3<R> a) { return {-a.x, -a.y, -a.z}; }
+template <class R> DUCK_HD V3<R> operator*(V3<R> a, R s) { return {a.x * s, a.y * s, a.z * s}; }
+template <class R> DUCK_HD V3<R> operator*(R s, V3<R> a) { return {a.x * s, a.y * s, a.z * s}; }
+template <class R> DUCK_HD V3<R> divide(V3<R> a, R s) { return a * (R(1) / s); }
+template <class R> DUCK_HD R dot(V3<R> a, V3<R> b) { return a.x * b.x + a.y * b.y + a.z * b.z; }
+template <class R> DUCK_HD V3<R> cross(V3<R> a, V3<R> b) {
+  return {a.y * b.z - a.z * b.y, a.z * b.x - a.x * b.z, a.x * b.y - a.y * b.x};
+}
+template <class R> DUCK_HD R norm(V3<R> a) { return msqrt(dot(a, a)); }
+template <class R> DUCK_HD R comp(V3<R> a, int k) { return k == 0 ? a.x : (k == 1 ? a.y : a.z); }
+template <class R> DUCK_HD V3<R> unitOrNan(V3<R> a) {
+  R n = norm(a);
+  if (double(n) < 1e-15)
+    return {R(NAN), R(NAN), R(NAN)};
+  return divide(a, n);
+}
+
+template <class R> DUCK_HD Q4<R> conj(Q4<R> q) { return {q.w, -q.x, -q.y, -q.z}; }
+template <class R> DUCK_HD Q4<R> operator*(Q4<R> a, Q4<R> b) {
+  return {a.w * b.w - a.x * b.x - a.y * b.y - a.z * b.z,
+          a.w * b.x + a.x * b.w + a.y * b.z - a.z * b.y,
+          a.w * b.y - a.x * b.z + a.y * b.w + a.z * b.x,
+          a.w * b.z + a.x * b.y - a.y * b.x + a.z * b.w};
+}
+template <class R> DUCK_HD Q4<R> normalized(Q4<R> q) {
+  R n = msqrt(q.w * q.w + q.x * q.x + q.y * q.y + q.z * q.z);
+  if (double(n) < 1e-15)
+    return {R(NAN), R(NAN), R(NAN), R(NAN)};
+  return {q.w / n, q.x / n, q.y / n, q.z / n};
+}
+// v + 2 u x (u x v + w v)
+template <class R> DUCK_HD V3<R> rotate(Q4<R> q, V3<R> v) {
+  V3<R> u{q.x, q.y, q.z};
+  return v + R(2) * cross(u, cross(u, v) + q.w * v);
+}
+// Rotation by the conjugate, without forming it (bitwise equal to
+// rotate(conj(q), v): negating u flips both cross products).
+template <class R> DUCK_HD V3<R> rotateInv(Q4<R> q, V3<R> v) { return rotate(conj(q), v); }
+
+template <class R> DUCK_HD Q4<R> expmap(V3<R> v) {
+  R a = norm(v), s;
+  if (double(a) < 1e-8)
+    s = R(0.5 - double(a * a / R(48))); // [double]
+  else
+    s = msin(a / R(2)) / a;
+  return normalized(Q4<R>{mcos(a / R(2)), s * v.x, s * v.y, s * v.z});
+}
+template <class R> DUCK_HD V3<R> logmap(Q4<R> q) {
+  q = normalized(q);
+  if (q.w < 0)
+    q = {-q.w, -q.x, -q.y, -q.z};
+  V3<R> v{q.x, q.y, q.z};
+  R s = norm(v);
+  R k = double(s) < 1e-10 ? R(2) : R(2) * matan2(s, q.w) / s;
+  return v * k;
+}
+
+// IEEE remainder(a, 2*pi) in double: n = nearest integer of a/(2 pi), then the
+// exactly representable a - n 2pi by one fused operation.  [double]
+template <class R> DUCK_HD R wrapAngle(R a) {
+  const double twoPi = 6.283185307179586476925286766559; // 2*acos(-1.0)
+  double d = double(a);
+  double n = rint(d / twoPi);
+  return R(fma(-n, twoPi, d));
+}
+
+template <class R> DUCK_HD R mn(R a, R b) { return a < b ? a : b; }
+template <class R> DUCK_HD R mx(R a, R b) { return a > b ? a : b; }
+template <class R> DUCK_HD R clampv(R v, R a, R b) { return mn(mx(v, a), b); }
+
+template <class R> DUCK_HD R hingeAngle(Q4<R> qa, Q4<R> qb, V3<R> axisA, V3<R> tangentA,
+                                        V3<R> tangentB) {
+  V3<R> axis = rotate(qa, axisA), t = rotate(qa, tangentA), u = rotate(qb, tangentB);
+  return matan2(dot(axis, cross(t, u)), dot(t, u));
+}
+
+} // namespace duckhip

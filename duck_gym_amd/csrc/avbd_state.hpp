@@ -1,0 +1,130 @@
+// Data layout of the batched AVBD step on gfx950.
+//
+// HBM: one contiguous `EnvState` blob per environment (env-major), holding
+// exactly the state that survives between launches: body poses/velocities,
+// per-env mass and inertia, joint multipliers and penalties, the last
+// controls, the compacted ground and self contact lists (warm-start cache),
+// diagnostics and the failure flag.  A workgroup copies its environments'
+// blobs into LDS once per launch (live contacts only) and back at the end.
+//
+// LDS: `EnvLds` = `EnvState` + per-step scratch (x0/q0/xp/qp, joint c0 and
+// angle0, colour schedule, per-body contact masks), one per environment of
+// the workgroup, plus one `Frames` copy of the shared joint model.
+//
+// Fields are structure-of-arrays indexed [component][body|joint] so that the
+// lanes of one environment, which work on different bodies or joints, touch
+// consecutive LDS words.
+#pragma once
+#include "avbd_math.hpp"
+
+#include <cstdint>
+
+namespace duckhip {
+
+constexpr int kMaxModelBodies = 32, kMaxModelJoints = 32, kMaxModelShapes = 32,
+              kMaxModelPairs = 32;
+
+// Read-only model in global memory (one copy per batch).
+template <class R> struct DeviceModel {
+  int nb, nj, ns, np, ground, iterations, groundCapacity, selfCapacity;
+  R dt, tolerance, alpha, gamma, betaLinear, betaAngular;
+  R gravity[3];
+  // bodies in the file state
+  R mass[kMaxModelBodies], inertia[3][kMaxModelBodies], x[3][kMaxModelBodies],
+      q[4][kMaxModelBodies], v[3][kMaxModelBodies], w[3][kMaxModelBodies];
+  int colors[kMaxModelBodies];
+  // joints: frames (as in Frames) and file values of the per-env parameters
+  int ja[kMaxModelJoints], jb[kMaxModelJoints], limited[kMaxModelJoints];
+  R ra[3][kMaxModelJoints], rb[3][kMaxModelJoints], axisA[3][kMaxModelJoints],
+      axisB[3][kMaxModelJoints], tangentA[3][kMaxModelJoints], tangentB[3][kMaxModelJoints];
+  R lo[kMaxModelJoints], hi[kMaxModelJoints], armature[kMaxModelJoints];
+  int adjStart[kMaxModelBodies + 1], adj[2 * kMaxModelJoints];
+  R damping[kMaxModelJoints], frictionloss[kMaxModelJoints], torque[kMaxModelJoints],
+      kp[kMaxModelJoints], target[kMaxModelJoints], maxTorque[kMaxModelJoints],
+      originalAngle[kMaxModelJoints];
+  // shapes
+  int sbody[kMaxModelShapes], stype[kMaxModelShapes], sground[kMaxModelShapes],
+      soffset[kMaxModelShapes], scount[kMaxModelShapes];
+  R center[3][kMaxModelShapes], size[3][kMaxModelShapes], sq[4][kMaxModelShapes],
+      sfriction[kMaxModelShapes], radius[kMaxModelShapes], interior[3][kMaxModelShapes];
+  // body-contact pairs (shape indices)
+  int pa[kMaxModelPairs], pb[kMaxModelPairs];
+  R pfriction[kMaxModelPairs];
+};
+
+// Joint model used inside the solve, staged in LDS once per workgroup.
+template <class R, int B, int J> struct Frames {
+  int a[J], b[J], limited[J];
+  R ra[3][J], rb[3][J], axisA[3][J], axisB[3][J], tangentA[3][J], tangentB[3][J];
+  R lo[J], hi[J], armature[J];
+  int adjStart[B + 1], adj[2 * J];
+  R shapeFriction[kMaxModelShapes];
+};
+
+// Ground contact (normal = +z, anchor on the plane).  id packs
+// shape (bits 0-5), body (6-11), feature (12-30) and stick (31).
+template <class R> struct GroundContact {
+  int id;
+  R local[3], anchor[2], c0, lambda[3], penalty[3];
+};
+// Body-body contact.  id packs body (0-5), other (6-11), shape (12-17),
+// otherShape (18-23), stick (31).
+template <class R> struct SelfContact {
+  int id;
+  R local[3], localB[3], t1[3], t2[3], n[3], c0, friction, lambda[3], penalty[3];
+};
+
+DUCK_HD int gcShape(int id) { return id & 63; }
+DUCK_HD int gcBody(int id) { return (id >> 6) & 63; }
+DUCK_HD int gcFeature(int id) { return (id >> 12) & 0x7ffff; }
+DUCK_HD bool gcStick(int id) { return id < 0; }
+DUCK_HD int gcPack(int shape, int body, int feature, bool stick) {
+  return shape | (body << 6) | (feature << 12) | (stick ? int(0x80000000u) : 0);
+}
+DUCK_HD int scBody(int id) { return id & 63; }
+DUCK_HD int scOther(int id) { return (id >> 6) & 63; }
+DUCK_HD int scShape(int id) { return (id >> 12) & 63; }
+DUCK_HD int scOtherShape(int id) { return (id >> 18) & 63; }
+DUCK_HD bool scStick(int id) { return id < 0; }
+DUCK_HD int scPack(int body, int other, int shape, int otherShape, bool stick) {
+  return body | (other << 6) | (shape << 12) | (otherShape << 18) |
+         (stick ? int(0x80000000u) : 0);
+}
+
+enum DiagSlot { kJointError, kPenetration, kContacts, kConverged, kAxisError, kIterations };
+
+// Persistent per-env state; the HBM blob is exactly this struct.
+template <class R, int B, int J, int CG, int CS> struct EnvState {
+  R x[3][B], q[4][B], v[3][B], w[3][B];
+  R mass[B], inertia[3][B];
+  R force[3];
+  R lambda[7][J], penalty[7][J];
+  R lambdaF[J], penaltyF[J];
+  R target[J], kp[J], maxTorque[J], torque[J], frictionloss[J], damping[J];
+  R diag[8];
+  R friction; // per-env ground friction; < 0 selects the shape friction
+  int failed, ngc, nsc, colorCount;
+  int colors[B]; // colouring of the last step (model colours + fresh ones)
+  GroundContact<R> gc[CG];
+  SelfContact<R> sc[CS];
+};
+
+template <class R, int B, int J, int CG, int CS> struct EnvLds {
+  EnvState<R, B, J, CG, CS> s;
+  // per-step scratch
+  R x0[3][B], q0[4][B], xp[3][B], qp[4][B];
+  R c0[7][J], angle0[J], velocity0[J];
+  R stepDiag[8];
+  uint64_t gmask[B];
+  uint32_t smask[B];
+  int order[B], colorStart[CS + 3];
+  int done, pad0, pad1, pad2;
+  int shapeCount[kMaxModelShapes];
+  int pairHit[kMaxModelPairs];
+};
+
+// Word offset of the contact lists inside the blob (everything before them is
+// copied unconditionally; only the live contacts after them are copied).
+template <class S> constexpr size_t headerBytes() { return offsetof(S, gc); }
+
+} // namespace duckhip

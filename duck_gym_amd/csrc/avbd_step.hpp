@@ -1,0 +1,415 @@
+// The AVBD environment step on gfx950: one wave64 workgroup advances
+// G = 64 / L environments, L lanes per environment.
+//
+// Per physics step of one environment (reference: src/cuda/kernel.cuh:937-1095):
+//   detection   lanes over shapes (ground manifolds) and pairs (MPR), then a
+//               prefix over shapes compacts the contact list in reference order
+//   warm start  lanes over joints; predictor lanes over bodies
+//   iterations  per colour: lanes over that colour's bodies, each running one
+//               6x6 block-descent solve (assembly + LDL^T/Cholesky in registers);
+//               then lanes over joints and contacts for the dual/penalty update
+//   epilogue    lanes over bodies (velocity recovery), joints and contacts
+//               (diagnostics)
+// Every __syncthreads() below is reached by all 64 lanes: per-environment
+// differences (colour counts, convergence, failure) are masked, never branched
+// around a barrier.
+#pragma once
+#include "avbd_state.hpp"
+
+namespace duckhip {
+
+struct StepArgs {
+  const void *model;   // DeviceModel<R>
+  const void *points;  // shape points, R[3] each
+  unsigned char *states; // EnvState blobs
+  long long blobBytes;
+  int count;
+  const void *targets; // [E,J] or null (step)
+  const void *forces;  // [E,3]
+  const void *motor;   // [E,J,3] (motor mode)
+  int substeps;
+  int motorMode;
+  double kp, limit;
+};
+
+DUCK_HD constexpr int tri(int i, int j) { return i * (i + 1) / 2 + j; }
+
+template <class R> struct Hess {
+  R h[21]; // lower triangle of the 6x6 Hessian
+  R g[6];
+};
+
+// Row (t, r) with t = s e_k: g += J f, H += (k J) J^T on the lower triangle.
+// Entries multiplied by an exact zero of J are skipped (they add +-0).
+template <class R> DUCK_HD void stampLinear(Hess<R> &H, int k, R s, V3<R> r, R f, R kk) {
+  H.g[k] += s * f;
+  H.g[3] += r.x * f;
+  H.g[4] += r.y * f;
+  H.g[5] += r.z * f;
+  H.h[tri(k, k)] += kk * s * s;
+  R r0 = kk * r.x, r1 = kk * r.y, r2 = kk * r.z;
+  H.h[tri(3, k)] += r0 * s;
+  H.h[tri(4, k)] += r1 * s;
+  H.h[tri(5, k)] += r2 * s;
+  H.h[tri(3, 3)] += r0 * r.x;
+  H.h[tri(4, 3)] += r1 * r.x;
+  H.h[tri(4, 4)] += r1 * r.y;
+  H.h[tri(5, 3)] += r2 * r.x;
+  H.h[tri(5, 4)] += r2 * r.y;
+  H.h[tri(5, 5)] += r2 * r.z;
+}
+// Row (0, r).
+template <class R> DUCK_HD void stampAngular(Hess<R> &H, V3<R> r, R f, R kk) {
+  H.g[3] += r.x * f;
+  H.g[4] += r.y * f;
+  H.g[5] += r.z * f;
+  R r0 = kk * r.x, r1 = kk * r.y, r2 = kk * r.z;
+  H.h[tri(3, 3)] += r0 * r.x;
+  H.h[tri(4, 3)] += r1 * r.x;
+  H.h[tri(4, 4)] += r1 * r.y;
+  H.h[tri(5, 3)] += r2 * r.x;
+  H.h[tri(5, 4)] += r2 * r.y;
+  H.h[tri(5, 5)] += r2 * r.z;
+}
+// General row (t, r).
+template <class R> DUCK_HD void stampFull(Hess<R> &H, V3<R> t, V3<R> r, R f, R kk) {
+  R J[6] = {t.x, t.y, t.z, r.x, r.y, r.z};
+#pragma unroll
+  for (int i = 0; i < 6; ++i) {
+    H.g[i] += J[i] * f;
+    R ki = kk * J[i];
+#pragma unroll
+    for (int j = 0; j <= i; ++j)
+      H.h[tri(i, j)] += ki * J[j];
+  }
+}
+// Diagonal majorisation of the rotational geometric stiffness
+// (kernel.cuh:283-301).  For float, 0.5*x - y in float equals the reference's
+// double evaluation rounded to float (no double rounding can occur).
+template <class R> DUCK_HD void geometricAdd(Hess<R> &H, V3<R> r, V3<R> f) {
+  R rf = dot(r, f);
+  R rv[3] = {r.x, r.y, r.z}, fv[3] = {f.x, f.y, f.z};
+#pragma unroll
+  for (int col = 0; col < 3; ++col) {
+    R sum = 0;
+#pragma unroll
+    for (int row = 0; row < 3; ++row) {
+      R a = R(0.5) * (rv[row] * fv[col] + fv[row] * rv[col]) - (row == col ? rf : R(0));
+      sum += a * a;
+    }
+    H.h[tri(3 + col, 3 + col)] += msqrt(sum);
+  }
+}
+
+// Cholesky solve of H x = -g with NaN on a bad pivot (kernel.cuh:177-228).
+template <class R> DUCK_HD void solve6(const Hess<R> &H, R x[6]) {
+  R L[21];
+#pragma unroll
+  for (int i = 0; i < 6; ++i) {
+#pragma unroll
+    for (int j = 0; j <= i; ++j) {
+      R v = H.h[tri(i, j)];
+#pragma unroll
+      for (int k = 0; k < j; ++k)
+        v -= L[tri(i, k)] * L[tri(j, k)];
+      if (i == j) {
+        if (!(v > 0) || !mfinite(v)) {
+#pragma unroll
+          for (int k = 0; k < 6; ++k)
+            x[k] = R(NAN);
+          return;
+        }
+        L[tri(i, i)] = msqrt(v);
+      } else {
+        L[tri(i, j)] = v / L[tri(j, j)];
+      }
+    }
+  }
+  R y[6];
+#pragma unroll
+  for (int i = 0; i < 6; ++i) {
+    y[i] = -H.g[i];
+#pragma unroll
+    for (int k = 0; k < i; ++k)
+      y[i] -= L[tri(i, k)] * y[k];
+    y[i] /= L[tri(i, i)];
+  }
+#pragma unroll
+  for (int i = 5; i >= 0; --i) {
+    x[i] = y[i];
+#pragma unroll
+    for (int k = i + 1; k < 6; ++k)
+      x[i] -= L[tri(k, i)] * x[k];
+    x[i] /= L[tri(i, i)];
+  }
+}
+
+// (1 - (a/2)/tan(a/2)) / a^2, the SO(3) log-Jacobian coefficient, evaluated
+// in double as the reference's float build does (kernel.cuh:841-850). [double]
+template <class R> DUCK_HD R logJacobianCoef(R a) {
+  double ad = double(a);
+  if (ad < 1e-5)
+    return R(1.0 / 12 + double(a * a / R(720)));
+  return R((1 - 0.5 * ad / tan(0.5 * ad)) / double(a * a));
+}
+
+template <class R> DUCK_HD V3<R> unitAxis(int k) {
+  return V3<R>{k == 0 ? R(1) : R(0), k == 1 ? R(1) : R(0), k == 2 ? R(1) : R(0)};
+}
+// r x e_k with the exact zero the general cross product produces.
+template <class R> DUCK_HD V3<R> crossUnit(V3<R> r, int k) { return cross(r, unitAxis<R>(k)); }
+
+// Coulomb-projected contact force (kernel.cuh:304-315).
+template <class R> DUCK_HD V3<R> contactForce(V3<R> C, const R lambda[3], const R penalty[3],
+                                              R friction) {
+  V3<R> f{lambda[0] + penalty[0] * C.x, lambda[1] + penalty[1] * C.y,
+          lambda[2] + penalty[2] * C.z};
+  f.z = mn(f.z, R(0));
+  R t = mhypot(f.x, f.y), bound = -friction * f.z;
+  if (t > bound && t > 0) {
+    f.x *= bound / t;
+    f.y *= bound / t;
+  }
+  return f;
+}
+
+template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
+  using Env = EnvLds<R, B, J, CG, CS>;
+  using Fr = Frames<R, B, J>;
+  const DeviceModel<R> &M;
+  const V3<R> *points;
+  const Fr &F;
+  Env &E;
+  int lane; // 0..L-1 within the environment
+
+  // ------------------------------------------------------------ access --
+  DUCK_HD V3<R> X(int b) const { return {E.s.x[0][b], E.s.x[1][b], E.s.x[2][b]}; }
+  DUCK_HD Q4<R> Q(int b) const { return {E.s.q[0][b], E.s.q[1][b], E.s.q[2][b], E.s.q[3][b]}; }
+  DUCK_HD V3<R> Vel(int b) const { return {E.s.v[0][b], E.s.v[1][b], E.s.v[2][b]}; }
+  DUCK_HD V3<R> Omega(int b) const { return {E.s.w[0][b], E.s.w[1][b], E.s.w[2][b]}; }
+  DUCK_HD V3<R> Inertia(int b) const {
+    return {E.s.inertia[0][b], E.s.inertia[1][b], E.s.inertia[2][b]};
+  }
+  DUCK_HD Q4<R> Q0(int b) const { return {E.q0[0][b], E.q0[1][b], E.q0[2][b], E.q0[3][b]}; }
+  DUCK_HD void setX(int b, V3<R> v) {
+    E.s.x[0][b] = v.x;
+    E.s.x[1][b] = v.y;
+    E.s.x[2][b] = v.z;
+  }
+  DUCK_HD void setQ(int b, Q4<R> q) {
+    E.s.q[0][b] = q.w;
+    E.s.q[1][b] = q.x;
+    E.s.q[2][b] = q.y;
+    E.s.q[3][b] = q.z;
+  }
+  DUCK_HD V3<R> frame(const R (&a)[3][J], int j) const { return {a[0][j], a[1][j], a[2][j]}; }
+  DUCK_HD R forceZ(int b) const { return b == 1 ? E.s.force[2] : R(0); }
+  DUCK_HD V3<R> force(int b) const {
+    return b == 1 ? V3<R>{E.s.force[0], E.s.force[1], E.s.force[2]} : V3<R>{0, 0, 0};
+  }
+  // Inertia frozen at q0 (kernel.cuh:275-280).
+  DUCK_HD V3<R> inertiaApply(Q4<R> q0, V3<R> I, V3<R> w, bool inverse) const {
+    V3<R> l = rotate(conj(q0), w);
+    if (inverse) {
+      l.x *= R(1) / I.x;
+      l.y *= R(1) / I.y;
+      l.z *= R(1) / I.z;
+    } else {
+      l.x *= I.x;
+      l.y *= I.y;
+      l.z *= I.z;
+    }
+    return rotate(q0, l);
+  }
+  DUCK_HD R groundFriction(int shape) const {
+    return E.s.friction >= 0 ? E.s.friction : F.shapeFriction[shape];
+  }
+
+  // Hinge constraint values (kernel.cuh:732-761): anchor (3), axis (2),
+  // limits (2); also returns the world frames used by the Jacobians.
+  struct JointEval {
+    R C[7], angle;
+    V3<R> ra, rb, axis, axisB, t1, t2;
+  };
+  DUCK_HD JointEval evalJoint(int ji) const {
+    JointEval o;
+    int a = F.a[ji], b = F.b[ji];
+    Q4<R> qa = Q(a), qb = Q(b);
+    o.ra = rotate(qa, frame(F.ra, ji));
+    o.rb = rotate(qb, frame(F.rb, ji));
+    V3<R> d = ((X(a) + o.ra) - X(b)) - o.rb;
+    o.axis = rotate(qa, frame(F.axisA, ji));
+    o.axisB = rotate(qb, frame(F.axisB, ji));
+    o.t1 = rotate(qa, frame(F.tangentA, ji));
+    o.t2 = cross(o.axis, o.t1);
+    V3<R> u = rotate(qb, frame(F.tangentB, ji));
+    o.angle = matan2(dot(o.axis, cross(o.t1, u)), dot(o.t1, u));
+    o.C[0] = d.x;
+    o.C[1] = d.y;
+    o.C[2] = d.z;
+    o.C[3] = dot(o.t1, o.axisB);
+    o.C[4] = dot(o.t2, o.axisB);
+    o.C[5] = o.angle - F.lo[ji];
+    o.C[6] = F.hi[ji] - o.angle;
+    return o;
+  }
+
+  // Ground contact values in the fixed world basis (kernel.cuh:805-827).
+  DUCK_HD V3<R> groundC(const GroundContact<R> &c, V3<R> &ra) const {
+    int b = gcBody(c.id);
+    ra = rotate(Q(b), V3<R>{c.local[0], c.local[1], c.local[2]});
+    V3<R> delta = (X(b) + ra) - V3<R>{c.anchor[0], c.anchor[1], R(0)};
+    delta.z -= M.alpha * c.c0;
+    return delta;
+  }
+  DUCK_HD V3<R> selfC(const SelfContact<R> &c, V3<R> &ra, V3<R> &rb) const {
+    int a = scBody(c.id), b = scOther(c.id);
+    ra = rotate(Q(a), V3<R>{c.local[0], c.local[1], c.local[2]});
+    rb = rotate(Q(b), V3<R>{c.localB[0], c.localB[1], c.localB[2]});
+    V3<R> delta = ((X(a) + ra) - X(b)) - rb;
+    V3<R> t1{c.t1[0], c.t1[1], c.t1[2]}, t2{c.t2[0], c.t2[1], c.t2[2]}, n{c.n[0], c.n[1], c.n[2]};
+    V3<R> C{dot(delta, t1), dot(delta, t2), dot(delta, n)};
+    C.z -= M.alpha * c.c0;
+    return C;
+  }
+
+  // --------------------------------------------------- 6x6 block solve --
+  // kernel.cuh:828-936 for one dynamic body.
+  DUCK_HD R updateBody(int bi, bool implicitDrive) {
+    const R h = M.dt;
+    V3<R> x = X(bi), xp{E.xp[0][bi], E.xp[1][bi], E.xp[2][bi]};
+    Q4<R> q = Q(bi), qp{E.qp[0][bi], E.qp[1][bi], E.qp[2][bi], E.qp[3][bi]}, q0 = Q0(bi);
+    V3<R> I = Inertia(bi);
+    Hess<R> H;
+#pragma unroll
+    for (int k = 0; k < 21; ++k)
+      H.h[k] = 0;
+    V3<R> dx = x - xp, theta = logmap(q * conj(qp));
+    R mh = E.s.mass[bi] / (h * h);
+    H.h[tri(0, 0)] = mh;
+    H.h[tri(1, 1)] = mh;
+    H.h[tri(2, 2)] = mh;
+    H.g[0] = mh * dx.x;
+    H.g[1] = mh * dx.y;
+    H.g[2] = mh * dx.z;
+    R coef = logJacobianCoef(norm(theta));
+    V3<R> rotJ[3];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      V3<R> e = unitAxis<R>(k);
+      rotJ[k] = (e - R(0.5) * cross(theta, e)) + coef * cross(theta, cross(theta, e));
+    }
+    V3<R> It = inertiaApply(q0, I, theta, false);
+    V3<R> IJ[3] = {inertiaApply(q0, I, rotJ[0], false), inertiaApply(q0, I, rotJ[1], false),
+                   inertiaApply(q0, I, rotJ[2], false)};
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      H.g[3 + k] = dot(rotJ[k], It) / (h * h);
+#pragma unroll
+      for (int l = 0; l <= k; ++l)
+        H.h[tri(3 + k, 3 + l)] = dot(rotJ[k], IJ[l]) / (h * h);
+    }
+    const R alpha = M.alpha;
+    for (int adj = F.adjStart[bi]; adj < F.adjStart[bi + 1]; ++adj) {
+      const int ji = F.adj[adj];
+      const bool parent = bi == F.a[ji];
+      const R s = parent ? R(1) : R(-1);
+      JointEval je = evalJoint(ji);
+      const int rows = F.limited[ji] ? 7 : 5;
+#pragma unroll
+      for (int k = 0; k < 7; ++k) {
+        if (k >= rows)
+          break;
+        R c0 = E.c0[k][ji];
+        R c = je.C[k] - alpha * (k < 5 ? c0 : mn(c0, R(0)));
+        R pen = E.s.penalty[k][ji];
+        R f = E.s.lambda[k][ji] + pen * c;
+        if (k >= 5)
+          f = mn(f, R(0));
+        if (k < 5 || f < 0) {
+          if (k < 3) {
+            V3<R> rrow = parent ? crossUnit(je.ra, k) : -crossUnit(je.rb, k);
+            stampLinear(H, k, s, rrow, f, pen);
+            V3<R> e{k == 0 ? f : R(0), k == 1 ? f : R(0), k == 2 ? f : R(0)};
+            geometricAdd(H, parent ? je.ra : -je.rb, e);
+          } else if (k < 5) {
+            V3<R> t = k == 3 ? je.t1 : je.t2;
+            stampAngular(H, parent ? cross(t, je.axisB) : cross(je.axisB, t), f, pen);
+            geometricAdd(H, parent ? t : je.axisB, (parent ? je.axisB : t) * f);
+          } else {
+            stampAngular(H, (k == 5) == parent ? -je.axis : je.axis, f, pen);
+          }
+        }
+      }
+      const V3<R> J5 = parent ? -je.axis : je.axis;
+      if (implicitDrive) {
+        // Implicit torque-limited PD potential (kernel.cuh:893-902).
+        R kp = E.s.kp[ji], maxT = E.s.maxTorque[ji];
+        R drive = kp * wrapAngle(je.angle - E.s.target[ji]) - E.s.torque[ji];
+        R ks = kp;
+        if (maxT > 0) {
+          if (mabs(drive) >= maxT)
+            ks = 0;
+          drive = clampv(drive, -maxT, maxT);
+        }
+        stampAngular(H, J5, drive, ks);
+      }
+      R damping = E.s.damping[ji], armature = F.armature[ji];
+      R delta = wrapAngle(je.angle - E.angle0[ji]);
+      R stiff = damping / h + armature / (h * h);
+      R force = damping / h * delta + armature / (h * h) * (delta - h * E.velocity0[ji]);
+      if (stiff > 0)
+        stampAngular(H, J5, force, stiff);
+      R fl = E.s.frictionloss[ji];
+      if (fl > 0) {
+        R trial = E.s.lambdaF[ji] + E.s.penaltyF[ji] * delta;
+        stampAngular(H, J5, clampv(trial, -fl, fl), mabs(trial) < fl ? E.s.penaltyF[ji] : R(0));
+      }
+    }
+    // Ground contacts of this body, in list order.
+    for (uint64_t m = E.gmask[bi]; m; m &= m - 1) {
+      const GroundContact<R> &c = E.s.gc[__builtin_ctzll(m)];
+      V3<R> ra;
+      V3<R> C = groundC(c, ra);
+      V3<R> f = contactForce(C, c.lambda, c.penalty, groundFriction(gcShape(c.id)));
+      if (f.z < 0) {
+        stampLinear(H, 0, R(1), crossUnit(ra, 0), f.x, c.penalty[0]);
+        stampLinear(H, 1, R(1), crossUnit(ra, 1), f.y, c.penalty[1]);
+        stampLinear(H, 2, R(1), crossUnit(ra, 2), f.z, c.penalty[2]);
+        geometricAdd(H, ra, f);
+      }
+    }
+    // Body-body contacts touching this body, in list order.
+    for (uint32_t m = E.smask[bi]; m; m &= m - 1) {
+      const SelfContact<R> &c = E.s.sc[__builtin_ctz(m)];
+      V3<R> ra, rb;
+      V3<R> C = selfC(c, ra, rb);
+      bool first = bi == scBody(c.id);
+      V3<R> r = first ? ra : rb;
+      R sign = first ? R(1) : R(-1);
+      V3<R> f = contactForce(C, c.lambda, c.penalty, c.friction);
+      if (f.z < 0) {
+        V3<R> basis[3] = {{c.t1[0], c.t1[1], c.t1[2]},
+                          {c.t2[0], c.t2[1], c.t2[2]},
+                          {c.n[0], c.n[1], c.n[2]}};
+        R fk[3] = {f.x, f.y, f.z};
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+          V3<R> e = basis[k] * sign;
+          stampFull(H, e, cross(r, e), fk[k], c.penalty[k]);
+        }
+        V3<R> fw = ((basis[0] * f.x) + (basis[1] * f.y)) + (basis[2] * f.z);
+        geometricAdd(H, r, fw * sign);
+      }
+    }
+    R st[6];
+    solve6(H, st);
+    V3<R> tx{st[0], st[1], st[2]}, rx{st[3], st[4], st[5]};
+    R scale = mn(R(1), mn(R(.1) / mx(norm(tx), R(1e-30)), R(.25) / mx(norm(rx), R(1e-30))));
+    setX(bi, x + scale * tx);
+    setQ(bi, normalized(expmap(scale * rx) * q));
+    return mx(norm(tx), norm(rx)) * scale;
+  }
+};
+
+} // namespace duckhip

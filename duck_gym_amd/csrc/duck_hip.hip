@@ -1,0 +1,548 @@
+// C ABI of the gfx950 AVBD batch (include/duck_hip.h): model upload, state
+// ownership, stream ordering and kernel dispatch.
+#include "../../include/duck_hip.h"
+#include "avbd_queries.hpp"
+#include "duck_model.hpp"
+
+#include <cstring>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+namespace duckhip {
+namespace {
+
+thread_local std::string g_lastError;
+
+struct DuckError : std::runtime_error {
+  int code;
+  DuckError(int c, const std::string &m) : std::runtime_error(m), code(c) {}
+};
+
+void hipCheck(hipError_t err, const char *what) {
+  if (err != hipSuccess)
+    throw DuckError(DUCK_ERR_DEVICE, std::string(what) + ": " + hipGetErrorString(err));
+}
+void require(bool ok, const std::string &message) {
+  if (!ok)
+    throw DuckError(DUCK_ERR_ARGUMENT, message);
+}
+
+// Makes `device` current for the lifetime of the guard.
+struct DeviceGuard {
+  int previous = -1;
+  explicit DeviceGuard(int device) {
+    hipCheck(hipGetDevice(&previous), "hipGetDevice");
+    if (previous != device)
+      hipCheck(hipSetDevice(device), "hipSetDevice");
+  }
+  ~DeviceGuard() {
+    int now = -1;
+    if (hipGetDevice(&now) == hipSuccess && now != previous && previous >= 0)
+      (void)hipSetDevice(previous);
+  }
+};
+
+template <class R> DeviceModel<R> pack(const HostModel &h, double dt, int iterations) {
+  DeviceModel<R> m;
+  std::memset(&m, 0, sizeof(m));
+  m.nb = h.bodies.size();
+  m.nj = h.joints.size();
+  m.ns = h.shapes.size();
+  m.np = h.pairs.size();
+  m.ground = h.ground;
+  m.iterations = iterations;
+  m.groundCapacity = h.groundCapacity;
+  m.selfCapacity = h.selfCapacity;
+  m.dt = R(dt);
+  // model.hpp:141-142: fp32 stops at 1e-6, fp64 at 1e-7.
+  m.tolerance = sizeof(R) == sizeof(float) ? R(1e-6) : R(1e-7);
+  m.alpha = R(0.9);
+  m.gamma = R(0.99);
+  m.betaLinear = R(1e7);
+  m.betaAngular = R(1e5);
+  for (int k = 0; k < 3; ++k)
+    m.gravity[k] = R(h.gravity[k]);
+  for (int b = 0; b < m.nb; ++b) {
+    const auto &s = h.bodies[b];
+    m.mass[b] = R(s.mass);
+    for (int k = 0; k < 3; ++k) {
+      m.inertia[k][b] = R(s.inertia[k]);
+      m.x[k][b] = R(s.x[k]);
+      m.v[k][b] = R(s.v[k]);
+      m.w[k][b] = R(s.w[k]);
+    }
+    for (int k = 0; k < 4; ++k)
+      m.q[k][b] = R(s.q[k]);
+    m.colors[b] = h.colors[b];
+  }
+  for (int j = 0; j < m.nj; ++j) {
+    const auto &s = h.joints[j];
+    m.ja[j] = s.a;
+    m.jb[j] = s.b;
+    m.limited[j] = s.limited;
+    for (int k = 0; k < 3; ++k) {
+      m.ra[k][j] = R(s.ra[k]);
+      m.rb[k][j] = R(s.rb[k]);
+      m.axisA[k][j] = R(s.axisA[k]);
+      m.axisB[k][j] = R(s.axisB[k]);
+      m.tangentA[k][j] = R(s.tangentA[k]);
+      m.tangentB[k][j] = R(s.tangentB[k]);
+    }
+    m.lo[j] = R(s.lo);
+    m.hi[j] = R(s.hi);
+    m.armature[j] = R(s.armature);
+    m.damping[j] = R(s.damping);
+    m.frictionloss[j] = R(s.frictionloss);
+    m.torque[j] = R(s.torque);
+    m.kp[j] = R(s.kp);
+    m.target[j] = R(s.target);
+    m.maxTorque[j] = R(s.maxTorque);
+  }
+  // Hinge angle of the file state in the batch precision, as resetPose
+  // evaluates it (kernel.cuh:407-412).
+  for (int j = 0; j < m.nj; ++j) {
+    int a = m.ja[j], b = m.jb[j];
+    Q4<R> qa{m.q[0][a], m.q[1][a], m.q[2][a], m.q[3][a]};
+    Q4<R> qb{m.q[0][b], m.q[1][b], m.q[2][b], m.q[3][b]};
+    m.originalAngle[j] = hingeAngle(qa, qb, V3<R>{m.axisA[0][j], m.axisA[1][j], m.axisA[2][j]},
+                                    V3<R>{m.tangentA[0][j], m.tangentA[1][j], m.tangentA[2][j]},
+                                    V3<R>{m.tangentB[0][j], m.tangentB[1][j], m.tangentB[2][j]});
+  }
+  for (size_t i = 0; i < h.adjacencyStart.size(); ++i)
+    m.adjStart[i] = h.adjacencyStart[i];
+  for (size_t i = 0; i < h.adjacency.size(); ++i)
+    m.adj[i] = h.adjacency[i];
+  for (int s = 0; s < m.ns; ++s) {
+    const auto &sh = h.shapes[s];
+    m.sbody[s] = sh.body;
+    m.stype[s] = sh.type;
+    m.sground[s] = sh.ground;
+    m.soffset[s] = sh.offset;
+    m.scount[s] = sh.count;
+    for (int k = 0; k < 3; ++k) {
+      m.center[k][s] = R(sh.center[k]);
+      m.size[k][s] = R(sh.size[k]);
+      m.interior[k][s] = R(sh.interior[k]);
+    }
+    for (int k = 0; k < 4; ++k)
+      m.sq[k][s] = R(sh.q[k]);
+    m.sfriction[s] = R(sh.friction);
+    m.radius[s] = R(sh.radius);
+  }
+  for (int p = 0; p < m.np; ++p) {
+    m.pa[p] = h.pairs[p].a;
+    m.pb[p] = h.pairs[p].b;
+    m.pfriction[p] = R(h.pairs[p].friction);
+  }
+  return m;
+}
+
+struct BatchBase {
+  virtual ~BatchBase() = default;
+  HostModel host;
+  std::vector<std::string> names;
+  int count = 0, device = 0, fpBits = 32, contactCapacity = 0;
+  long long blobBytes = 0;
+  virtual void reset(const unsigned char *, const void *, const void *, const void *,
+                     hipStream_t) = 0;
+  virtual void step(const void *, const void *, int, double, double, hipStream_t) = 0;
+  virtual void stepMotor(const void *, const void *, hipStream_t) = 0;
+  virtual void state(void *, void *, void *, hipStream_t) = 0;
+  virtual void contactForces(int, void *, hipStream_t) = 0;
+  virtual void selfContactStats(void *, hipStream_t) = 0;
+  virtual void contactCounts(void *, hipStream_t) = 0;
+  virtual void generalizedLoads(const void *, void *, hipStream_t) = 0;
+  virtual void reference(const void *, const void *, int, double, double, void *, void *,
+                         void *) = 0;
+  virtual void layout(long long *out) const = 0;
+  virtual void exportState(void *, hipStream_t) = 0;
+  virtual void importState(const void *, hipStream_t) = 0;
+};
+
+template <class R, int B, int J, int CG, int CS, int L> class Batch final : public BatchBase {
+  using State = EnvState<R, B, J, CG, CS>;
+  static constexpr int G = 64 / L;
+  DeviceModel<R> *dModel = nullptr;
+  V3<R> *dPoints = nullptr;
+  unsigned char *dStates = nullptr;
+  hipEvent_t ready = nullptr;
+
+  void wait(hipStream_t s) { hipCheck(hipStreamWaitEvent(s, ready, 0), "hipStreamWaitEvent"); }
+  void record(hipStream_t s) { hipCheck(hipEventRecord(ready, s), "hipEventRecord"); }
+  void launched(const char *what) { hipCheck(hipGetLastError(), what); }
+  static int blocks64(int n) { return (n + 63) / 64; }
+
+  void advance(unsigned char *states, int n, const void *targets, const void *forces,
+               const void *motor, int substeps, double kp, double limit, hipStream_t s) {
+    StepArgs args{dModel, dPoints, states, blobBytes, n, targets, forces, motor,
+                  substeps, motor != nullptr, kp, limit};
+    advanceKernel<R, B, J, CG, CS, L><<<(n + G - 1) / G, 64, 0, s>>>(args);
+    launched("advanceKernel");
+  }
+
+public:
+  Batch(HostModel &&model, int n, double dt, int iterations, int gpu) {
+    host = std::move(model);
+    count = n;
+    device = gpu;
+    fpBits = sizeof(R) * 8;
+    contactCapacity = host.groundCapacity + host.selfCapacity;
+    blobBytes = (sizeof(State) + 255) / 256 * 256;
+    for (auto &j : host.joints)
+      names.push_back(j.name);
+    DeviceGuard guard(device);
+    DeviceModel<R> packed = pack<R>(host, dt, iterations);
+    std::vector<V3<R>> pts(std::max<size_t>(1, host.points.size() / 3));
+    for (size_t i = 0; i < host.points.size() / 3; ++i)
+      pts[i] = V3<R>{R(host.points[3 * i]), R(host.points[3 * i + 1]), R(host.points[3 * i + 2])};
+    try {
+      hipCheck(hipMalloc(&dModel, sizeof(DeviceModel<R>)), "hipMalloc(model)");
+      hipCheck(hipMalloc(&dPoints, pts.size() * sizeof(V3<R>)), "hipMalloc(points)");
+      hipCheck(hipMalloc(&dStates, size_t(blobBytes) * count), "hipMalloc(state)");
+      hipCheck(hipMemcpy(dModel, &packed, sizeof(packed), hipMemcpyHostToDevice), "upload model");
+      hipCheck(hipMemcpy(dPoints, pts.data(), pts.size() * sizeof(V3<R>), hipMemcpyHostToDevice),
+               "upload points");
+      hipCheck(hipMemset(dStates, 0, size_t(blobBytes) * count), "hipMemset(state)");
+      initializeKernel<R, B, J, CG, CS><<<blocks64(count), 64, 0, 0>>>(dModel, dStates, blobBytes,
+                                                                        count);
+      launched("initializeKernel");
+      hipCheck(hipDeviceSynchronize(), "initialize");
+      hipCheck(hipEventCreateWithFlags(&ready, hipEventDisableTiming), "hipEventCreate");
+      record(0);
+    } catch (...) {
+      release();
+      throw;
+    }
+  }
+  void release() {
+    if (ready) {
+      (void)hipEventSynchronize(ready);
+      (void)hipEventDestroy(ready);
+      ready = nullptr;
+    }
+    if (dStates)
+      (void)hipFree(dStates);
+    if (dPoints)
+      (void)hipFree(dPoints);
+    if (dModel)
+      (void)hipFree(dModel);
+    dStates = nullptr;
+    dPoints = nullptr;
+    dModel = nullptr;
+  }
+  ~Batch() override {
+    try {
+      DeviceGuard guard(device);
+      release();
+    } catch (...) {
+    }
+  }
+
+  void reset(const unsigned char *mask, const void *q, const void *root, const void *ext,
+             hipStream_t s) override {
+    DeviceGuard guard(device);
+    require(mask && q && root, "reset: null buffer");
+    wait(s);
+    resetKernel<R, B, J, CG, CS><<<blocks64(count), 64, 0, s>>>(
+        dModel, dStates, blobBytes, count, mask, static_cast<const R *>(q),
+        static_cast<const R *>(root), static_cast<const R *>(ext));
+    launched("resetKernel");
+    record(s);
+  }
+  void step(const void *target, const void *force, int substeps, double kp, double limit,
+            hipStream_t s) override {
+    DeviceGuard guard(device);
+    require(target && force, "step: null buffer");
+    // extension.cu:290-294: zero limit = uncapped; negative/non-finite invalid.
+    require(substeps > 0 && kp >= 0 && std::isfinite(kp) && limit >= 0 && std::isfinite(limit),
+            "Invalid controls");
+    wait(s);
+    advance(dStates, count, target, force, nullptr, substeps, kp, limit, s);
+    record(s);
+  }
+  void stepMotor(const void *motor, const void *force, hipStream_t s) override {
+    DeviceGuard guard(device);
+    require(motor && force, "step_motor: null buffer");
+    wait(s);
+    advance(dStates, count, nullptr, force, motor, 1, 0, 0, s);
+    record(s);
+  }
+  void state(void *bodies, void *joints, void *diag, hipStream_t s) override {
+    DeviceGuard guard(device);
+    require(bodies && joints && diag, "state: null buffer");
+    wait(s);
+    snapshotKernel<R, B, J, CG, CS><<<blocks64(count), 64, 0, s>>>(
+        dModel, dStates, blobBytes, count, static_cast<R *>(bodies), static_cast<R *>(joints),
+        static_cast<R *>(diag));
+    launched("snapshotKernel");
+    record(s);
+  }
+  void contactForces(int groundOnly, void *out, hipStream_t s) override {
+    DeviceGuard guard(device);
+    require(out, "contact_forces: null buffer");
+    wait(s);
+    contactForcesKernel<R, B, J, CG, CS><<<blocks64(count), 64, 0, s>>>(
+        dModel, dStates, blobBytes, count, groundOnly, static_cast<R *>(out));
+    launched("contactForcesKernel");
+    record(s);
+  }
+  void selfContactStats(void *out, hipStream_t s) override {
+    DeviceGuard guard(device);
+    require(out, "self_contact_stats: null buffer");
+    wait(s);
+    selfContactStatsKernel<R, B, J, CG, CS><<<blocks64(count), 64, 0, s>>>(
+        dModel, dStates, blobBytes, count, static_cast<R *>(out));
+    launched("selfContactStatsKernel");
+    record(s);
+  }
+  void contactCounts(void *out, hipStream_t s) override {
+    DeviceGuard guard(device);
+    require(out, "contact_counts: null buffer");
+    wait(s);
+    contactCountsKernel<R, B, J, CG, CS><<<blocks64(count), 64, 0, s>>>(dStates, blobBytes, count,
+                                                                        static_cast<R *>(out));
+    launched("contactCountsKernel");
+    record(s);
+  }
+  void generalizedLoads(const void *offset, void *out, hipStream_t s) override {
+    DeviceGuard guard(device);
+    require(offset && out, "generalized_loads: null buffer");
+    wait(s);
+    generalizedLoadsKernel<R, B, J, CG, CS><<<blocks64(count), 64, 0, s>>>(
+        dModel, dStates, blobBytes, count, static_cast<const R *>(offset), static_cast<R *>(out));
+    launched("generalizedLoadsKernel");
+    record(s);
+  }
+  void reference(const void *target, const void *force, int substeps, double kp, double limit,
+                 void *bodies, void *joints, void *diag) override {
+    DeviceGuard guard(device);
+    require(target && force && bodies && joints && diag && substeps > 0,
+            "Invalid CPU reference inputs");
+    const int nb = host.bodies.size(), nj = host.joints.size();
+    unsigned char *state = nullptr;
+    R *buf = nullptr;
+    const size_t nbuf = nj + 3 + nb * 13 + nj * 2 + 6;
+    try {
+      hipCheck(hipMalloc(&state, blobBytes), "hipMalloc(reference state)");
+      hipCheck(hipMalloc(&buf, nbuf * sizeof(R)), "hipMalloc(reference io)");
+      R *dTarget = buf, *dForce = buf + nj, *dB = dForce + 3, *dJ = dB + nb * 13,
+        *dD = dJ + nj * 2;
+      hipCheck(hipMemcpy(dTarget, target, nj * sizeof(R), hipMemcpyHostToDevice), "upload");
+      hipCheck(hipMemcpy(dForce, force, 3 * sizeof(R), hipMemcpyHostToDevice), "upload");
+      hipCheck(hipMemset(state, 0, blobBytes), "hipMemset");
+      initializeKernel<R, B, J, CG, CS><<<1, 64, 0, 0>>>(dModel, state, blobBytes, 1);
+      launched("initializeKernel");
+      // extension.cu:403-410 sets force, kp, limit and target only; the
+      // model's torque/friction/damping are already in place.
+      advance(state, 1, dTarget, dForce, nullptr, substeps, kp, limit, 0);
+      snapshotKernel<R, B, J, CG, CS><<<1, 64, 0, 0>>>(dModel, state, blobBytes, 1, dB, dJ, dD);
+      launched("snapshotKernel");
+      hipCheck(hipMemcpy(bodies, dB, nb * 13 * sizeof(R), hipMemcpyDeviceToHost), "download");
+      hipCheck(hipMemcpy(joints, dJ, nj * 2 * sizeof(R), hipMemcpyDeviceToHost), "download");
+      hipCheck(hipMemcpy(diag, dD, 6 * sizeof(R), hipMemcpyDeviceToHost), "download");
+    } catch (...) {
+      if (state)
+        (void)hipFree(state);
+      if (buf)
+        (void)hipFree(buf);
+      throw;
+    }
+    hipCheck(hipFree(state), "hipFree");
+    hipCheck(hipFree(buf), "hipFree");
+  }
+  void layout(long long *out) const override;
+  void exportState(void *dst, hipStream_t s) override {
+    DeviceGuard guard(device);
+    require(dst, "export_state: null buffer");
+    wait(s);
+    hipCheck(hipMemcpyAsync(dst, dStates, size_t(blobBytes) * count, hipMemcpyDeviceToDevice, s),
+             "export_state");
+    record(s);
+  }
+  void importState(const void *src, hipStream_t s) override {
+    DeviceGuard guard(device);
+    require(src, "import_state: null buffer");
+    wait(s);
+    hipCheck(hipMemcpyAsync(dStates, src, size_t(blobBytes) * count, hipMemcpyDeviceToDevice, s),
+             "import_state");
+    record(s);
+  }
+};
+
+#define DUCK_OFF(T, f) static_cast<long long>(offsetof(T, f))
+template <class R, int B, int J, int CG, int CS, int L>
+void Batch<R, B, J, CG, CS, L>::layout(long long *o) const {
+  using S = EnvState<R, B, J, CG, CS>;
+  using GC = GroundContact<R>;
+  using SC = SelfContact<R>;
+  const long long v[] = {
+      B, J, CG, CS, sizeof(R), blobBytes, static_cast<long long>(headerBytes<S>()),
+      DUCK_OFF(S, x), DUCK_OFF(S, q), DUCK_OFF(S, v), DUCK_OFF(S, w), DUCK_OFF(S, mass),
+      DUCK_OFF(S, inertia), DUCK_OFF(S, force), DUCK_OFF(S, lambda), DUCK_OFF(S, penalty),
+      DUCK_OFF(S, lambdaF), DUCK_OFF(S, penaltyF), DUCK_OFF(S, target), DUCK_OFF(S, kp),
+      DUCK_OFF(S, maxTorque), DUCK_OFF(S, torque), DUCK_OFF(S, frictionloss),
+      DUCK_OFF(S, damping), DUCK_OFF(S, diag), DUCK_OFF(S, friction), DUCK_OFF(S, failed),
+      DUCK_OFF(S, ngc), DUCK_OFF(S, nsc), DUCK_OFF(S, colors), DUCK_OFF(S, colorCount),
+      DUCK_OFF(S, gc), static_cast<long long>(sizeof(GC)), DUCK_OFF(S, sc),
+      static_cast<long long>(sizeof(SC)), DUCK_OFF(GC, id), DUCK_OFF(GC, local),
+      DUCK_OFF(GC, anchor), DUCK_OFF(GC, c0), DUCK_OFF(GC, lambda), DUCK_OFF(GC, penalty),
+      DUCK_OFF(SC, id), DUCK_OFF(SC, local), DUCK_OFF(SC, localB), DUCK_OFF(SC, t1),
+      DUCK_OFF(SC, t2), DUCK_OFF(SC, n), DUCK_OFF(SC, c0), DUCK_OFF(SC, friction),
+      DUCK_OFF(SC, lambda), DUCK_OFF(SC, penalty)};
+  static_assert(sizeof(v) / sizeof(v[0]) == 51, "layout descriptor has 51 entries");
+  for (int i = 0; i < 51; ++i)
+    o[i] = v[i];
+}
+#undef DUCK_OFF
+
+const char *kMicroDuckJoints[14] = {
+    "left_hip_yaw",    "left_hip_roll",  "left_hip_pitch", "left_knee",
+    "left_ankle",      "neck_pitch",     "head_pitch",     "head_yaw",
+    "head_roll",       "right_hip_yaw",  "right_hip_roll", "right_hip_pitch",
+    "right_knee",      "right_ankle"};
+
+template <class R>
+BatchBase *makeBatch(HostModel &&m, int n, double dt, int iterations, int device) {
+  const int nb = m.bodies.size(), nj = m.joints.size(), ns = m.shapes.size(),
+            np = m.pairs.size();
+  if (nb <= 16 && nj <= 16 && ns <= 16 && np <= 8 && m.groundCapacity <= 64)
+    return new Batch<R, 16, 16, 64, 8, 8>(std::move(m), n, dt, iterations, device);
+  // Per-body contact masks are 64-bit: at most 64 ground contacts per env.
+  if (m.groundCapacity > 64)
+    throw DuckError(DUCK_ERR_MODEL, "Model exceeds selected state contact capacity");
+  return new Batch<R, 32, 32, 64, 32, 32>(std::move(m), n, dt, iterations, device);
+}
+
+template <class F> int guarded(F &&f) {
+  try {
+    f();
+    return DUCK_OK;
+  } catch (const DuckError &e) {
+    g_lastError = e.what();
+    return e.code;
+  } catch (const std::invalid_argument &e) {
+    // model.hpp:5-8 checks (pybind11 maps them to ValueError)
+    g_lastError = e.what();
+    return DUCK_ERR_MODEL;
+  } catch (const std::exception &e) {
+    // Solver::load errors (pybind11 maps them to RuntimeError)
+    g_lastError = e.what();
+    return DUCK_ERR_RUNTIME;
+  }
+}
+BatchBase *as(void *h) {
+  if (!h)
+    throw DuckError(DUCK_ERR_ARGUMENT, "null batch handle");
+  return static_cast<BatchBase *>(h);
+}
+hipStream_t st(void *s) { return static_cast<hipStream_t>(s); }
+
+} // namespace
+} // namespace duckhip
+
+using namespace duckhip;
+
+extern "C" {
+
+const char *duck_last_error(void) { return g_lastError.c_str(); }
+
+int duck_create(const char *model_path, int num_envs, double dt, int iterations, int device,
+                int fp_bits, unsigned flags, void **out_handle) {
+  return guarded([&] {
+    require(out_handle != nullptr && model_path != nullptr, "null argument");
+    *out_handle = nullptr;
+    require(num_envs > 0 && num_envs <= 65536 && dt > 0 && std::isfinite(dt) && iterations > 0,
+            "Invalid batch parameters");
+    require(fp_bits == 32 || fp_bits == 64, "fp_bits must be 32 or 64");
+    int devices = 0;
+    hipCheck(hipGetDeviceCount(&devices), "hipGetDeviceCount");
+    require(device >= 0 && device < devices, "Invalid device index");
+    HostModel m = loadModel(model_path);
+    if (flags & DUCK_FLAG_SPECIALIZED) {
+      require(m.bodies.size() == 16 && m.joints.size() == 14,
+              "MicroDuck specialized backend requires 16 bodies and 14 hinges");
+      for (int i = 0; i < 14; ++i) {
+        std::string label = m.joints[i].name;
+        if (label.rfind("robot/", 0) == 0)
+          label = label.substr(6);
+        require(label == kMicroDuckJoints[i], "Unsupported MicroDuck joint layout");
+      }
+    }
+    BatchBase *b = fp_bits == 64 ? makeBatch<double>(std::move(m), num_envs, dt, iterations, device)
+                                 : makeBatch<float>(std::move(m), num_envs, dt, iterations, device);
+    *out_handle = b;
+  });
+}
+
+void duck_destroy(void *handle) { delete static_cast<BatchBase *>(handle); }
+
+int duck_dims(void *handle, int *bodies, int *joints, int *contact_capacity) {
+  return guarded([&] {
+    auto *b = as(handle);
+    if (bodies)
+      *bodies = b->host.bodies.size();
+    if (joints)
+      *joints = b->host.joints.size();
+    if (contact_capacity)
+      *contact_capacity = b->contactCapacity;
+  });
+}
+int duck_num_envs(void *handle) { return handle ? as(handle)->count : 0; }
+int duck_fp_bits(void *handle) { return handle ? as(handle)->fpBits : 0; }
+long long duck_state_bytes(void *handle) { return handle ? as(handle)->blobBytes : 0; }
+
+const char *duck_joint_name(void *handle, int index) {
+  if (!handle)
+    return nullptr;
+  auto *b = as(handle);
+  if (index < 0 || index >= int(b->names.size()))
+    return nullptr;
+  return b->names[index].c_str();
+}
+
+int duck_reset(void *handle, const unsigned char *mask, const void *q, const void *root,
+               const void *ext, void *hip_stream) {
+  return guarded([&] { as(handle)->reset(mask, q, root, ext, st(hip_stream)); });
+}
+int duck_step(void *handle, const void *target, const void *force, int substeps, double kp,
+              double limit, void *hip_stream) {
+  return guarded([&] { as(handle)->step(target, force, substeps, kp, limit, st(hip_stream)); });
+}
+int duck_step_motor(void *handle, const void *motor, const void *force, void *hip_stream) {
+  return guarded([&] { as(handle)->stepMotor(motor, force, st(hip_stream)); });
+}
+int duck_state(void *handle, void *bodies, void *joints, void *diag, void *hip_stream) {
+  return guarded([&] { as(handle)->state(bodies, joints, diag, st(hip_stream)); });
+}
+int duck_contact_forces(void *handle, int ground_only, void *out, void *hip_stream) {
+  return guarded([&] { as(handle)->contactForces(ground_only, out, st(hip_stream)); });
+}
+int duck_self_contact_stats(void *handle, void *out, void *hip_stream) {
+  return guarded([&] { as(handle)->selfContactStats(out, st(hip_stream)); });
+}
+int duck_contact_counts(void *handle, void *out, void *hip_stream) {
+  return guarded([&] { as(handle)->contactCounts(out, st(hip_stream)); });
+}
+int duck_generalized_loads(void *handle, const void *offset, void *out, void *hip_stream) {
+  return guarded([&] { as(handle)->generalizedLoads(offset, out, st(hip_stream)); });
+}
+int duck_state_layout(void *handle, long long *out) {
+  return guarded([&] {
+    require(out != nullptr, "null argument");
+    as(handle)->layout(out);
+  });
+}
+int duck_export_state(void *handle, void *dst, void *hip_stream) {
+  return guarded([&] { as(handle)->exportState(dst, st(hip_stream)); });
+}
+int duck_import_state(void *handle, const void *src, void *hip_stream) {
+  return guarded([&] { as(handle)->importState(src, st(hip_stream)); });
+}
+int duck_reference(void *handle, const void *target, const void *force, int substeps, double kp,
+                   double limit, void *bodies, void *joints, void *diag) {
+  return guarded(
+      [&] { as(handle)->reference(target, force, substeps, kp, limit, bodies, joints, diag); });
+}
+}

@@ -1,0 +1,54 @@
+"""Build libduck_hip.so (gfx950) in-tree with hipcc.
+
+Flags:
+  -ffp-contract=off  no FMA contraction, so float results track the reference
+                     CPU build (the reference compiles its GPU path with
+                     --fmad=false, scripts/build_cuda.py:37)
+  -Xclang -target-feature -Xclang -packed-fp32-ops
+                     no packed FP32 instructions
+"""
+
+from __future__ import annotations
+
+import os
+import subprocess
+from pathlib import Path
+
+PACKAGE = Path(__file__).resolve().parent
+ROOT = PACKAGE.parent
+LIBRARY = PACKAGE / "libduck_hip.so"
+SOURCES = [PACKAGE / "csrc" / "duck_hip.hip", PACKAGE / "csrc" / "duck_model.cpp"]
+HEADERS = sorted((PACKAGE / "csrc").glob("*.hpp")) + [ROOT / "include" / "duck_hip.h"]
+ARCH = os.environ.get("DUCK_HIP_ARCH", "gfx950")
+FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
+    "-ffp-contract=off",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall", "-Wno-unused-function", "-Wno-unused-variable",
+]
+
+
+def hipcc():
+    for candidate in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", "hipcc"):
+        if candidate and (Path(candidate).exists() or candidate == "hipcc"):
+            return candidate
+    raise FileNotFoundError("hipcc not found")
+
+
+def build(force: bool = True, verbose: bool = False) -> Path:
+    """Compile the HIP library; `force=False` skips an up-to-date build."""
+    if not force and LIBRARY.exists():
+        newest = max(p.stat().st_mtime for p in SOURCES + HEADERS)
+        if LIBRARY.stat().st_mtime >= newest:
+            return LIBRARY
+    tmp = LIBRARY.with_suffix(".so.tmp")
+    cmd = [hipcc(), *FLAGS, f"-I{ROOT / 'include'}", *map(str, SOURCES), "-o", str(tmp)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    subprocess.run(cmd, check=True)
+    os.replace(tmp, LIBRARY)
+    return LIBRARY
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

@@ -1,0 +1,266 @@
+"""`CudaBatch`: the reference's native batch interface over libduck_hip.so.
+
+Mirrors the pybind11 class of src/cuda/extension.cu:436-452 (constructor
+arguments, method names, shapes, dtypes and error behaviour): inputs are
+caller-owned device tensors checked exactly as extension.cu:206-213 checks
+them (device, dtype, contiguity, shape -> RuntimeError), outputs are fresh
+tensors, and every call is asynchronous on the current torch stream.  The
+physics runs in the HIP kernels of libduck_hip.so; there is no CPU fallback:
+constructing a batch without the built library raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import torch
+
+LIBRARY = Path(__file__).resolve().parent / "libduck_hip.so"
+_lib = None
+
+
+def library():
+    """Load libduck_hip.so (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not LIBRARY.exists():
+            raise RuntimeError(
+                f"{LIBRARY} is missing: build it with `python -m duck_gym_amd.hipbuild` "
+                "(the HIP extension is required; there is no CPU fallback)")
+        lib = ctypes.CDLL(str(LIBRARY))
+        vp, ip, cp = ctypes.c_void_p, ctypes.c_int, ctypes.c_char_p
+        dbl = ctypes.c_double
+        sig = {
+            "duck_create": (ip, [cp, ip, dbl, ip, ip, ip, ctypes.c_uint, ctypes.POINTER(vp)]),
+            "duck_destroy": (None, [vp]),
+            "duck_dims": (ip, [vp, ctypes.POINTER(ip), ctypes.POINTER(ip), ctypes.POINTER(ip)]),
+            "duck_num_envs": (ip, [vp]),
+            "duck_fp_bits": (ip, [vp]),
+            "duck_state_bytes": (ctypes.c_longlong, [vp]),
+            "duck_joint_name": (cp, [vp, ip]),
+            "duck_reset": (ip, [vp, vp, vp, vp, vp, vp]),
+            "duck_step": (ip, [vp, vp, vp, ip, dbl, dbl, vp]),
+            "duck_step_motor": (ip, [vp, vp, vp, vp]),
+            "duck_state": (ip, [vp, vp, vp, vp, vp]),
+            "duck_contact_forces": (ip, [vp, ip, vp, vp]),
+            "duck_self_contact_stats": (ip, [vp, vp, vp]),
+            "duck_contact_counts": (ip, [vp, vp, vp]),
+            "duck_generalized_loads": (ip, [vp, vp, vp, vp]),
+            "duck_reference": (ip, [vp, vp, vp, ip, dbl, dbl, vp, vp, vp]),
+            "duck_state_layout": (ip, [vp, ctypes.POINTER(ctypes.c_longlong)]),
+            "duck_export_state": (ip, [vp, vp, vp]),
+            "duck_import_state": (ip, [vp, vp, vp]),
+            "duck_last_error": (cp, []),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+EXPORTED = (
+    "duck_create", "duck_destroy", "duck_dims", "duck_num_envs", "duck_fp_bits",
+    "duck_state_bytes", "duck_joint_name", "duck_reset", "duck_step", "duck_step_motor",
+    "duck_state", "duck_contact_forces", "duck_self_contact_stats", "duck_contact_counts",
+    "duck_generalized_loads", "duck_reference", "duck_state_layout", "duck_export_state",
+    "duck_import_state", "duck_last_error",
+)
+
+
+def _raise(code, what):
+    """Map a C-ABI error code to the exception the reference raises:
+    TORCH_CHECK and std::runtime_error -> RuntimeError, std::invalid_argument
+    (model.hpp) -> ValueError."""
+    msg = library().duck_last_error().decode()
+    if code == 2:
+        raise ValueError(f"{what}: {msg}")
+    if code == 3:
+        raise RuntimeError(f"{what}: HIP failure: {msg}")
+    raise RuntimeError(f"{what}: {msg}")
+
+
+class CudaBatch:
+    """Batched AVBD environments on one MI355X (gfx950) device."""
+
+    def __init__(self, model, num_envs, dt=0.001, iterations=200, device=0, fp64=False,
+                 specialized=False, shared_memory=False):
+        # `shared_memory` is accepted for signature compatibility: the gfx950
+        # kernel always stages environment state in LDS.
+        lib = library()
+        self._h = None
+        handle = ctypes.c_void_p()
+        code = lib.duck_create(str(model).encode(), int(num_envs), float(dt), int(iterations),
+                               int(device), 64 if fp64 else 32, 1 if specialized else 0,
+                               ctypes.byref(handle))
+        if code:
+            _raise(code, "CudaBatch")
+        self._h = handle
+        self.device = torch.device("cuda", int(device))
+        self.dtype = torch.float64 if fp64 else torch.float32
+        self.num_envs = int(num_envs)
+        b, j, c = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+        lib.duck_dims(self._h, ctypes.byref(b), ctypes.byref(j), ctypes.byref(c))
+        self.num_bodies, self.num_joints, self.contact_capacity = b.value, j.value, c.value
+        self._names = [lib.duck_joint_name(self._h, i).decode() for i in range(self.num_joints)]
+
+    def __del__(self):
+        if getattr(self, "_h", None) and _lib is not None:
+            _lib.duck_destroy(self._h)
+            self._h = None
+
+    @property
+    def joint_names(self):
+        return list(self._names)
+
+    @property
+    def state_bytes(self):
+        return int(library().duck_state_bytes(self._h))
+
+    # --------------------------------------------------------------- checks
+    def _stream(self):
+        return ctypes.c_void_p(torch.cuda.current_stream(self.device).cuda_stream)
+
+    def _check(self, t, shape, dtype=None):
+        dtype = self.dtype if dtype is None else dtype
+        if not (isinstance(t, torch.Tensor) and t.is_cuda and t.device.index == self.device.index
+                and t.dtype == dtype and t.is_contiguous() and list(t.shape) == list(shape)):
+            raise RuntimeError("Invalid CUDA tensor device/dtype/shape/contiguity")
+        t.record_stream(torch.cuda.current_stream(self.device))
+        return ctypes.c_void_p(t.data_ptr())
+
+    def _empty(self, *shape):
+        return torch.empty(shape, device=self.device, dtype=self.dtype)
+
+    # ------------------------------------------------------------- methods
+    def reset(self, mask, q, root, ext=None):
+        E, J = self.num_envs, self.num_joints
+        args = [self._check(mask, [E], torch.bool), self._check(q, [E, J]),
+                self._check(root, [E, 6]),
+                None if ext is None else self._check(ext, [E, 5])]
+        with torch.cuda.device(self.device):
+            code = library().duck_reset(self._h, *args, self._stream())
+        if code:
+            _raise(code, "reset")
+
+    def step(self, target, forces, substeps, kp, limit):
+        E, J = self.num_envs, self.num_joints
+        t, f = self._check(target, [E, J]), self._check(forces, [E, 3])
+        with torch.cuda.device(self.device):
+            code = library().duck_step(self._h, t, f, int(substeps), float(kp), float(limit),
+                                       self._stream())
+        if code:
+            _raise(code, "step")
+
+    def step_motor(self, motor, forces):
+        E, J = self.num_envs, self.num_joints
+        m, f = self._check(motor, [E, J, 3]), self._check(forces, [E, 3])
+        with torch.cuda.device(self.device):
+            code = library().duck_step_motor(self._h, m, f, self._stream())
+        if code:
+            _raise(code, "step_motor")
+
+    def state(self):
+        E = self.num_envs
+        b = self._empty(E, self.num_bodies, 13)
+        j = self._empty(E, self.num_joints, 2)
+        d = self._empty(E, 6)
+        with torch.cuda.device(self.device):
+            code = library().duck_state(self._h, ctypes.c_void_p(b.data_ptr()),
+                                        ctypes.c_void_p(j.data_ptr()),
+                                        ctypes.c_void_p(d.data_ptr()), self._stream())
+        if code:
+            _raise(code, "state")
+        return b, j, d
+
+    def contact_forces(self, ground_only=False):
+        out = self._empty(self.num_envs, self.num_bodies, 3)
+        with torch.cuda.device(self.device):
+            code = library().duck_contact_forces(self._h, int(bool(ground_only)),
+                                                 ctypes.c_void_p(out.data_ptr()), self._stream())
+        if code:
+            _raise(code, "contact_forces")
+        return out
+
+    def self_contact_stats(self):
+        out = self._empty(self.num_envs, 2)
+        with torch.cuda.device(self.device):
+            code = library().duck_self_contact_stats(self._h, ctypes.c_void_p(out.data_ptr()),
+                                                     self._stream())
+        if code:
+            _raise(code, "self_contact_stats")
+        return out
+
+    def contact_counts(self):
+        out = self._empty(self.num_envs, 2)
+        with torch.cuda.device(self.device):
+            code = library().duck_contact_counts(self._h, ctypes.c_void_p(out.data_ptr()),
+                                                 self._stream())
+        if code:
+            _raise(code, "contact_counts")
+        return out
+
+    def generalized_loads(self, offset):
+        o = self._check(offset, [self.num_envs, 3])
+        out = self._empty(self.num_envs, self.num_joints, 3)
+        with torch.cuda.device(self.device):
+            code = library().duck_generalized_loads(self._h, o, ctypes.c_void_p(out.data_ptr()),
+                                                    self._stream())
+        if code:
+            _raise(code, "generalized_loads")
+        return out
+
+    def reference(self, target, forces, substeps, kp, limit):
+        J = self.num_joints
+        if not (isinstance(target, torch.Tensor) and target.device.type == "cpu"
+                and target.is_contiguous() and target.dtype == self.dtype
+                and list(target.shape) == [J]):
+            raise RuntimeError("Invalid CPU reference target")
+        if not (isinstance(forces, torch.Tensor) and forces.device.type == "cpu"
+                and forces.is_contiguous() and list(forces.shape) == [3]
+                and forces.dtype == self.dtype and substeps > 0):
+            raise RuntimeError("Invalid CPU reference inputs")
+        b = torch.empty(self.num_bodies, 13, dtype=self.dtype)
+        j = torch.empty(J, 2, dtype=self.dtype)
+        d = torch.empty(6, dtype=self.dtype)
+        with torch.cuda.device(self.device):
+            torch.cuda.synchronize(self.device)
+            code = library().duck_reference(
+                self._h, ctypes.c_void_p(target.data_ptr()), ctypes.c_void_p(forces.data_ptr()),
+                int(substeps), float(kp), float(limit), ctypes.c_void_p(b.data_ptr()),
+                ctypes.c_void_p(j.data_ptr()), ctypes.c_void_p(d.data_ptr()))
+        if code:
+            _raise(code, "reference")
+        return b, j, d
+
+    # ------------------------------------------------ state introspection
+    def state_layout(self):
+        out = (ctypes.c_longlong * 51)()
+        code = library().duck_state_layout(self._h, out)
+        if code:
+            _raise(code, "state_layout")
+        return list(out)
+
+    def codec(self):
+        from .state import StateCodec
+
+        return StateCodec(self.state_layout(), self.num_bodies, self.num_joints)
+
+    def export_state(self):
+        """uint8 tensor [E, state_bytes] copy of every environment's HBM state."""
+        out = torch.empty(self.num_envs, self.state_bytes, device=self.device, dtype=torch.uint8)
+        with torch.cuda.device(self.device):
+            code = library().duck_export_state(self._h, ctypes.c_void_p(out.data_ptr()),
+                                               self._stream())
+        if code:
+            _raise(code, "export_state")
+        return out
+
+    def import_state(self, raw):
+        raw = self._check(raw, [self.num_envs, self.state_bytes], torch.uint8)
+        with torch.cuda.device(self.device):
+            code = library().duck_import_state(self._h, raw, self._stream())
+        if code:
+            _raise(code, "import_state")

@@ -1,0 +1,110 @@
+/* C ABI of the MI355X (gfx950) batched AVBD environment step.
+ *
+ * Drop-in replacement for the CUDA launch path of the reference batch
+ * (src/cuda/extension.cu:160-173 `Interface`, bound to Python as `CudaBatch`
+ * at extension.cu:436-452).  The library owns the model and the per-env
+ * state in HBM; callers own every input and output buffer.  Device buffers
+ * are plain device pointers in the batch dtype (float32, or float64 with
+ * fp_bits = 64), C-contiguous with the shapes given below; every call is
+ * asynchronous on `hip_stream` (a hipStream_t, NULL = the null stream) and
+ * is ordered after the batch's previous call on any stream by a private
+ * event, as extension.cu:204-205 orders them.
+ *
+ * Every function returns 0 on success or a nonzero code; duck_last_error()
+ * then describes the failure (thread-local).  Numerical faults of one
+ * environment are not errors: they set that environment's diag[5] (failed)
+ * until a reset clears it (kernel.cuh:382, 395).
+ */
+#ifndef DUCK_HIP_H
+#define DUCK_HIP_H
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  DUCK_OK = 0,
+  DUCK_ERR_ARGUMENT = 1, /* invalid argument (TORCH_CHECK in extension.cu) */
+  DUCK_ERR_MODEL = 2,    /* model rejected by the flattening checks (model.hpp:5-8) */
+  DUCK_ERR_DEVICE = 3,   /* HIP runtime failure */
+  DUCK_ERR_RUNTIME = 4   /* unreadable or malformed model file (solver.cpp:67-174) */
+};
+
+/* Flags of duck_create. */
+#define DUCK_FLAG_SPECIALIZED 1u /* require the MicroDuck 16-body/14-hinge layout */
+
+/* CudaBatch(model, num_envs, dt, iterations, device, fp64, specialized)
+ * (extension.cu:216-265, 423-441).  num_envs in [1, 65536]. */
+int duck_create(const char *model_path, int num_envs, double dt, int iterations, int device,
+                int fp_bits, unsigned flags, void **out_handle);
+void duck_destroy(void *handle);
+
+/* Bodies (including the static world body 0), hinges and contact capacity. */
+int duck_dims(void *handle, int *bodies, int *joints, int *contact_capacity);
+int duck_num_envs(void *handle);
+int duck_fp_bits(void *handle);
+/* CudaBatch.joint_names (extension.cu:416-421); valid until duck_destroy. */
+const char *duck_joint_name(void *handle, int index);
+
+/* CudaBatch.reset(mask[E] bool, q[E,J], root[E,6]) (extension.cu:273-284):
+ * masked re-initialisation and forward kinematics from joint angles and a
+ * root (xyz offset, rotation vector).  `ext` (may be NULL) is an [E,5] batch
+ * extension with no reference counterpart: ground friction (< 0 keeps the
+ * shape friction), mass/inertia scale, initial linear velocity xyz. */
+int duck_reset(void *handle, const unsigned char *mask, const void *q, const void *root,
+               const void *ext, void *hip_stream);
+
+/* CudaBatch.step(target[E,J], forces[E,3], substeps, kp, limit)
+ * (extension.cu:285-306): substeps > 0, kp >= 0, limit >= 0 (0 = uncapped). */
+int duck_step(void *handle, const void *target, const void *force, int substeps, double kp,
+              double limit, void *hip_stream);
+
+/* CudaBatch.step_motor(motor[E,J,3], forces[E,3]) (extension.cu:307-320):
+ * one step with explicit (torque, dry-friction budget, damping) per hinge. */
+int duck_step_motor(void *handle, const void *motor, const void *force, void *hip_stream);
+
+/* CudaBatch.state() (extension.cu:321-335): bodies[E,B,13] (COM xyz, wxyz,
+ * v, w), joints[E,J,2] (angle, rate), diag[E,6] (joint error, penetration,
+ * contacts, converged, axis error, failed). */
+int duck_state(void *handle, void *bodies, void *joints, void *diag, void *hip_stream);
+
+/* CudaBatch.contact_forces(ground_only) -> [E,B,3] (extension.cu:336-347). */
+int duck_contact_forces(void *handle, int ground_only, void *out, void *hip_stream);
+/* CudaBatch.self_contact_stats() -> [E,2] (extension.cu:348-359). */
+int duck_self_contact_stats(void *handle, void *out, void *hip_stream);
+/* CudaBatch.contact_counts() -> [E,2] (extension.cu:360-370). */
+int duck_contact_counts(void *handle, void *out, void *hip_stream);
+/* CudaBatch.generalized_loads(offset[E,3]) -> [E,J,3] (extension.cu:371-384). */
+int duck_generalized_loads(void *handle, const void *offset, void *out, void *hip_stream);
+
+/* CudaBatch.reference(target[J], forces[3], substeps, kp, limit)
+ * (extension.cu:385-415): one environment advanced from the model file's
+ * initial state; host pointers in the batch dtype.  Synchronous.  Computed on
+ * the batch's device with the same kernels (this library carries no CPU
+ * solver). */
+int duck_reference(void *handle, const void *target, const void *force, int substeps, double kp,
+                   double limit, void *bodies, void *joints, void *diag);
+
+/* Size in bytes of one environment's HBM state blob. */
+long long duck_state_bytes(void *handle);
+
+/* State introspection (no reference counterpart: the reference keeps its
+ * state opaque).  For tests that compare the full per-env state with the CPU
+ * oracle and that seed identical states.  duck_state_layout writes 51
+ * int64 values: capacities B J CG CS, scalar bytes, blob bytes, header bytes,
+ * the byte offsets of the EnvState fields x q v w mass inertia force lambda
+ * penalty lambdaF penaltyF target kp maxTorque torque frictionloss damping
+ * diag friction failed ngc nsc colors colorCount gc, ground-contact bytes, the
+ * offset of sc, self-contact bytes, then the field offsets of a ground contact
+ * (id local anchor c0 lambda penalty) and of a self contact (id local localB
+ * t1 t2 n c0 friction lambda penalty).  Export/import copy all E blobs
+ * (E * duck_state_bytes bytes) to/from a device buffer. */
+int duck_state_layout(void *handle, long long *out);
+int duck_export_state(void *handle, void *dst, void *hip_stream);
+int duck_import_state(void *handle, const void *src, void *hip_stream);
+
+const char *duck_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

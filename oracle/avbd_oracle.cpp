@@ -1019,7 +1019,7 @@ template <class R> struct Env {
             V3<R> e;
             e.at(k) = f;
             geometric(H, rotate(b.q, bi == j.a ? j.ra : neg(j.rb)), e);
-          } else {
+          } else if (k < 5) {
             V3<R> aa = rotate(bodies[j.a].q, j.axisA), ta = rotate(bodies[j.a].q, j.tangentA);
             if (k == 4)
               ta = cross(aa, ta);

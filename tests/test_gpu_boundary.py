@@ -1,0 +1,171 @@
+"""Boundary behaviour of `CudaBatch` on the GPU, after tests/cuda_boundary.py
+and tests/test_tensor_env.py of the reference: input validation errors,
+per-env NaN isolation and reset recovery, masked reset, output ownership,
+cross-stream ordering, batch-size invariance (bit-exact) and substep
+chunking (bit-exact)."""
+
+import numpy as np
+import pytest
+import torch
+
+from duck_gym_amd import CudaBatch
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+DT, ITER, KP = 0.005, 10, 8.0
+
+
+def _batch(model, n, fp64=False, iterations=ITER):
+    return CudaBatch(model, n, DT, iterations, 0, fp64)
+
+
+def _reset_home(batch, home, dtype=torch.float32):
+    n = batch.num_envs
+    batch.reset(torch.ones(n, dtype=torch.bool, device=DEV),
+                torch.tensor(np.tile(home, (n, 1)), dtype=dtype, device=DEV),
+                torch.zeros(n, 6, dtype=dtype, device=DEV))
+
+
+def test_invalid_inputs_raise(models, home):
+    b = _batch(models["standing"], 4)
+    _reset_home(b, home)
+    good = torch.tensor(np.tile(home, (4, 1)), dtype=torch.float32, device=DEV)
+    forces = torch.zeros(4, 3, device=DEV)
+    for bad in (good.double(), good[:, :-1].contiguous(), good.cpu(), good.t().contiguous().t()):
+        with pytest.raises(RuntimeError):
+            b.step(bad, forces, 1, KP, 0.0)
+    with pytest.raises(RuntimeError):
+        b.step(good, forces, 0, KP, 0.0)
+    with pytest.raises(RuntimeError):
+        b.step(good, forces, 1, -1.0, 0.0)
+    with pytest.raises(RuntimeError):
+        b.step(good, forces, 1, KP, float("nan"))
+    # TORCH_CHECK (extension.cu:219) and Solver::load (solver.cpp:69-70)
+    # surface as RuntimeError in the reference.
+    with pytest.raises(RuntimeError):
+        CudaBatch(models["standing"], 0, DT, ITER)
+    with pytest.raises(RuntimeError):
+        CudaBatch(str(models["standing"]) + ".missing", 4, DT, ITER)
+    assert b.joint_names[0] == "left_hip_yaw" and len(b.joint_names) == 14
+
+
+def test_nan_isolation_and_reset_recovery(models, home):
+    b = _batch(models["standing"], 4)
+    _reset_home(b, home)
+    target = torch.tensor(np.tile(home, (4, 1)), dtype=torch.float32, device=DEV)
+    target[2, 0] = float("nan")
+    b.step(target, torch.zeros(4, 3, device=DEV), 1, KP, 0.0)
+    assert b.state()[2][:, 5].tolist() == [0, 0, 1, 0]
+    frozen = b.state()[0][2].clone()
+    target[2, 0] = 0.0
+    b.step(target, torch.zeros(4, 3, device=DEV), 1, KP, 0.0)
+    torch.testing.assert_close(b.state()[0][2], frozen, rtol=0, atol=0)
+    motor = torch.zeros(4, 14, 3, device=DEV)
+    motor[1, 0, 1] = -1  # negative friction budget is invalid (kernel.cuh:454)
+    b.step_motor(motor, torch.zeros(4, 3, device=DEV))
+    assert b.state()[2][:, 5].tolist() == [0, 1, 1, 0]
+    _reset_home(b, home)
+    assert not b.state()[2][:, 5].any()
+
+
+def test_masked_reset_and_output_ownership(models, home):
+    b = _batch(models["standing"], 4)
+    _reset_home(b, home)
+    initial = b.state()[0].clone()
+    target = torch.tensor(np.tile(home, (4, 1)), dtype=torch.float32, device=DEV)
+    target[:, 0] += 0.05
+    b.step(target, torch.zeros(4, 3, device=DEV), 5, KP, 0.0)
+    before = b.state()[0]
+    mask = torch.tensor([True, False, False, False], device=DEV)
+    b.reset(mask, torch.tensor(np.tile(home, (4, 1)), dtype=torch.float32, device=DEV),
+            torch.zeros(4, 6, device=DEV))
+    after = b.state()[0]
+    torch.testing.assert_close(after[0], initial[0], rtol=0, atol=0)
+    torch.testing.assert_close(after[1:], before[1:], rtol=0, atol=0)
+    forces = b.contact_forces()
+    assert torch.isfinite(forces).all() and (forces[:, :, 2] >= 0).all()
+    forces.fill_(999)
+    assert not (b.contact_forces() == 999).all()
+    snap = b.state()[0]
+    snap.fill_(123)
+    assert not torch.equal(snap, b.state()[0])
+
+
+def test_cross_stream_step_is_ordered(models, home):
+    b = _batch(models["standing"], 4)
+    ref = _batch(models["standing"], 4)
+    for x in (b, ref):
+        _reset_home(x, home)
+    target = torch.tensor(np.tile(home, (4, 1)), dtype=torch.float32, device=DEV)
+    target[1, 0] += 0.03
+    forces = torch.zeros(4, 3, device=DEV)
+    forces[1, 0] = 0.02
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        t2, f2 = target.clone(), forces.clone()
+        b.step(t2, f2, 5, KP, 0.0)
+        del t2, f2
+    out = b.state()  # current stream: must see the side-stream step
+    ref.step(target, forces, 5, KP, 0.0)
+    for x, y in zip(out, ref.state()):
+        torch.testing.assert_close(x, y, rtol=0, atol=0)
+
+
+@pytest.mark.parametrize("fp64", [False, True])
+def test_batch_size_invariance_bit_exact(models, home, fp64):
+    dtype = torch.float64 if fp64 else torch.float32
+    rng = np.random.default_rng(2)
+    targets = home + rng.uniform(-0.2, 0.2, (37, 14))
+    single = _batch(models["selfc"], 1, fp64)
+    many = _batch(models["selfc"], 37, fp64)
+    _reset_home(single, home, dtype)
+    _reset_home(many, home, dtype)
+    t_many = torch.tensor(targets, dtype=dtype, device=DEV)
+    f_many = torch.zeros(37, 3, dtype=dtype, device=DEV)
+    t_one = t_many[21:22].contiguous()
+    f_one = f_many[21:22].contiguous()
+    for _ in range(20):
+        many.step(t_many, f_many, 1, KP, 0.0)
+        single.step(t_one, f_one, 1, KP, 0.0)
+    for one, batch in zip(single.state(), many.state()):
+        torch.testing.assert_close(one[0], batch[21], rtol=0, atol=0)
+
+
+def test_substep_chunking_bit_exact(models, home):
+    rng = np.random.default_rng(4)
+    targets = torch.tensor(home + rng.uniform(-0.2, 0.2, (16, 14)), dtype=torch.float32, device=DEV)
+    forces = torch.zeros(16, 3, device=DEV)
+    a, b = _batch(models["standing"], 16), _batch(models["standing"], 16)
+    _reset_home(a, home)
+    _reset_home(b, home)
+    a.step(targets, forces, 12, KP, 0.0)
+    for _ in range(12):
+        b.step(targets, forces, 1, KP, 0.0)
+    torch.testing.assert_close(a.state()[0], b.state()[0], rtol=0, atol=0)
+    torch.testing.assert_close(a.state()[1], b.state()[1], rtol=0, atol=0)
+
+
+def test_reference_method_matches_fresh_batch(models, home):
+    """`reference()` advances one env from the model file's initial state."""
+    b = _batch(models["standing"], 3, fp64=True)
+    target = torch.tensor(home, dtype=torch.float64)
+    rb, rj, rd = b.reference(target, torch.zeros(3, dtype=torch.float64), 4, KP, 0.0)
+    fresh = _batch(models["standing"], 1, fp64=True)  # initialised to the file state
+    fresh.step(target[None].to(DEV), torch.zeros(1, 3, dtype=torch.float64, device=DEV), 4, KP, 0.0)
+    fb, fj, fd = (t[0].cpu() for t in fresh.state())
+    torch.testing.assert_close(rb, fb, rtol=0, atol=0)
+    torch.testing.assert_close(rj, fj, rtol=0, atol=0)
+    with pytest.raises(RuntimeError):
+        b.reference(target.float(), torch.zeros(3, dtype=torch.float64), 1, KP, 0.0)
+
+
+def test_pendulum_fixture_generic_model(models):
+    """The reference's own 2-body fixture (tests/fixtures/pendulum.duck)."""
+    b = CudaBatch(models["pendulum"], 3, 0.001, 100, 0, True)
+    assert b.num_bodies == 2 and b.num_joints == 1
+    b.step(torch.zeros(3, 1, dtype=torch.float64, device=DEV),
+           torch.zeros(3, 3, dtype=torch.float64, device=DEV), 50, 0.0, 0.0)
+    bodies, joints, diag = b.state()
+    assert torch.isfinite(bodies).all() and not diag[:, 5].any()
+    torch.testing.assert_close(bodies[0], bodies[2], rtol=0, atol=0)

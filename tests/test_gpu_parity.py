@@ -1,0 +1,238 @@
+"""HIP AVBD step versus the CPU oracle on identical seeded states.
+
+Gates (per the parity contract of this path):
+* contact-pair sets and colouring bit-exact on identical input states;
+* float64 trajectories equal to the oracle's to rounding (1e-9 m/rad over
+  dozens of steps) -- this pins every code path of the kernel;
+* float32 body poses within 1e-5 m/rad after one step and 1e-3 after 100
+  steps of the fixed HOME pose; joint torques within 1e-4 relative.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from duck_gym_amd import CudaBatch
+from oracle.oracle import Oracle
+from parity_support import compare_env, oracle_envs, oracle_state, seed_batch
+
+pytestmark = pytest.mark.gpu
+DT, ITER, KP = 0.005, 10, 8.0
+DEV = "cuda:0"
+
+
+def _run_pair(model, targets, steps, fp64, limit=0.0, forces=None, root=None, substeps=1):
+    """Reset GPU and oracle envs to the same seeded state, then step both."""
+    E = len(targets)
+    dtype = torch.float64 if fp64 else torch.float32
+    batch = CudaBatch(model, E, DT, ITER, 0, fp64)
+    oracles = oracle_envs(model, E, DT, ITER, fp64)
+    q0 = targets[:, :] if root is None else targets
+    for o, q in zip(oracles, q0):
+        o.reset(q, np.zeros(6) if root is None else root)
+    seed_batch(batch, oracles)
+    forces = np.zeros((E, 3)) if forces is None else forces
+    tg = torch.tensor(targets, dtype=dtype, device=DEV)
+    fg = torch.tensor(forces, dtype=dtype, device=DEV)
+    codec = batch.codec()
+    history = []
+    for step in range(steps):
+        batch.step(tg, fg, substeps, KP, limit)
+        for o, t, f in zip(oracles, targets, forces):
+            o.step(t, f, substeps, KP, limit)
+        raw = batch.export_state().cpu().numpy()
+        history.append([(codec.decode(raw[e]), oracle_state(o)) for e, o in enumerate(oracles)])
+    return batch, oracles, history
+
+
+def _legs_together(home, rng, n):
+    targets = home + rng.uniform(-0.3, 0.3, (n, 14))
+    targets[:, 1] -= 0.4  # left hip roll inward
+    targets[:, 10] += 0.4  # right hip roll inward
+    targets[:, 0] += 0.3
+    targets[:, 9] -= 0.3
+    return targets
+
+
+@pytest.mark.parametrize("name", ["standing", "friction", "selfc"])
+def test_fp64_trajectory_matches_oracle(models, home, name):
+    """Ground and body-body contact (MPR, fresh colours), PD drive with a
+    torque limit, active hinge limits, damping, dry friction: the float64
+    kernel follows the oracle to rounding over 40 steps."""
+    rng = np.random.default_rng(7)
+    targets = home + rng.uniform(-0.3, 0.3, (6, 14))
+    if name == "selfc":
+        targets = _legs_together(home, rng, 6)  # drives hip rolls past their limits
+    _, _, history = _run_pair(models[name], targets, 40, True, limit=0.5)
+    worst = 0.0
+    for step, envs in enumerate(history):
+        for e, (gpu, ref) in enumerate(envs):
+            d = compare_env(gpu, ref, 1e-9, f"{name} step {step + 1} env {e}")
+            worst = max(worst, d["x"], d["q"])
+    print(f"{name}: worst fp64 pose difference over 40 steps = {worst:.3e}")
+
+
+def test_fp64_self_contact_single_iteration_matches_oracle(models, home):
+    """Body-body contacts with one AVBD iteration per step and the state
+    re-seeded from the oracle before every step: each single body sweep
+    agrees to 1e-9 in float64."""
+    rng = np.random.default_rng(7)
+    E = 6
+    targets = _legs_together(home, rng, E)
+    batch = CudaBatch(models["selfc"], E, DT, 1, 0, True)
+    oracles = oracle_envs(models["selfc"], E, DT, 1, True)
+    for o, q in zip(oracles, targets):
+        o.reset(q)
+    codec = batch.codec()
+    tg = torch.tensor(targets, device=DEV)
+    fg = torch.zeros(E, 3, dtype=torch.float64, device=DEV)
+    contacts = 0
+    worst = 0.0
+    for step in range(40):
+        seed_batch(batch, oracles)
+        batch.step(tg, fg, 1, KP, 0.5)
+        for o, t in zip(oracles, targets):
+            o.step(t, None, 1, KP, 0.5)
+        raw = batch.export_state().cpu().numpy()
+        for e, o in enumerate(oracles):
+            gpu, ref = codec.decode(raw[e]), oracle_state(o)
+            d = compare_env(gpu, ref, 1e-9, f"step {step + 1} env {e}")
+            worst = max(worst, d["x"], d["q"])
+            contacts += len(ref["sc"])
+    assert contacts > 0, "the scenario produced no body-body contacts"
+    print(f"self contact: {contacts} body-body contacts, worst pose difference {worst:.3e}")
+
+
+def test_fp32_home_pose_tolerances(models, home):
+    targets = np.tile(home, (4, 1))
+    for fp64_oracle in (False, True):
+        batch = CudaBatch(models["standing"], 4, DT, ITER, 0, False)
+        oracles = oracle_envs(models["standing"], 4, DT, ITER, fp64_oracle)
+        for o in oracles:
+            o.reset(home)
+        seed_batch(batch, oracles)
+        tg = torch.tensor(targets, dtype=torch.float32, device=DEV)
+        fg = torch.zeros(4, 3, device=DEV)
+        for step in range(1, 101):
+            batch.step(tg, fg, 1, KP, 0.0)
+            for o in oracles:
+                o.step(home, None, 1, KP, 0.0)
+            if step in (1, 100):
+                b, j, d = (t.cpu().double().numpy() for t in batch.state())
+                tol = 1e-5 if step == 1 else 1e-3
+                for e, o in enumerate(oracles):
+                    ob, oj, od = o.snapshot()
+                    assert np.abs(b[e, :, :3] - ob[:, :3]).max() < tol
+                    assert np.abs(b[e, :, 3:7] - ob[:, 3:7]).max() < tol
+                    assert np.abs(j[e, :, 0] - oj[:, 0]).max() < tol
+                loads = batch.generalized_loads(torch.zeros(4, 3, device=DEV)).cpu().double().numpy()
+                for e, o in enumerate(oracles):
+                    ref = o.generalized_loads()
+                    # applied joint torque: 1e-4 relative (absolute below 1e-4 N m)
+                    err = np.abs(loads[e, :, 2] - ref[:, 2])
+                    assert np.all(err <= 1e-4 * np.maximum(1.0, np.abs(ref[:, 2]))), (step, err.max())
+
+
+@pytest.mark.parametrize("name", ["standing", "selfc"])
+def test_contact_sets_and_colours_bit_exact_on_identical_states(models, home, name):
+    """Seed the HIP batch with oracle states mid-trajectory, step once, and
+    require identical compacted contact lists and colours."""
+    rng = np.random.default_rng(11)
+    E = 8
+    oracles = oracle_envs(models[name], E, DT, ITER, False)
+    targets = home + rng.uniform(-0.35, 0.35, (E, 14))
+    if name == "selfc":
+        targets[:, 1] -= 0.45
+        targets[:, 10] += 0.45
+    for e, o in enumerate(oracles):
+        o.reset(home, [0, 0, 0.002 * e, 0.05 * rng.standard_normal(), 0.05 * rng.standard_normal(), 0])
+    batch = CudaBatch(models[name], E, DT, ITER, 0, False)
+    codec = batch.codec()
+    tg = torch.tensor(targets, dtype=torch.float32, device=DEV)
+    fg = torch.zeros(E, 3, device=DEV)
+    checked = 0
+    for round_ in range(12):
+        for _ in range(5):
+            for o, t in zip(oracles, targets):
+                o.step(t, None, 1, KP, 0.0)
+        seed_batch(batch, oracles)
+        batch.step(tg, fg, 1, KP, 0.0)
+        for o, t in zip(oracles, targets):
+            o.step(t, None, 1, KP, 0.0)
+        raw = batch.export_state().cpu().numpy()
+        for e, o in enumerate(oracles):
+            compare_env(codec.decode(raw[e]), oracle_state(o), 1e-5, f"round {round_} env {e}")
+            checked += 1
+    assert checked == 12 * E
+
+
+def test_motor_channels_fp64(models, home):
+    rng = np.random.default_rng(3)
+    E = 4
+    batch = CudaBatch(models["friction"], E, DT, ITER, 0, True)
+    oracles = oracle_envs(models["friction"], E, DT, ITER, True)
+    for o in oracles:
+        o.reset(home)
+    seed_batch(batch, oracles)
+    codec = batch.codec()
+    for step in range(30):
+        motor = np.stack([rng.uniform(-0.2, 0.2, (E, 14)), rng.uniform(0, 0.05, (E, 14)),
+                          rng.uniform(0, 0.3, (E, 14))], -1)
+        batch.step_motor(torch.tensor(motor, device=DEV), torch.zeros(E, 3, dtype=torch.float64, device=DEV))
+        for o, m in zip(oracles, motor):
+            o.set_motor(m)
+            o.advance(1)
+        raw = batch.export_state().cpu().numpy()
+        for e, o in enumerate(oracles):
+            compare_env(codec.decode(raw[e]), oracle_state(o), 1e-9, f"motor step {step} env {e}")
+
+
+def test_queries_fp64(models, home):
+    """contact_forces / self_contact_stats / contact_counts /
+    generalized_loads / state on identical (seeded) states."""
+    rng = np.random.default_rng(5)
+    E = 4
+    targets = _legs_together(home, rng, E)
+    batch = CudaBatch(models["selfc"], E, DT, ITER, 0, True)
+    oracles = oracle_envs(models["selfc"], E, DT, ITER, True)
+    for o, t in zip(oracles, targets):
+        o.reset(t)
+        for _ in range(25):
+            o.step(t, None, 1, KP, 0.5)
+    seed_batch(batch, oracles)
+    assert sum(o.contact_counts()[1] for o in oracles) > 0, "no body-body contacts to query"
+    offset = rng.uniform(-0.01, 0.01, (E, 3))
+    loads = batch.generalized_loads(torch.tensor(offset, device=DEV)).cpu().numpy()
+    forces = batch.contact_forces().cpu().numpy()
+    ground = batch.contact_forces(True).cpu().numpy()
+    stats = batch.self_contact_stats().cpu().numpy()
+    counts = batch.contact_counts().cpu().numpy()
+    b, j, d = (t.cpu().numpy() for t in batch.state())
+    for e, o in enumerate(oracles):
+        np.testing.assert_allclose(loads[e], o.generalized_loads(offset[e]), rtol=1e-10, atol=1e-12)
+        np.testing.assert_allclose(forces[e], o.contact_forces(), rtol=1e-12, atol=1e-12)
+        np.testing.assert_allclose(ground[e], o.contact_forces(True), rtol=1e-12, atol=1e-12)
+        np.testing.assert_allclose(stats[e], o.self_contact_stats(), rtol=1e-10, atol=1e-14)
+        np.testing.assert_array_equal(counts[e], o.contact_counts())
+        ob, oj, od = o.snapshot()
+        np.testing.assert_array_equal(b[e], ob)
+        np.testing.assert_allclose(j[e], oj, rtol=0, atol=1e-14)
+        np.testing.assert_allclose(d[e], od, rtol=0, atol=0)
+
+
+def test_reset_matches_oracle_fp64(models, home):
+    rng = np.random.default_rng(9)
+    E = 5
+    q = home + rng.uniform(-0.2, 0.2, (E, 14))
+    root = np.concatenate([rng.uniform(-0.01, 0.01, (E, 3)), rng.uniform(-0.3, 0.3, (E, 3))], 1)
+    batch = CudaBatch(models["standing"], E, DT, ITER, 0, True)
+    batch.reset(torch.ones(E, dtype=torch.bool, device=DEV), torch.tensor(q, device=DEV),
+                torch.tensor(root, device=DEV))
+    b, j, _ = (t.cpu().numpy() for t in batch.state())
+    for e in range(E):
+        o = Oracle(models["standing"], DT, ITER, True)
+        o.reset(q[e], root[e])
+        ob, oj, _ = o.snapshot()
+        np.testing.assert_allclose(b[e], ob, rtol=0, atol=1e-13)
+        np.testing.assert_allclose(j[e], oj, rtol=0, atol=1e-12)
+        np.testing.assert_allclose(j[e, :, 0], q[e], rtol=0, atol=1e-12)
