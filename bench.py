@@ -1,0 +1,215 @@
+"""Physics env-steps/s of the batched AVBD env step on one MI355X.
+
+Workload: the MicroDuck-like biped (16 bodies, 14 hinges, kp 8, kd 0.2,
+ground friction 0.8), 4096 environments in float32, held at the fixed HOME
+pose with zero action, dt = 1/200 s, 10 AVBD iterations per step.  One
+"step" is one physics step of every environment: one launch of the fused
+step kernel (`CudaBatch.step(target, forces, 1, kp, 0)`), inputs resident in
+HBM.  W untimed warm-up steps follow a reset, then exactly K steps are timed
+between device synchronisations; the kernel's own duration is measured with
+HIP events on the launch stream.
+
+The JSON line also carries
+  roofline      algorithmic HBM bytes per launch of the step kernel (the
+                persistent state read and written once per step plus the
+                controls read) over its measured duration, against 8 TB/s;
+                `traffic` is the measured HBM bytes per launch from
+                rocprofv3 FETCH_SIZE/WRITE_SIZE when recorded in profiles/
+  cpu_baseline  the reference's own CPU build of the same solver core
+                (src/cuda/kernel.cuh via src/cuda/cpu_bindings.cpp, compiled
+                in place into oracle/_ref) on a bounded sample, all threads
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import sys
+import tempfile
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "physics env-steps/s at 4096 envs on 1 MI355X; achieved HBM GB/s vs peak"
+HBM_PEAK_GBS = 8000.0
+ENVS, DT, ITERATIONS, KP = 4096, 0.005, 10, 8.0
+
+
+def state_bytes_per_env(contacts, bodies=15, joints=14):
+    """Minimal persistent state of one env (float32): bodies (x, q, v, w),
+    joint multipliers/penalties (lambda 7, penalty 7, lambdaF, penaltyF),
+    the contact warm-start cache (56 B per live contact) and count/flag."""
+    return bodies * 13 * 4 + joints * 16 * 4 + 56 * contacts + 8
+
+
+def algorithmic_bytes_per_launch(envs, contacts, model_bytes):
+    """State read + written once, targets [J] + forces [3] read, model once."""
+    per_env = 2 * state_bytes_per_env(contacts) + (14 + 3) * 4
+    return envs * per_env + model_bytes
+
+
+def measured_traffic():
+    """HBM bytes per launch recorded from rocprofv3 counters, if present."""
+    path = ROOT / "profiles" / "advance_kernel_microduck_4096_counters.md"
+    if not path.exists():
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", path.read_text())
+    return float(m.group(1)) if m else None
+
+
+def cpu_baseline(model, home, seconds_budget=12.0):
+    """Time the reference CPU core (oracle/_ref/_duck_reference.CpuBatch32)
+    on a bounded sample of the same workload; fall back to this repository's
+    oracle ("port") when the reference build is absent."""
+    import numpy as np
+
+    threads = max(1, min(16, os.cpu_count() or 1))
+    envs = 64 * threads
+    sys.path.insert(0, str(ROOT / "oracle" / "_ref"))
+    try:
+        import _duck_reference  # noqa: F401
+
+        batch = _duck_reference.CpuBatch32(str(model), envs, DT, ITERATIONS, threads)
+        q = np.tile(home, (envs, 1)).astype(np.float32)
+        batch.reset(np.ones(envs, bool), q, np.zeros((envs, 6), np.float32))
+        forces = np.zeros((envs, 3), np.float32)
+        batch.step(q, forces, 1, KP, 1e9)  # warm
+        steps, start = 0, time.perf_counter()
+        while time.perf_counter() - start < seconds_budget:
+            batch.step(q, forces, 1, KP, 1e9)  # limit 1e9 = uncapped for PD torques
+            steps += 1
+        elapsed = time.perf_counter() - start
+        kind, cores = "reference", threads
+        sample = (f"{envs} envs x {steps} steps of src/cuda/kernel.cuh's CPU build "
+                  f"(CpuBatch32, {threads} threads), same model/HOME/dt/iterations")
+    except ImportError:
+        from concurrent.futures import ThreadPoolExecutor
+
+        from oracle.oracle import Oracle
+
+        envs = 4 * threads
+        oracles = [Oracle(model, DT, ITERATIONS, False) for _ in range(envs)]
+        for o in oracles:
+            o.reset(home)
+
+        def run(o, n):
+            for _ in range(n):
+                o.step(home, None, 1, KP, 0.0)
+
+        steps, start = 0, time.perf_counter()
+        with ThreadPoolExecutor(threads) as pool:
+            while time.perf_counter() - start < seconds_budget:
+                list(pool.map(lambda o: run(o, 5), oracles))
+                steps += 5
+        elapsed = time.perf_counter() - start
+        kind, cores = "port", threads
+        sample = f"{envs} envs x {steps} steps of the CPU oracle, {threads} threads"
+    return {"value": envs * steps / elapsed, "unit": "env-steps/s", "cores": cores,
+            "kind": kind, "sample": sample}
+
+
+def main():
+    p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=1000)
+    p.add_argument("--warmup", type=int, default=100)
+    p.add_argument("--envs", type=int, default=ENVS)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    args = p.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one MI355X: environments shard across GPUs with no "
+              "exchange, and this build runs on a single-GPU box (use --gpus 1).",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    from duck_gym_amd import CudaBatch
+    from duck_gym_amd.microduck import HOME, JOINT_NAMES, write_model
+
+    home = np.array([HOME[n] for n in JOINT_NAMES])
+    tmp = tempfile.TemporaryDirectory()
+    model = write_model(Path(tmp.name) / "standing")
+    E = args.envs
+    dev = torch.device("cuda:0")
+    batch = CudaBatch(model, E, DT, ITERATIONS, 0, False)
+    target = torch.tensor(np.tile(home, (E, 1)), dtype=torch.float32, device=dev)
+    forces = torch.zeros(E, 3, dtype=torch.float32, device=dev)
+    batch.reset(torch.ones(E, dtype=torch.bool, device=dev), target.clone(),
+                torch.zeros(E, 6, device=dev))
+    for _ in range(args.warmup):
+        batch.step(target, forces, 1, KP, 0.0)
+    torch.cuda.synchronize()
+
+    stream = torch.cuda.current_stream()
+    begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    begin.record(stream)
+    for _ in range(args.steps):
+        batch.step(target, forces, 1, KP, 0.0)
+    end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    kernel_s = begin.elapsed_time(end) / 1000.0 / args.steps  # per launch
+
+    counts = batch.contact_counts()
+    _, _, diag = batch.state()
+    contacts = float(counts[:, 0].float().mean())
+    failed = int((diag[:, 5] != 0).sum())
+    finite = bool(torch.isfinite(batch.state()[0]).all())
+    if failed or not finite:
+        raise RuntimeError(f"invalid benchmark state: {failed} failed envs, finite={finite}")
+
+    value = E * args.steps / wall
+    model_bytes = 4 * 4096  # read-only model tables streamed per launch (upper bound)
+    algo = algorithmic_bytes_per_launch(E, round(contacts), model_bytes)
+    achieved = algo / kernel_s / 1e9
+    traffic = measured_traffic() if E == ENVS else None
+    line = {
+        "metric": METRIC,
+        "value": value,
+        "unit": "env-steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": wall / args.steps * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic",
+        "config": {
+            "workload": "MicroDuck-like biped (16 bodies, 14 hinges), fixed HOME pose, zero "
+                        "action, ground contact",
+            "envs": E,
+            "iterations": ITERATIONS,
+            "dt_s": DT,
+            "kp": KP,
+            "launch": "one physics step per kernel launch",
+            "live_ground_contacts_per_env": contacts,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS,
+            "traffic": traffic,
+            "kernel_ms": kernel_s * 1e3,
+            "algorithmic_bytes_per_launch": algo,
+        },
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(model, home)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()
