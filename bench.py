@@ -119,7 +119,21 @@ def main():
     p.add_argument("--warmup", type=int, default=100)
     p.add_argument("--envs", type=int, default=ENVS)
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                   help="only run a plain device copy of MIB MiB (three times): the "
+                        "reference dispatch for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE")
     args = p.parse_args()
+    if args.copy_calibration:
+        import torch
+
+        n = args.copy_calibration * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_read": n * 4, "copy_bytes_written": n * 4}), flush=True)
+        return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures one MI355X: environments shard across GPUs with no "
