@@ -1,0 +1,219 @@
+// Control-step kernels of the tensor VecEnv (python/duck_gym/tensor_env.py):
+// action clamping and servo targets, and the observation, reward, failure,
+// timeout and episode bookkeeping that the reference assembles from ~40 torch
+// ops per control step (tensor_env.py:178-219, 221-391).  One lane per
+// environment; the root pose and joint state are read straight from the HBM
+// state blob, so no [E,B,13] snapshot is materialised.
+#pragma once
+#include "../../include/duck_hip.h"
+#include "avbd_queries.hpp"
+
+namespace duckhip {
+
+enum TaskMode { kTaskStep = 0, kTaskReset = 1 };
+
+DUCK_HD float mexp(float x) { return expf(x); }
+DUCK_HD double mexp(double x) { return exp(x); }
+
+// Observation widths (tensor_env.py:238-258 and the 48-wide rollout layout).
+DUCK_HD int taskObsDim(const DuckTask &t, int nj) {
+  if (t.kind == DUCK_TASK_STANDING)
+    return 10 + 3 * nj;
+  if (t.kind == DUCK_TASK_LOCOMOTION)
+    return 16 + 3 * nj + (t.velocity_filter ? 2 : 0);
+  return 6 + 3 * nj;
+}
+
+// a = clamp(actions, -1, 1); target = clamp(ref + scale a, lower, upper)
+// with ref = HOME when `reference` is null (tensor_env.py:260-277, 279-285).
+template <class R>
+__global__ void taskTargetsKernel(DuckTask t, int count, int nj, const R *actions,
+                                  const R *reference, R *clamped, R *target) {
+  int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= count * nj)
+    return;
+  int j = i % nj;
+  R a = actions[i];
+  // torch.clamp propagates NaN; so do these comparisons (NaN fails both).
+  a = a < R(-1) ? R(-1) : (a > R(1) ? R(1) : a);
+  R ref = reference ? reference[i] : R(t.home[j]);
+  R v = ref + R(t.action_scale) * a;
+  R lo = R(t.lower[j]), hi = R(t.upper[j]);
+  v = v < lo ? lo : (v > hi ? hi : v);
+  clamped[i] = a;
+  target[i] = v;
+}
+
+struct TaskBuffers {
+  const unsigned char *mask; // reset mode: envs whose bookkeeping restarts
+  void *action;              // [E,J] R: this step's clamped action (step) / current actions
+  void *lastAction;          // [E,J] R: previous action; step mode overwrites it with action
+  const void *commands;      // [E,2] R (locomotion, rollout)
+  long long *episode;        // [E]
+  void *filtered;            // [E,2] R (locomotion velocity filter)
+  float *returns;            // [E]
+  void *forces;              // [E,3] R (reset mode zeroes masked rows), may be null
+  float *obs;                // [E,D]
+  float *reward;             // [E]
+  unsigned char *failed, *timeout, *done; // [E]
+  void *diag;                // [E,6] R, may be null
+};
+
+template <class R, int B, int J, int CG, int CS>
+__global__ void taskKernel(DuckTask t, int mode, const DeviceModel<R> *model,
+                           unsigned char *states, long long blobBytes, int count, TaskBuffers io) {
+  int e = blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= count)
+    return;
+  const DeviceModel<R> &M = *model;
+  auto &s = blobAt<EnvState<R, B, J, CG, CS>>(states, blobBytes, e);
+  StateView<R, B, J, CG, CS> view{M, s};
+  const int nj = M.nj;
+  R *act = static_cast<R *>(io.action) + size_t(e) * nj;
+  R *last = static_cast<R *>(io.lastAction) + size_t(e) * nj;
+  R *filt = io.filtered ? static_cast<R *>(io.filtered) + size_t(e) * 2 : nullptr;
+  const R *cmd = io.commands ? static_cast<const R *>(io.commands) + size_t(e) * 2 : nullptr;
+
+  if (mode == kTaskReset && io.mask && io.mask[e]) {
+    // tensor_env.py:199-203: restart the episode bookkeeping of reset envs.
+    for (int j = 0; j < nj; ++j)
+      act[j] = R(0);
+    if (filt)
+      filt[0] = filt[1] = R(0);
+    if (io.forces)
+      for (int k = 0; k < 3; ++k)
+        static_cast<R *>(io.forces)[size_t(e) * 3 + k] = R(0);
+    io.episode[e] = 0;
+    io.returns[e] = 0.f;
+  }
+
+  // Root frame q = q_body1 (x) conj(root_iquat) (tensor_env.py:140-142, 222).
+  const int root = 1;
+  Q4<R> qb = view.Q(root);
+  Q4<R> iq{R(t.iquat[0]), -R(t.iquat[1]), -R(t.iquat[2]), -R(t.iquat[3])};
+  Q4<R> q = qb * iq;
+  V3<R> g = rotateInv(q, V3<R>{R(0), R(0), R(-1)});
+  V3<R> vel{s.v[0][root], s.v[1][root], s.v[2][root]};
+  V3<R> v = rotateInv(q, vel);
+  V3<R> w = rotateInv(q, view.W(root));
+  R yawC = R(1) - R(2) * (q.y * q.y + q.z * q.z);
+  R yawS = R(2) * (q.w * q.z + q.x * q.y);
+  R height = s.x[2][root] - R(t.root_height);
+
+  R reward = 0;
+  bool failed = false, timeout = false;
+  if (mode == kTaskStep) {
+    // Failure (tensor_env.py:294-301; the rollout task fails on a fall).
+    bool finite = true;
+    for (int b = 0; b < M.nb; ++b) {
+      for (int k = 0; k < 3; ++k)
+        finite = finite && mfinite(s.x[k][b]) && mfinite(s.v[k][b]) && mfinite(s.w[k][b]);
+      for (int k = 0; k < 4; ++k)
+        finite = finite && mfinite(s.q[k][b]);
+    }
+    const R cosHalf = R(cosf(0.5f)); // torch.cos of a float32 0.5
+    if (t.kind == DUCK_TASK_ROLLOUT)
+      failed = s.x[2][root] < R(t.fall_height);
+    else
+      failed = g.z > -cosHalf || mabs(height) > R(0.04) || s.diag[kJointError] > R(0.005) ||
+               s.diag[kPenetration] > R(0.005);
+    failed = failed || s.failed > 0 || !finite;
+
+    R pose = 0, act2 = 0, dact2 = 0;
+    for (int j = 0; j < nj; ++j) {
+      R d = view.angle(j) - R(t.home[j]);
+      pose += d * d;
+      act2 += act[j] * act[j];
+      R da = act[j] - last[j];
+      dact2 += da * da;
+    }
+    R tilt = g.x * g.x + g.y * g.y;
+    R w2 = dot(w, w);
+    if (t.kind == DUCK_TASK_STANDING) {
+      // tensor_env.py:302-310
+      reward = R(1.5) * mexp(R(-20) * tilt) + mexp(R(-2000) * height * height) +
+               R(0.5) * mexp(R(-10) * dot(v, v)) - R(0.02) * w2 - R(0.05) * pose -
+               R(0.01) * act2 - R(0.02) * dact2;
+    } else {
+      // tensor_env.py:311-327: world-frame COM velocity against the command.
+      R vx = vel.x, vy = vel.y;
+      if (t.kind == DUCK_TASK_LOCOMOTION && t.velocity_filter) {
+        R alpha = R(t.velocity_alpha);
+        filt[0] = (R(1) - alpha) * filt[0] + alpha * vx;
+        filt[1] = (R(1) - alpha) * filt[1] + alpha * vy;
+        vx = filt[0];
+        vy = filt[1];
+      }
+      R ex = vx - cmd[0], ey = vy - cmd[1];
+      R error = ex * ex + ey * ey;
+      R sigma = R(t.tracking_sigma);
+      reward = R(1) * mexp(R(-20) * tilt) + mexp(R(-2000) * height * height) +
+               R(t.tracking_weight) * mexp(-error / (sigma * sigma)) - R(0.1) * w2 -
+               R(t.heading_weight) * (R(1) - yawC) - R(0.02) * act2 - R(0.03) * dact2;
+    }
+    reward = (failed ? R(-2) : reward) * R(t.control_dt);
+    long long ep = io.episode[e] + 1;
+    io.episode[e] = ep;
+    io.returns[e] += float(reward);
+    timeout = ep >= t.max_episode_length && !failed;
+    io.reward[e] = float(reward);
+    io.failed[e] = failed;
+    io.timeout[e] = timeout;
+    io.done[e] = failed || timeout;
+    for (int j = 0; j < nj; ++j)
+      last[j] = act[j];
+    if (io.diag) {
+      R *d = static_cast<R *>(io.diag) + size_t(e) * 6;
+      d[0] = s.diag[kJointError];
+      d[1] = s.diag[kPenetration];
+      d[2] = s.diag[kContacts];
+      d[3] = s.diag[kConverged];
+      d[4] = s.diag[kAxisError];
+      d[5] = R(s.failed);
+    }
+  }
+
+  // Observation (tensor_env.py:238-258), cast to float32.
+  float *o = io.obs + size_t(e) * taskObsDim(t, nj);
+  int k = 0;
+  o[k++] = float(g.x);
+  o[k++] = float(g.y);
+  o[k++] = float(g.z);
+  if (t.kind != DUCK_TASK_ROLLOUT) {
+    o[k++] = float(v.x);
+    o[k++] = float(v.y);
+    o[k++] = float(v.z);
+  }
+  o[k++] = float(w.x);
+  o[k++] = float(w.y);
+  o[k++] = float(w.z);
+  if (t.kind != DUCK_TASK_ROLLOUT)
+    o[k++] = float(height);
+  for (int j = 0; j < nj; ++j)
+    o[k + j] = float(view.angle(j) - R(t.home[j]));
+  k += nj;
+  for (int j = 0; j < nj; ++j) {
+    R rate = dot(view.W(M.jb[j]) - view.W(M.ja[j]), rotate(view.Q(M.ja[j]), view.mv(M.axisA, j)));
+    o[k + j] = float(R(0.1) * rate);
+  }
+  k += nj;
+  for (int j = 0; j < nj; ++j)
+    o[k + j] = float(act[j]);
+  k += nj;
+  if (t.kind == DUCK_TASK_LOCOMOTION) {
+    // (episode * control_dt) * (2 pi / period), the factor formed in double.
+    R phase = R(io.episode[e]) * R(t.control_dt) * R(2 * 3.14159265358979323846 / t.gait_period);
+    o[k++] = float(cmd[0]);
+    o[k++] = float(cmd[1]);
+    o[k++] = float(yawC);
+    o[k++] = float(yawS);
+    o[k++] = float(msin(phase));
+    o[k++] = float(mcos(phase));
+    if (t.velocity_filter) {
+      o[k++] = float(filt[0]);
+      o[k++] = float(filt[1]);
+    }
+  }
+}
+
+} // namespace duckhip

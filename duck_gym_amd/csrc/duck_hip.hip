@@ -1,7 +1,7 @@
 // C ABI of the gfx950 AVBD batch (include/duck_hip.h): model upload, state
 // ownership, stream ordering and kernel dispatch.
 #include "../../include/duck_hip.h"
-#include "avbd_queries.hpp"
+#include "avbd_task.hpp"
 #include "duck_model.hpp"
 
 #include <cstring>
@@ -159,6 +159,9 @@ struct BatchBase {
   virtual void layout(long long *out) const = 0;
   virtual void exportState(void *, hipStream_t) = 0;
   virtual void importState(const void *, hipStream_t) = 0;
+  virtual void taskTargets(const DuckTask &, const void *, const void *, void *, void *,
+                           hipStream_t) = 0;
+  virtual void task(const DuckTask &, int, const TaskBuffers &, hipStream_t) = 0;
 };
 
 template <class R, int B, int J, int CG, int CS, int L> class Batch final : public BatchBase {
@@ -352,6 +355,24 @@ public:
     hipCheck(hipFree(state), "hipFree");
     hipCheck(hipFree(buf), "hipFree");
   }
+  void taskTargets(const DuckTask &t, const void *actions, const void *reference, void *clamped,
+                   void *target, hipStream_t s) override {
+    DeviceGuard guard(device);
+    require(actions && clamped && target, "task targets: null buffer");
+    const int nj = host.joints.size();
+    taskTargetsKernel<R><<<blocks64(count * nj), 64, 0, s>>>(
+        t, count, nj, static_cast<const R *>(actions), static_cast<const R *>(reference),
+        static_cast<R *>(clamped), static_cast<R *>(target));
+    launched("taskTargetsKernel");
+  }
+  void task(const DuckTask &t, int mode, const TaskBuffers &io, hipStream_t s) override {
+    DeviceGuard guard(device);
+    wait(s);
+    taskKernel<R, B, J, CG, CS><<<blocks64(count), 64, 0, s>>>(t, mode, dModel, dStates, blobBytes,
+                                                                count, io);
+    launched("taskKernel");
+    record(s);
+  }
   void layout(long long *out) const override;
   void exportState(void *dst, hipStream_t s) override {
     DeviceGuard guard(device);
@@ -539,6 +560,65 @@ int duck_export_state(void *handle, void *dst, void *hip_stream) {
 }
 int duck_import_state(void *handle, const void *src, void *hip_stream) {
   return guarded([&] { as(handle)->importState(src, st(hip_stream)); });
+}
+static void checkTask(BatchBase *b, const DuckTask *t) {
+  require(t != nullptr, "null task");
+  require(t->kind == DUCK_TASK_STANDING || t->kind == DUCK_TASK_LOCOMOTION ||
+              t->kind == DUCK_TASK_ROLLOUT,
+          "Invalid task kind");
+  require(int(b->host.joints.size()) <= DUCK_MAX_JOINTS, "too many joints for a task");
+  require(std::isfinite(t->control_dt) && t->control_dt > 0 && std::isfinite(t->gait_period) &&
+              t->gait_period > 0 && std::isfinite(t->action_scale) && t->action_scale > 0,
+          "Invalid control configuration");
+  require(t->kind == DUCK_TASK_STANDING || (std::isfinite(t->tracking_sigma) && t->tracking_sigma > 0),
+          "tracking sigma must be positive");
+  require(b->host.bodies.size() >= 2, "task needs a root body (body 1)");
+}
+int duck_task_obs_dim(const DuckTask *task, int joints) {
+  if (!task || joints < 0 || joints > DUCK_MAX_JOINTS)
+    return -1;
+  return taskObsDim(*task, joints);
+}
+int duck_task_targets(void *handle, const DuckTask *task, const void *actions,
+                      const void *reference, void *clamped, void *target, void *hip_stream) {
+  return guarded([&] {
+    auto *b = as(handle);
+    checkTask(b, task);
+    b->taskTargets(*task, actions, reference, clamped, target, st(hip_stream));
+  });
+}
+int duck_task_step(void *handle, const DuckTask *task, const void *action, void *last_action,
+                   const void *commands, long long *episode, void *filtered, float *returns,
+                   float *obs, float *reward, unsigned char *failed, unsigned char *timeout,
+                   unsigned char *done, void *diag, void *hip_stream) {
+  return guarded([&] {
+    auto *b = as(handle);
+    checkTask(b, task);
+    require(action && last_action && episode && returns && obs && reward && failed && timeout &&
+                done,
+            "task step: null buffer");
+    require(task->kind == DUCK_TASK_STANDING || commands, "task step: commands required");
+    require(!(task->kind == DUCK_TASK_LOCOMOTION && task->velocity_filter) || filtered,
+            "task step: filtered velocity required");
+    TaskBuffers io{nullptr, const_cast<void *>(action), last_action, commands, episode,
+                   filtered, returns, nullptr, obs, reward, failed, timeout, done, diag};
+    b->task(*task, kTaskStep, io, st(hip_stream));
+  });
+}
+int duck_task_observe(void *handle, const DuckTask *task, const unsigned char *reset_mask,
+                      void *actions, const void *commands, long long *episode, void *filtered,
+                      float *returns, void *forces, float *obs, void *hip_stream) {
+  return guarded([&] {
+    auto *b = as(handle);
+    checkTask(b, task);
+    require(actions && episode && returns && obs, "task observe: null buffer");
+    require(task->kind != DUCK_TASK_LOCOMOTION || commands, "task observe: commands required");
+    require(!(task->kind == DUCK_TASK_LOCOMOTION && task->velocity_filter) || filtered,
+            "task observe: filtered velocity required");
+    TaskBuffers io{reset_mask, actions, actions, commands, episode, filtered, returns,
+                   forces, obs, nullptr, nullptr, nullptr, nullptr, nullptr};
+    b->task(*task, kTaskReset, io, st(hip_stream));
+  });
 }
 int duck_reference(void *handle, const void *target, const void *force, int substeps, double kp,
                    double limit, void *bodies, void *joints, void *diag) {

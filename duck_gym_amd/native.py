@@ -52,6 +52,10 @@ def library():
             "duck_export_state": (ip, [vp, vp, vp]),
             "duck_import_state": (ip, [vp, vp, vp]),
             "duck_last_error": (cp, []),
+            "duck_task_obs_dim": (ip, [ctypes.POINTER(DuckTask), ip]),
+            "duck_task_targets": (ip, [vp, ctypes.POINTER(DuckTask), vp, vp, vp, vp, vp]),
+            "duck_task_step": (ip, [vp, ctypes.POINTER(DuckTask)] + [vp] * 13),
+            "duck_task_observe": (ip, [vp, ctypes.POINTER(DuckTask)] + [vp] * 9),
         }
         for name, (res, args) in sig.items():
             fn = getattr(lib, name)
@@ -66,8 +70,27 @@ EXPORTED = (
     "duck_state_bytes", "duck_joint_name", "duck_reset", "duck_step", "duck_step_motor",
     "duck_state", "duck_contact_forces", "duck_self_contact_stats", "duck_contact_counts",
     "duck_generalized_loads", "duck_reference", "duck_state_layout", "duck_export_state",
-    "duck_import_state", "duck_last_error",
+    "duck_import_state", "duck_last_error", "duck_task_obs_dim", "duck_task_targets",
+    "duck_task_step", "duck_task_observe",
 )
+
+MAX_JOINTS = 32
+TASK_STANDING, TASK_LOCOMOTION, TASK_ROLLOUT = 0, 1, 2
+
+
+class DuckTask(ctypes.Structure):
+    """`DuckTask` of include/duck_hip.h: the constants of one tensor-env task."""
+
+    _fields_ = [
+        ("kind", ctypes.c_int), ("velocity_filter", ctypes.c_int),
+        ("home", ctypes.c_double * MAX_JOINTS), ("lower", ctypes.c_double * MAX_JOINTS),
+        ("upper", ctypes.c_double * MAX_JOINTS), ("iquat", ctypes.c_double * 4),
+        ("root_height", ctypes.c_double), ("action_scale", ctypes.c_double),
+        ("control_dt", ctypes.c_double), ("gait_period", ctypes.c_double),
+        ("tracking_weight", ctypes.c_double), ("heading_weight", ctypes.c_double),
+        ("tracking_sigma", ctypes.c_double), ("velocity_alpha", ctypes.c_double),
+        ("fall_height", ctypes.c_double), ("max_episode_length", ctypes.c_longlong),
+    ]
 
 
 def _raise(code, what):
@@ -234,6 +257,54 @@ class CudaBatch:
         if code:
             _raise(code, "reference")
         return b, j, d
+
+    # ---------------------------------------------- tensor-env control step
+    def _ptr(self, t, shape, dtype=None):
+        return None if t is None else self._check(t, shape, dtype)
+
+    def task_obs_dim(self, task):
+        return int(library().duck_task_obs_dim(ctypes.byref(task), self.num_joints))
+
+    def task_targets(self, task, actions, reference, clamped, target):
+        """clamped <- clamp(actions, -1, 1); target <- clamp(ref + scale a, lower, upper)."""
+        E, J = self.num_envs, self.num_joints
+        args = [self._check(actions, [E, J]), self._ptr(reference, [E, J]),
+                self._check(clamped, [E, J]), self._check(target, [E, J])]
+        with torch.cuda.device(self.device):
+            code = library().duck_task_targets(self._h, ctypes.byref(task), *args, self._stream())
+        if code:
+            _raise(code, "task_targets")
+
+    def task_step(self, task, action, last_action, commands, episode, filtered, returns, obs,
+                  reward, failed, timeout, done, diag):
+        """Failure, reward, counters and the observation after a physics step."""
+        E, J = self.num_envs, self.num_joints
+        f32, i64, u8 = torch.float32, torch.int64, torch.bool
+        args = [self._check(action, [E, J]), self._check(last_action, [E, J]),
+                self._ptr(commands, [E, 2]), self._check(episode, [E], i64),
+                self._ptr(filtered, [E, 2]), self._check(returns, [E], f32),
+                self._check(obs, [E, self.task_obs_dim(task)], f32),
+                self._check(reward, [E], f32), self._check(failed, [E], u8),
+                self._check(timeout, [E], u8), self._check(done, [E], u8),
+                self._ptr(diag, [E, 6])]
+        with torch.cuda.device(self.device):
+            code = library().duck_task_step(self._h, ctypes.byref(task), *args, self._stream())
+        if code:
+            _raise(code, "task_step")
+
+    def task_observe(self, task, reset_mask, actions, commands, episode, filtered, returns,
+                     forces, obs):
+        """Restart the bookkeeping of `reset_mask` envs, then observe every env."""
+        E, J = self.num_envs, self.num_joints
+        args = [self._ptr(reset_mask, [E], torch.bool), self._check(actions, [E, J]),
+                self._ptr(commands, [E, 2]), self._check(episode, [E], torch.int64),
+                self._ptr(filtered, [E, 2]), self._check(returns, [E], torch.float32),
+                self._ptr(forces, [E, 3]),
+                self._check(obs, [E, self.task_obs_dim(task)], torch.float32)]
+        with torch.cuda.device(self.device):
+            code = library().duck_task_observe(self._h, ctypes.byref(task), *args, self._stream())
+        if code:
+            _raise(code, "task_observe")
 
     # ------------------------------------------------ state introspection
     def state_layout(self):

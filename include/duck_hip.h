@@ -102,6 +102,57 @@ int duck_state_layout(void *handle, long long *out);
 int duck_export_state(void *handle, void *dst, void *hip_stream);
 int duck_import_state(void *handle, const void *src, void *hip_stream);
 
+/* ---- Control step of the tensor VecEnv (python/duck_gym/tensor_env.py) ----
+ * The reference assembles targets, observations, rewards and terminations
+ * from ~40 torch ops per control step (tensor_env.py:178-219, 221-391); here
+ * they are three kernels that read the HBM state directly. */
+#define DUCK_MAX_JOINTS 32
+enum {
+  DUCK_TASK_STANDING = 0,   /* tensor_env.py task="standing": 52-wide observation */
+  DUCK_TASK_LOCOMOTION = 1, /* task="locomotion": 58 (+2 with the velocity filter) */
+  DUCK_TASK_ROLLOUT = 2     /* 48-wide observation (gravity, w, q-HOME, 0.1 qdot, action),
+                               locomotion reward, failure = base height below fall_height */
+};
+typedef struct DuckTask {
+  int kind;            /* DUCK_TASK_* */
+  int velocity_filter; /* locomotion: velocity_filter_seconds > 0 */
+  double home[DUCK_MAX_JOINTS], lower[DUCK_MAX_JOINTS], upper[DUCK_MAX_JOINTS];
+  double iquat[4];     /* metadata root_iquat (w x y z); the root frame is q_body1 * conj(iquat) */
+  double root_height, action_scale, control_dt, gait_period;
+  double tracking_weight, heading_weight, tracking_sigma, velocity_alpha;
+  double fall_height;
+  long long max_episode_length;
+} DuckTask;
+
+/* Observation width of `task` for a batch with `joints` hinges. */
+int duck_task_obs_dim(const DuckTask *task, int joints);
+
+/* TensorEnv.step head (tensor_env.py:331-335, 260-277): a = clamp(actions,-1,1),
+ * target = clamp(ref + action_scale a, lower, upper); ref = HOME when
+ * `reference` is NULL (the gait reference otherwise).  [E,J] batch dtype. */
+int duck_task_targets(void *handle, const DuckTask *task, const void *actions,
+                      const void *reference, void *clamped, void *target, void *hip_stream);
+
+/* TensorEnv.step tail after the physics (tensor_env.py:345-391): failure,
+ * reward, returns, episode counters, timeouts, done, the observation of the
+ * new state and diag[E,6].  `action` [E,J] is this step's clamped action;
+ * `last_action` [E,J] holds the previous one and is overwritten with `action`.
+ * commands [E,2] (locomotion/rollout, else NULL), episode [E] int64, filtered
+ * [E,2] (velocity filter, else NULL), returns/obs/reward float32, failed /
+ * timeout / done [E] bytes. */
+int duck_task_step(void *handle, const DuckTask *task, const void *action, void *last_action,
+                   const void *commands, long long *episode, void *filtered, float *returns,
+                   float *obs, float *reward, unsigned char *failed, unsigned char *timeout,
+                   unsigned char *done, void *diag, void *hip_stream);
+
+/* TensorEnv.reset bookkeeping + get_observations (tensor_env.py:199-219, 259):
+ * for envs in `reset_mask` (may be NULL) zero the actions, filtered velocity,
+ * forces [E,3] (may be NULL), episode counter and return; then write the
+ * observation of every env. */
+int duck_task_observe(void *handle, const DuckTask *task, const unsigned char *reset_mask,
+                      void *actions, const void *commands, long long *episode, void *filtered,
+                      float *returns, void *forces, float *obs, void *hip_stream);
+
 const char *duck_last_error(void);
 
 #ifdef __cplusplus

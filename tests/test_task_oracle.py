@@ -1,0 +1,186 @@
+"""Pin the tensor-env oracle (oracle/task_oracle.py) against what does not
+depend on it: scipy's rotation algebra, and closed-form states whose every
+observation entry and reward term is known by hand (upright, pure tilt,
+pure yaw, known world velocities, single reward terms switched on one at a
+time), plus the failure and timeout thresholds of tensor_env.py:294-301,
+358-360."""
+
+import math
+
+import numpy as np
+import pytest
+from scipy.spatial.transform import Rotation
+
+from duck_gym_amd.microduck import HOME, JOINT_NAMES, model_text
+from oracle import task_oracle as T
+
+META = model_text()[1]
+J = 14
+HOME_V = np.array([HOME[n] for n in JOINT_NAMES])
+DT = 0.1
+
+
+def wxyz(rot):
+    x, y, z, w = rot.as_quat()
+    return np.array([w, x, y, z])
+
+
+def state(root=Rotation.identity(), v=(0, 0, 0), w_local=(0, 0, 0), height=0.0, q=None,
+          qd=None, B=16):
+    """A snapshot whose root frame is `root`: body 1 orientation = root * iquat."""
+    bodies = np.zeros((1, B, 13))
+    bodies[:, :, 3] = 1
+    iq = META["root_iquat"]
+    body_rot = root * Rotation.from_quat([iq[1], iq[2], iq[3], iq[0]])
+    bodies[0, 1, 3:7] = wxyz(body_rot)
+    bodies[0, 1, 2] = META["root_height"] + height
+    bodies[0, 1, 7:10] = v
+    bodies[0, 1, 10:13] = root.apply(w_local)
+    joints = np.zeros((1, J, 2))
+    joints[0, :, 0] = HOME_V if q is None else q
+    joints[0, :, 1] = 0 if qd is None else qd
+    return bodies, joints, np.zeros((1, 6))
+
+
+def run(kind=T.STANDING, bodies=None, joints=None, diag=None, a=None, last=None, **kw):
+    a = np.zeros((1, J)) if a is None else a
+    last = np.zeros((1, J)) if last is None else last
+    kw.setdefault("control_dt", DT)
+    kw.setdefault("episode", np.array([0]))
+    kw.setdefault("max_episode_length", 100)
+    if kind != T.STANDING:
+        kw.setdefault("commands", np.zeros((1, 2)))
+    return T.step_outputs(kind, bodies, joints, diag, a, last, META, **kw)
+
+
+def test_rotation_helpers_match_scipy():
+    rng = np.random.default_rng(1)
+    for _ in range(50):
+        ra, rb = Rotation.random(random_state=rng), Rotation.random(random_state=rng)
+        prod = T.quat_multiply(wxyz(ra), wxyz(rb))
+        assert np.allclose(Rotation.from_quat([*prod[1:], prod[0]]).as_matrix(),
+                           (ra * rb).as_matrix(), atol=1e-12)
+        v = rng.normal(size=3)
+        assert np.allclose(T.inverse_rotate(wxyz(ra), v), ra.inv().apply(v), atol=1e-12)
+
+
+def test_upright_home_is_the_reward_maximum():
+    b, j, d = state()
+    failed, reward, ep, timeout, done, _ = run(bodies=b, joints=j, diag=d)
+    assert not failed[0] and not done[0] and ep[0] == 1
+    assert reward[0] == pytest.approx(3.0 * DT, abs=1e-12)  # 1.5 + 1 + 0.5
+    obs = T.observe(T.STANDING, b, j, np.zeros((1, J)), META)
+    expect = np.zeros(52)
+    expect[2] = -1.0
+    assert np.allclose(obs[0], expect, atol=1e-12)
+
+
+@pytest.mark.parametrize("theta", [0.2, 0.49, 0.51, 1.0])
+def test_tilt_gravity_and_failure(theta):
+    b, j, d = state(root=Rotation.from_rotvec([theta, 0, 0]))
+    _, g, _, _, _ = T.root_frame(b, META["root_iquat"])
+    assert np.allclose(g[0], [0, -math.sin(theta), -math.cos(theta)], atol=1e-12)
+    failed, reward, *_ = run(bodies=b, joints=j, diag=d)
+    assert failed[0] == (theta > 0.5)
+    if theta < 0.5:
+        expect = 1.5 * math.exp(-20 * math.sin(theta) ** 2) + 1 + 0.5
+        assert reward[0] == pytest.approx(expect * DT, rel=1e-12)
+    else:
+        assert reward[0] == pytest.approx(-2 * DT)
+
+
+def test_yaw_local_velocity_and_heading():
+    psi = 0.7
+    b, j, d = state(root=Rotation.from_rotvec([0, 0, psi]), v=(1.0, 0, 0))
+    _, g, v, _, yaw = T.root_frame(b, META["root_iquat"])
+    assert np.allclose(yaw[0], [math.cos(psi), math.sin(psi)], atol=1e-12)
+    assert np.allclose(v[0], [math.cos(psi), -math.sin(psi), 0], atol=1e-12)
+    assert np.allclose(g[0], [0, 0, -1], atol=1e-12)
+    # Locomotion: the world velocity equals the command -> full tracking term;
+    # the heading term charges 1 - cos(psi).
+    failed, reward, *_ = run(T.LOCOMOTION, b, j, d, commands=np.array([[1.0, 0]]))
+    expect = 1 + 1 + 4.0 - 0.4 * (1 - math.cos(psi))
+    assert not failed[0] and reward[0] == pytest.approx(expect * DT, rel=1e-12)
+
+
+def test_single_reward_terms():
+    base = 3.0
+    b, j, d = state(w_local=(1.0, 0, 0))  # -0.02 |w|^2
+    assert run(bodies=b, joints=j, diag=d)[1][0] == pytest.approx((base - 0.02) * DT)
+    b, j, d = state(v=(0, 0.3, 0))  # 0.5 exp(-10 |v|^2)
+    assert run(bodies=b, joints=j, diag=d)[1][0] == pytest.approx(
+        (2.5 + 0.5 * math.exp(-0.9)) * DT)
+    b, j, d = state(height=0.01)  # exp(-2000 h^2)
+    assert run(bodies=b, joints=j, diag=d)[1][0] == pytest.approx(
+        (2.0 + math.exp(-0.2)) * DT)
+    b, j, d = state(q=HOME_V + 0.1)  # -0.05 sum (q - HOME)^2
+    assert run(bodies=b, joints=j, diag=d)[1][0] == pytest.approx((base - 0.05 * J * 0.01) * DT)
+    b, j, d = state()
+    a = np.full((1, J), 0.5)  # -0.01 |a|^2 - 0.02 |a - a_prev|^2
+    assert run(bodies=b, joints=j, diag=d, a=a)[1][0] == pytest.approx(
+        (base - 0.01 * J * 0.25 - 0.02 * J * 0.25) * DT)
+    assert run(bodies=b, joints=j, diag=d, a=a, last=a)[1][0] == pytest.approx(
+        (base - 0.01 * J * 0.25) * DT)
+    # Locomotion weights: -0.1 |w|^2, -0.02 |a|^2, -0.03 |da|^2, tracking sigma.
+    b, j, d = state(w_local=(0, 1.0, 0), v=(0.02, 0, 0))
+    r = run(T.LOCOMOTION, b, j, d, a=a, commands=np.zeros((1, 2)))[1][0]
+    expect = 2 + 4.0 * math.exp(-0.0004 / 0.0016) - 0.1 - 0.02 * J * 0.25 - 0.03 * J * 0.25
+    assert r == pytest.approx(expect * DT, rel=1e-12)
+
+
+def test_failure_thresholds_and_timeouts():
+    for k, value, fails in ((0, 0.0049, False), (0, 0.0051, True), (1, 0.006, True),
+                            (5, 1.0, True)):
+        b, j, d = state()
+        d[0, k] = value
+        assert run(bodies=b, joints=j, diag=d)[0][0] == fails
+    for h, fails in ((0.039, False), (0.041, True), (-0.041, True)):
+        b, j, d = state(height=h)
+        assert run(bodies=b, joints=j, diag=d)[0][0] == fails
+    b, j, d = state()
+    b[0, 7, 4] = np.nan
+    assert run(bodies=b, joints=j, diag=d)[0][0]
+    b, j, d = state()
+    failed, _, ep, timeout, done, _ = run(bodies=b, joints=j, diag=d, episode=np.array([99]))
+    assert ep[0] == 100 and timeout[0] and done[0] and not failed[0]
+    b, j, d = state(height=0.05)
+    failed, _, _, timeout, done, _ = run(bodies=b, joints=j, diag=d, episode=np.array([99]))
+    assert failed[0] and not timeout[0] and done[0]
+    # Rollout task: only a fall below fall_height (and numerical faults) fail.
+    b, j, d = state(root=Rotation.from_rotvec([1.0, 0, 0]), height=0.05)
+    assert not run(T.ROLLOUT, b, j, d)[0][0]
+    b[0, 1, 2] = 0.079
+    assert run(T.ROLLOUT, b, j, d)[0][0]
+
+
+def test_observation_layouts():
+    qd = np.arange(J) * 1.0
+    q = HOME_V + np.arange(J) * 0.01
+    b, j, d = state(q=q, qd=qd, height=0.02, v=(0.1, 0.2, 0.3), w_local=(0.4, 0.5, 0.6))
+    a = np.linspace(-1, 1, J)[None]
+    obs = T.observe(T.STANDING, b, j, a, META)[0]
+    assert obs.shape == (52,)
+    assert np.allclose(obs[:10], [0, 0, -1, 0.1, 0.2, 0.3, 0.4, 0.5, 0.6, 0.02], atol=1e-12)
+    assert np.allclose(obs[10:24], np.arange(J) * 0.01)
+    assert np.allclose(obs[24:38], 0.1 * qd)
+    assert np.allclose(obs[38:52], a[0])
+    obs = T.observe(T.ROLLOUT, b, j, a, META)[0]
+    assert obs.shape == (48,)
+    assert np.allclose(obs[:6], [0, 0, -1, 0.4, 0.5, 0.6], atol=1e-12)
+    assert np.allclose(obs[34:48], a[0])
+    obs = T.observe(T.LOCOMOTION, b, j, a, META, commands=np.array([[0.05, 0]]),
+                    episode=np.array([3]), control_dt=0.02, filtered=np.array([[7.0, 8.0]]))[0]
+    phase = 3 * 0.02 * 2 * math.pi / 0.8
+    assert obs.shape == (60,)
+    assert np.allclose(obs[52:], [0.05, 0, 1, 0, math.sin(phase), math.cos(phase), 7, 8],
+                       atol=1e-12)
+
+
+def test_targets_clamp():
+    lower, upper = np.array(META["lower"]), np.array(META["upper"])
+    acts = np.array([[2.0, -3.0] + [0.5] * 12])
+    a, target = T.targets(acts, HOME_V, lower, upper, 10.0)
+    assert a[0, 0] == 1 and a[0, 1] == -1 and a[0, 2] == 0.5
+    assert target[0, 0] == upper[0] and target[0, 1] == lower[1]
+    a, target = T.targets(np.zeros((1, J)), HOME_V, lower, upper, 0.3)
+    assert np.array_equal(target[0], HOME_V)
