@@ -259,20 +259,15 @@ __global__ void contactCountsKernel(unsigned char *states, long long blobBytes, 
 }
 
 // Recursive Newton-Euler at zero joint acceleration (kernel.cuh:504-554):
-// per hinge [bias, contact/limit, applied actuator torque].
+// per hinge [bias, contact/limit, applied actuator torque] into o[3 j + k];
+// `off` is the root COM offset of the acceleration reference point.
 template <class R, int B, int J, int CG, int CS>
-__global__ void generalizedLoadsKernel(const DeviceModel<R> *model, unsigned char *states,
-                                       long long blobBytes, int count, const R *offset, R *out) {
-  int e = blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= count)
-    return;
-  const DeviceModel<R> &M = *model;
-  auto &s = blobAt<EnvState<R, B, J, CG, CS>>(states, blobBytes, e);
-  StateView<R, B, J, CG, CS> v{M, s};
+DUCK_HD void rneaLoads(const DeviceModel<R> &M, const EnvState<R, B, J, CG, CS> &s, const R *off,
+                       R *o) {
+  StateView<R, B, J, CG, CS> v{M, const_cast<EnvState<R, B, J, CG, CS> &>(s)};
   V3<R> acc[B], alpha[B], force[B], moment[B], contact[B], contactMoment[B];
   for (int b = 0; b < M.nb; ++b)
     acc[b] = alpha[b] = force[b] = moment[b] = contact[b] = contactMoment[b] = V3<R>{0, 0, 0};
-  const R *off = offset + size_t(e) * 3;
   acc[1] = cross(v.W(1), cross(v.W(1), rotate(v.Q(1), V3<R>{off[0], off[1], off[2]})));
   for (int j = 0; j < M.nj; ++j) {
     const int a = M.ja[j], b = M.jb[j];
@@ -318,7 +313,6 @@ __global__ void generalizedLoadsKernel(const DeviceModel<R> *model, unsigned cha
     contactMoment[b] = contactMoment[b] +
                        cross(rotate(v.Q(b), V3<R>{c.localB[0], c.localB[1], c.localB[2]}), -f);
   }
-  R *o = out + size_t(e) * M.nj * 3;
   for (int k = M.nj - 1; k >= 0; --k) {
     const int a = M.ja[k], b = M.jb[k];
     Q4<R> qa = v.Q(a), qb = v.Q(b);
@@ -334,6 +328,16 @@ __global__ void generalizedLoadsKernel(const DeviceModel<R> *model, unsigned cha
     contactMoment[a] = contactMoment[a] + (contactMoment[b] + cross(shift, contact[b]));
     contact[a] = contact[a] + contact[b];
   }
+}
+
+template <class R, int B, int J, int CG, int CS>
+__global__ void generalizedLoadsKernel(const DeviceModel<R> *model, unsigned char *states,
+                                       long long blobBytes, int count, const R *offset, R *out) {
+  int e = blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= count)
+    return;
+  const auto &s = blobAt<EnvState<R, B, J, CG, CS>>(states, blobBytes, e);
+  rneaLoads<R, B, J, CG, CS>(*model, s, offset + size_t(e) * 3, out + size_t(e) * model->nj * 3);
 }
 
 } // namespace duckhip

@@ -1,6 +1,7 @@
 // C ABI of the gfx950 AVBD batch (include/duck_hip.h): model upload, state
 // ownership, stream ordering and kernel dispatch.
 #include "../../include/duck_hip.h"
+#include "avbd_servo.hpp"
 #include "avbd_task.hpp"
 #include "duck_model.hpp"
 
@@ -162,6 +163,7 @@ struct BatchBase {
   virtual void taskTargets(const DuckTask &, const void *, const void *, void *, void *,
                            hipStream_t) = 0;
   virtual void task(const DuckTask &, int, const TaskBuffers &, hipStream_t) = 0;
+  virtual void servo(const DuckServo &, const ServoBuffers &, hipStream_t) = 0;
 };
 
 template <class R, int B, int J, int CG, int CS, int L> class Batch final : public BatchBase {
@@ -371,6 +373,14 @@ public:
     taskKernel<R, B, J, CG, CS><<<blocks64(count), 64, 0, s>>>(t, mode, dModel, dStates, blobBytes,
                                                                 count, io);
     launched("taskKernel");
+    record(s);
+  }
+  void servo(const DuckServo &p, const ServoBuffers &io, hipStream_t s) override {
+    DeviceGuard guard(device);
+    wait(s);
+    servoKernel<R, B, J, CG, CS><<<blocks64(count), 64, 0, s>>>(p, dModel, dStates, blobBytes,
+                                                                 count, io);
+    launched("servoKernel");
     record(s);
   }
   void layout(long long *out) const override;
@@ -618,6 +628,29 @@ int duck_task_observe(void *handle, const DuckTask *task, const unsigned char *r
     TaskBuffers io{reset_mask, actions, actions, commands, episode, filtered, returns,
                    forces, obs, nullptr, nullptr, nullptr, nullptr, nullptr};
     b->task(*task, kTaskReset, io, st(hip_stream));
+  });
+}
+int duck_servo(void *handle, const DuckServo *servo, const void *target, void *history,
+               int cursor, unsigned char *initialized, const void *root_offset,
+               void *previous_motor, void *previous_applied, void *motor, void *supply,
+               void *hip_stream) {
+  return guarded([&] {
+    auto *b = as(handle);
+    require(servo != nullptr, "null servo parameters");
+    require(target && history && initialized && root_offset && previous_motor &&
+                previous_applied && motor,
+            "servo: null buffer");
+    require(servo->lag >= 0 && servo->lag < 1024 && cursor >= 0 && cursor <= servo->lag,
+            "servo: invalid lag or cursor");
+    const double values[] = {servo->kt, servo->resistance, servo->dtheta_stribeck, servo->alpha,
+                             servo->vin, servo->vin_min, servo->kp_fw, servo->force_limit};
+    for (double v : values)
+      require(std::isfinite(v), "servo: non-finite parameter");
+    require(servo->resistance != 0 && servo->dtheta_stribeck != 0 && servo->vin_min > 0,
+            "servo: resistance, dtheta_stribeck and vin_min must be nonzero");
+    ServoBuffers io{target, history, cursor, initialized, root_offset, previous_motor,
+                    previous_applied, motor, supply};
+    b->servo(*servo, io, st(hip_stream));
   });
 }
 int duck_reference(void *handle, const void *target, const void *force, int substeps, double kp,

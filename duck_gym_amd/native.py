@@ -56,6 +56,7 @@ def library():
             "duck_task_targets": (ip, [vp, ctypes.POINTER(DuckTask), vp, vp, vp, vp, vp]),
             "duck_task_step": (ip, [vp, ctypes.POINTER(DuckTask)] + [vp] * 13),
             "duck_task_observe": (ip, [vp, ctypes.POINTER(DuckTask)] + [vp] * 9),
+            "duck_servo": (ip, [vp, ctypes.POINTER(DuckServo), vp, vp, ip] + [vp] * 7),
         }
         for name, (res, args) in sig.items():
             fn = getattr(lib, name)
@@ -71,10 +72,22 @@ EXPORTED = (
     "duck_state", "duck_contact_forces", "duck_self_contact_stats", "duck_contact_counts",
     "duck_generalized_loads", "duck_reference", "duck_state_layout", "duck_export_state",
     "duck_import_state", "duck_last_error", "duck_task_obs_dim", "duck_task_targets",
-    "duck_task_step", "duck_task_observe",
+    "duck_task_step", "duck_task_observe", "duck_servo",
 )
 
 MAX_JOINTS = 32
+
+
+class DuckServo(ctypes.Structure):
+    """`DuckServo` of include/duck_hip.h: XL330/m6 actuator parameters."""
+
+    _fields_ = [(name, ctypes.c_double) for name in (
+        "kt", "resistance", "dtheta_stribeck", "alpha", "friction_base", "friction_stribeck",
+        "load_friction_external", "load_friction_motor", "load_friction_external_stribeck",
+        "load_friction_motor_stribeck", "load_friction_external_quad",
+        "load_friction_motor_quad", "friction_viscous", "vin", "vin_drop_gain", "vin_min",
+        "kp_fw", "kp_scale", "kd_scale", "friction_scale", "force_limit")] + [
+        ("lag", ctypes.c_int)]
 TASK_STANDING, TASK_LOCOMOTION, TASK_ROLLOUT = 0, 1, 2
 
 
@@ -257,6 +270,25 @@ class CudaBatch:
         if code:
             _raise(code, "reference")
         return b, j, d
+
+    # ------------------------------------------------------ servo substep
+    def servo(self, params, target, history, cursor, initialized, root_offset, previous_motor,
+              previous_applied, supply=None):
+        """One BAM servo substep (include/duck_hip.h duck_servo); returns the
+        motor channels [E,J,3] for `step_motor`."""
+        E, J = self.num_envs, self.num_joints
+        lag = int(params.lag)
+        motor = self._empty(E, J, 3)
+        args = [self._check(target, [E, J]), self._check(history, [lag + 1, E, J]),
+                ctypes.c_int(int(cursor)), self._check(initialized, [E], torch.bool),
+                self._check(root_offset, [E, 3]), self._check(previous_motor, [E, J]),
+                self._check(previous_applied, [E, J]), ctypes.c_void_p(motor.data_ptr()),
+                self._ptr(supply, [E])]
+        with torch.cuda.device(self.device):
+            code = library().duck_servo(self._h, ctypes.byref(params), *args, self._stream())
+        if code:
+            _raise(code, "servo")
+        return motor
 
     # ---------------------------------------------- tensor-env control step
     def _ptr(self, t, shape, dtype=None):

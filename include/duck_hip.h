@@ -153,6 +153,32 @@ int duck_task_observe(void *handle, const DuckTask *task, const unsigned char *r
                       void *actions, const void *commands, long long *episode, void *filtered,
                       float *returns, void *forces, float *obs, void *hip_stream);
 
+/* ---- BAM servo substep (python/duck_gym/bam_env.py:307-326) ----
+ * Parameters of the XL330/m6 actuator equations (python/duck_gym/actuator.py:
+ * 16-77; names as in the BAM parameter dictionary and the official config). */
+typedef struct DuckServo {
+  double kt, resistance, dtheta_stribeck, alpha, friction_base, friction_stribeck;
+  double load_friction_external, load_friction_motor, load_friction_external_stribeck;
+  double load_friction_motor_stribeck, load_friction_external_quad, load_friction_motor_quad;
+  double friction_viscous;
+  double vin, vin_drop_gain, vin_min, kp_fw, kp_scale, kd_scale, friction_scale, force_limit;
+  int lag; /* actuator delay in physics steps; the ring holds lag + 1 targets */
+} DuckServo;
+
+/* One servo substep before duck_step_motor: history[cursor] = target (every
+ * slot for envs whose `initialized` flag is 0, which is then set), delayed =
+ * history[(cursor - lag) mod (lag + 1)]; external hinge load = -bias +
+ * constraint of the Newton-Euler pass with root COM offset `root_offset`
+ * [E,3] (duck_generalized_loads columns 0 and 1); the XL330 model gives
+ * motor [E,J,3] = (clamped torque, friction budget, damping), and
+ * previous_motor / previous_applied [E,J] are replaced by this substep's raw /
+ * clamped torque.  history [lag+1,E,J]; supply [E] may be NULL.  The caller
+ * advances `cursor` = (cursor + 1) mod (lag + 1) per substep. */
+int duck_servo(void *handle, const DuckServo *servo, const void *target, void *history,
+               int cursor, unsigned char *initialized, const void *root_offset,
+               void *previous_motor, void *previous_applied, void *motor, void *supply,
+               void *hip_stream);
+
 const char *duck_last_error(void);
 
 #ifdef __cplusplus

@@ -140,3 +140,31 @@ def test_state_codec_round_trip():
     c = out["sc"][0]
     assert (c["body"], c["other"], c["shape"], c["otherShape"]) == (1, 2, 3, 4)
     np.testing.assert_array_equal(c["n"], s["sc"][0]["n"])
+
+
+def test_ctypes_structs_match_the_c_header(tmp_path):
+    """DuckTask / DuckServo field offsets in ctypes equal the C layout."""
+    import shutil
+    import subprocess
+
+    from duck_gym_amd.native import DuckServo, DuckTask
+
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no C compiler")
+    lines = ['#include <stddef.h>', '#include <stdio.h>', '#include "duck_hip.h"', "int main(void){"]
+    for struct, cls in (("DuckTask", DuckTask), ("DuckServo", DuckServo)):
+        lines.append(f'printf("{struct} %zu\\n", sizeof({struct}));')
+        for name, _ in cls._fields_:
+            lines.append(f'printf("{struct}.{name} %zu\\n", offsetof({struct}, {name}));')
+    lines.append("return 0;}")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run([cc, "-I", str(ROOT / "include"), str(src), "-o", str(exe)], check=True)
+    got = dict(l.split() for l in subprocess.run([str(exe)], capture_output=True, text=True,
+                                                 check=True).stdout.splitlines())
+    for struct, cls in (("DuckTask", DuckTask), ("DuckServo", DuckServo)):
+        assert int(got[struct]) == ctypes.sizeof(cls)
+        for name, _ in cls._fields_:
+            assert int(got[f"{struct}.{name}"]) == getattr(cls, name).offset, (struct, name)
