@@ -380,6 +380,12 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
   __syncthreads();
 
   Stepper<R, B, J, CG, CS, L> stp{M, points, F, E, lane};
+  // Block-solve lanes: with P == 2, lanes l and l ^ 8 (same 16-lane DPP row)
+  // share a body; `slot` numbers the bodies a colour pass runs at once.
+  constexpr int P = Stepper<R, B, J, CG, CS, L>::P;
+  static_assert(P == 1 || L % 16 == 0, "split block solves need 16-lane groups");
+  const int part = P == 2 ? (lane >> 3) & 1 : 0;
+  const int slot = P == 2 ? (lane & 7) + 8 * (lane >> 4) : lane;
   const R h = M.dt, alpha = M.alpha, gamma = M.gamma, ag = alpha * gamma;
 
   for (int sub = 0; sub < args.substeps; ++sub) {
@@ -705,7 +711,7 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
                                             divide(stp.force(b), mass));
         V3<R> spin = -cross(w, stp.inertiaApply(q, I, w, false));
         V3<R> wp = w + h * stp.inertiaApply(q, I, spin, true);
-        Q4<R> qp = expmap(h * wp) * q;
+        Q4<R> qp = fexpmap(h * wp) * q;
         for (int k = 0; k < 3; ++k)
           E.xp[k][b] = comp(xp, k);
         E.qp[0][b] = qp.w;
@@ -726,8 +732,8 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
       R maxUpdate = 0;
       for (int c = 0; c < colours; ++c) {
         if (work && c < E.s.colorCount)
-          for (int k = E.colorStart[c] + lane; k < E.colorStart[c + 1]; k += L)
-            maxUpdate = mx(maxUpdate, stp.updateBody(E.order[k], true));
+          for (int k = E.colorStart[c] + slot; k < E.colorStart[c + 1]; k += L / P)
+            maxUpdate = mx(maxUpdate, stp.updateBody(E.order[k], true, part));
         __syncthreads();
       }
       maxUpdate = groupMax<L>(maxUpdate);
@@ -810,7 +816,7 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
           continue;
         V3<R> x = stp.X(b), x0{E.x0[0][b], E.x0[1][b], E.x0[2][b]};
         V3<R> v = (x - x0) * invh;
-        V3<R> w = logmap(stp.Q(b) * conj(stp.Q0(b))) * invh;
+        V3<R> w = flogmap(stp.Q(b) * conj(stp.Q0(b))) * invh;
         for (int k = 0; k < 3; ++k) {
           E.s.v[k][b] = comp(v, k);
           E.s.w[k][b] = comp(w, k);

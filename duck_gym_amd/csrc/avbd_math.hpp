@@ -30,6 +30,44 @@ DUCK_HD double mabs(double x) { return fabs(x); }
 DUCK_HD bool mfinite(float x) { return isfinite(x); }
 DUCK_HD bool mfinite(double x) { return isfinite(x); }
 
+// Solver arithmetic.  The float solver uses the gfx950 reciprocal, square
+// root and reciprocal square root instructions (about 1 ulp) instead of the
+// correctly rounded multi-instruction sequences; the double solver keeps the
+// correctly rounded operations and so tracks the float64 oracle to rounding.
+// Only the block solve, predictor and velocity recovery use these; contact
+// detection and colouring keep the exact operations (their outputs are
+// discrete and must not move).
+DUCK_HD float frcp(float x) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __builtin_amdgcn_rcpf(x);
+#else
+  return 1.0f / x;
+#endif
+}
+DUCK_HD double frcp(double x) { return 1.0 / x; }
+DUCK_HD float fsqrt(float x) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __builtin_amdgcn_sqrtf(x);
+#else
+  return sqrtf(x);
+#endif
+}
+DUCK_HD double fsqrt(double x) { return sqrt(x); }
+DUCK_HD float frsqrt(float x) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __builtin_amdgcn_rsqf(x);
+#else
+  return 1.0f / sqrtf(x);
+#endif
+}
+DUCK_HD double frsqrt(double x) { return 1.0 / sqrt(x); }
+// a / b: a * rcp(b) in float, a true division in double.
+DUCK_HD float fdiv(float a, float b) { return a * frcp(b); }
+DUCK_HD double fdiv(double a, double b) { return a / b; }
+// a / b given inv = frcp(b): the float path multiplies, the double path divides.
+DUCK_HD float fdivInv(float a, float, float inv) { return a * inv; }
+DUCK_HD double fdivInv(double a, double b, double) { return a / b; }
+
 template <class R> struct V3 {
   R x, y, z;
 };
@@ -97,9 +135,71 @@ template <class R> DUCK_HD V3<R> logmap(Q4<R> q) {
   return v * k;
 }
 
+// Fast forms of norm / normalized / expmap / logmap for the float solver
+// (exact forms for double).  Small rotations, the common case inside the
+// block solve, use truncated Taylor series whose first omitted term is below
+// 1e-11 relative on the stated ranges.
+template <class R> DUCK_HD R fnorm(V3<R> a) { return fsqrt(dot(a, a)); }
+template <class R> DUCK_HD Q4<R> fnormalized(Q4<R> q) {
+  if constexpr (sizeof(R) == sizeof(float)) {
+    R n2 = q.w * q.w + q.x * q.x + q.y * q.y + q.z * q.z;
+    if (double(n2) < 1e-30)
+      return {R(NAN), R(NAN), R(NAN), R(NAN)};
+    R inv = frsqrt(n2);
+    return {q.w * inv, q.x * inv, q.y * inv, q.z * inv};
+  } else {
+    return normalized(q);
+  }
+}
+template <class R> DUCK_HD Q4<R> fexpmap(V3<R> v) {
+  if constexpr (sizeof(R) == sizeof(float)) {
+    R a = fnorm(v), s, c;
+    if (a < R(0.25)) {
+      R a2 = a * a;
+      // sin(a/2)/a and cos(a/2)
+      s = R(0.5) + a2 * (R(-1.0 / 48) + a2 * (R(1.0 / 3840) + a2 * R(-1.0 / 645120)));
+      c = R(1) + a2 * (R(-0.125) + a2 * (R(1.0 / 384) + a2 * (R(-1.0 / 46080) +
+                                                               a2 * R(1.0 / 10321920))));
+    } else {
+      s = msin(a / R(2)) / a;
+      c = mcos(a / R(2));
+    }
+    return fnormalized(Q4<R>{c, s * v.x, s * v.y, s * v.z});
+  } else {
+    return expmap(v);
+  }
+}
+template <class R> DUCK_HD V3<R> flogmap(Q4<R> q) {
+  if constexpr (sizeof(R) == sizeof(float)) {
+    q = fnormalized(q);
+    if (q.w < 0)
+      q = {-q.w, -q.x, -q.y, -q.z};
+    V3<R> v{q.x, q.y, q.z};
+    R s = fnorm(v), k;
+    if (double(s) < 1e-10) {
+      k = R(2);
+    } else if (q.w > R(0.99)) {
+      // 2 atan(s/w)/s = (2/w) atan(t)/t with t = s/w < 0.143
+      R iw = frcp(q.w), t = s * iw, t2 = t * t;
+      R p = R(1) + t2 * (R(-1.0 / 3) + t2 * (R(0.2) + t2 * (R(-1.0 / 7) +
+                                                            t2 * (R(1.0 / 9) + t2 * R(-1.0 / 11)))));
+      k = (R(2) * iw) * p;
+    } else {
+      k = R(2) * matan2(s, q.w) / s;
+    }
+    return v * k;
+  } else {
+    return logmap(q);
+  }
+}
+
 // IEEE remainder(a, 2*pi) in double: n = nearest integer of a/(2 pi), then the
 // exactly representable a - n 2pi by one fused operation.  [double]
 template <class R> DUCK_HD R wrapAngle(R a) {
+  // |a| < 3.14159 < pi: the nearest multiple is 0 and fma(-(+-0), 2 pi, d)
+  // is d, except that d = -0 yields +0 -- which a + 0 reproduces exactly.
+  if (mabs(a) < R(3.14159))
+    return a + R(0);
   const double twoPi = 6.283185307179586476925286766559; // 2*acos(-1.0)
   double d = double(a);
   double n = rint(d / twoPi);

@@ -86,24 +86,25 @@ template <class R> DUCK_HD void stampFull(Hess<R> &H, V3<R> t, V3<R> r, R f, R k
 // Diagonal majorisation of the rotational geometric stiffness
 // (kernel.cuh:283-301).  For float, 0.5*x - y in float equals the reference's
 // double evaluation rounded to float (no double rounding can occur).
+// The 3x3 matrix is symmetric (its off-diagonal entries are bitwise equal:
+// IEEE + and * commute), so six entries are formed; column sums keep row order.
 template <class R> DUCK_HD void geometricAdd(Hess<R> &H, V3<R> r, V3<R> f) {
   R rf = dot(r, f);
-  R rv[3] = {r.x, r.y, r.z}, fv[3] = {f.x, f.y, f.z};
-#pragma unroll
-  for (int col = 0; col < 3; ++col) {
-    R sum = 0;
-#pragma unroll
-    for (int row = 0; row < 3; ++row) {
-      R a = R(0.5) * (rv[row] * fv[col] + fv[row] * rv[col]) - (row == col ? rf : R(0));
-      sum += a * a;
-    }
-    H.h[tri(3 + col, 3 + col)] += msqrt(sum);
-  }
+  R a00 = R(0.5) * (r.x * f.x + f.x * r.x) - rf;
+  R a11 = R(0.5) * (r.y * f.y + f.y * r.y) - rf;
+  R a22 = R(0.5) * (r.z * f.z + f.z * r.z) - rf;
+  R a01 = R(0.5) * (r.x * f.y + f.x * r.y);
+  R a02 = R(0.5) * (r.x * f.z + f.x * r.z);
+  R a12 = R(0.5) * (r.y * f.z + f.y * r.z);
+  H.h[tri(3, 3)] += fsqrt(((R(0) + a00 * a00) + a01 * a01) + a02 * a02);
+  H.h[tri(4, 4)] += fsqrt(((R(0) + a01 * a01) + a11 * a11) + a12 * a12);
+  H.h[tri(5, 5)] += fsqrt(((R(0) + a02 * a02) + a12 * a12) + a22 * a22);
 }
 
 // Cholesky solve of H x = -g with NaN on a bad pivot (kernel.cuh:177-228).
+// The float path multiplies by reciprocal pivots (fdivInv).
 template <class R> DUCK_HD void solve6(const Hess<R> &H, R x[6]) {
-  R L[21];
+  R L[21], inv[6];
 #pragma unroll
   for (int i = 0; i < 6; ++i) {
 #pragma unroll
@@ -119,9 +120,10 @@ template <class R> DUCK_HD void solve6(const Hess<R> &H, R x[6]) {
             x[k] = R(NAN);
           return;
         }
-        L[tri(i, i)] = msqrt(v);
+        L[tri(i, i)] = fsqrt(v);
+        inv[i] = frcp(L[tri(i, i)]);
       } else {
-        L[tri(i, j)] = v / L[tri(j, j)];
+        L[tri(i, j)] = fdivInv(v, L[tri(j, j)], inv[j]);
       }
     }
   }
@@ -132,7 +134,7 @@ template <class R> DUCK_HD void solve6(const Hess<R> &H, R x[6]) {
 #pragma unroll
     for (int k = 0; k < i; ++k)
       y[i] -= L[tri(i, k)] * y[k];
-    y[i] /= L[tri(i, i)];
+    y[i] = fdivInv(y[i], L[tri(i, i)], inv[i]);
   }
 #pragma unroll
   for (int i = 5; i >= 0; --i) {
@@ -140,13 +142,23 @@ template <class R> DUCK_HD void solve6(const Hess<R> &H, R x[6]) {
 #pragma unroll
     for (int k = i + 1; k < 6; ++k)
       x[i] -= L[tri(k, i)] * x[k];
-    x[i] /= L[tri(i, i)];
+    x[i] = fdivInv(x[i], L[tri(i, i)], inv[i]);
   }
 }
 
 // (1 - (a/2)/tan(a/2)) / a^2, the SO(3) log-Jacobian coefficient, evaluated
 // in double as the reference's float build does (kernel.cuh:841-850). [double]
+// The float solver sums the series 1/12 + a^2/720 + a^4/30240 + a^6/1209600
+// + a^8/47900160 for a < 0.5 (first omitted term < 1e-11 relative).
 template <class R> DUCK_HD R logJacobianCoef(R a) {
+  if constexpr (sizeof(R) == sizeof(float)) {
+    if (a < R(0.5)) {
+      R a2 = a * a;
+      return R(1.0 / 12) +
+             a2 * (R(1.0 / 720) + a2 * (R(1.0 / 30240) + a2 * (R(1.0 / 1209600) +
+                                                                a2 * R(1.0 / 47900160))));
+    }
+  }
   double ad = double(a);
   if (ad < 1e-5)
     return R(1.0 / 12 + double(a * a / R(720)));
@@ -165,12 +177,29 @@ template <class R> DUCK_HD V3<R> contactForce(V3<R> C, const R lambda[3], const 
   V3<R> f{lambda[0] + penalty[0] * C.x, lambda[1] + penalty[1] * C.y,
           lambda[2] + penalty[2] * C.z};
   f.z = mn(f.z, R(0));
-  R t = mhypot(f.x, f.y), bound = -friction * f.z;
+  R t, bound = -friction * f.z;
+  if constexpr (sizeof(R) == sizeof(float))
+    t = fsqrt(f.x * f.x + f.y * f.y); // magnitudes here are far from overflow
+  else
+    t = mhypot(f.x, f.y);
   if (t > bound && t > 0) {
-    f.x *= bound / t;
-    f.y *= bound / t;
+    R ratio = fdiv(bound, t);
+    f.x *= ratio;
+    f.y *= ratio;
   }
   return f;
+}
+
+// Value of the lane 8 positions away inside the same 16-lane row (DPP
+// row_ror:8, i.e. lane ^ 8): the two halves of a split block solve.
+__device__ __forceinline__ float pairSwap(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));
+}
+__device__ __forceinline__ double pairSwap(double v) {
+  const unsigned long long b = static_cast<unsigned long long>(__double_as_longlong(v));
+  const unsigned lo = __builtin_amdgcn_update_dpp(0, int(unsigned(b)), 0x128, 0xF, 0xF, false);
+  const unsigned hi = __builtin_amdgcn_update_dpp(0, int(unsigned(b >> 32)), 0x128, 0xF, 0xF, false);
+  return __longlong_as_double(static_cast<long long>((static_cast<unsigned long long>(hi) << 32) | lo));
 }
 
 template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
@@ -181,6 +210,9 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
   const Fr &F;
   Env &E;
   int lane; // 0..L-1 within the environment
+  // Lanes per block solve: with 16 or more lanes per environment two lanes
+  // (lane and lane ^ 8) share each body's assembly and combine it by DPP.
+  static constexpr int P = L >= 16 ? 2 : 1;
 
   // ------------------------------------------------------------ access --
   DUCK_HD V3<R> X(int b) const { return {E.s.x[0][b], E.s.x[1][b], E.s.x[2][b]}; }
@@ -274,8 +306,12 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
   }
 
   // --------------------------------------------------- 6x6 block solve --
-  // kernel.cuh:828-936 for one dynamic body.
-  DUCK_HD R updateBody(int bi, bool implicitDrive) {
+  // kernel.cuh:828-936 for one dynamic body.  With P == 2 the two lanes of
+  // a pair call this for the same body: part 0 assembles the inertia block,
+  // the odd-position hinges and the odd-position contacts, part 1 the even
+  // ones; the partial systems are summed on both lanes (bitwise the same
+  // sum), both solve, part 0 writes the pose.
+  __device__ R updateBody(int bi, bool implicitDrive, int part) {
     const R h = M.dt;
     V3<R> x = X(bi), xp{E.xp[0][bi], E.xp[1][bi], E.xp[2][bi]};
     Q4<R> q = Q(bi), qp{E.qp[0][bi], E.qp[1][bi], E.qp[2][bi], E.qp[3][bi]}, q0 = Q0(bi);
@@ -284,33 +320,39 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
 #pragma unroll
     for (int k = 0; k < 21; ++k)
       H.h[k] = 0;
-    V3<R> dx = x - xp, theta = logmap(q * conj(qp));
-    R mh = E.s.mass[bi] / (h * h);
-    H.h[tri(0, 0)] = mh;
-    H.h[tri(1, 1)] = mh;
-    H.h[tri(2, 2)] = mh;
-    H.g[0] = mh * dx.x;
-    H.g[1] = mh * dx.y;
-    H.g[2] = mh * dx.z;
-    R coef = logJacobianCoef(norm(theta));
-    V3<R> rotJ[3];
 #pragma unroll
-    for (int k = 0; k < 3; ++k) {
-      V3<R> e = unitAxis<R>(k);
-      rotJ[k] = (e - R(0.5) * cross(theta, e)) + coef * cross(theta, cross(theta, e));
-    }
-    V3<R> It = inertiaApply(q0, I, theta, false);
-    V3<R> IJ[3] = {inertiaApply(q0, I, rotJ[0], false), inertiaApply(q0, I, rotJ[1], false),
-                   inertiaApply(q0, I, rotJ[2], false)};
+    for (int k = 0; k < 6; ++k)
+      H.g[k] = 0;
+    const R h2 = h * h, ih2 = frcp(h2), ih = frcp(h);
+    if (part == 0) {
+      V3<R> dx = x - xp, theta = flogmap(q * conj(qp));
+      R mh = fdivInv(E.s.mass[bi], h2, ih2);
+      H.h[tri(0, 0)] = mh;
+      H.h[tri(1, 1)] = mh;
+      H.h[tri(2, 2)] = mh;
+      H.g[0] = mh * dx.x;
+      H.g[1] = mh * dx.y;
+      H.g[2] = mh * dx.z;
+      R coef = logJacobianCoef(fnorm(theta));
+      V3<R> rotJ[3];
 #pragma unroll
-    for (int k = 0; k < 3; ++k) {
-      H.g[3 + k] = dot(rotJ[k], It) / (h * h);
+      for (int k = 0; k < 3; ++k) {
+        V3<R> e = unitAxis<R>(k);
+        rotJ[k] = (e - R(0.5) * cross(theta, e)) + coef * cross(theta, cross(theta, e));
+      }
+      V3<R> It = inertiaApply(q0, I, theta, false);
+      V3<R> IJ[3] = {inertiaApply(q0, I, rotJ[0], false), inertiaApply(q0, I, rotJ[1], false),
+                     inertiaApply(q0, I, rotJ[2], false)};
 #pragma unroll
-      for (int l = 0; l <= k; ++l)
-        H.h[tri(3 + k, 3 + l)] = dot(rotJ[k], IJ[l]) / (h * h);
+      for (int k = 0; k < 3; ++k) {
+        H.g[3 + k] = fdivInv(dot(rotJ[k], It), h2, ih2);
+#pragma unroll
+        for (int l = 0; l <= k; ++l)
+          H.h[tri(3 + k, 3 + l)] = fdivInv(dot(rotJ[k], IJ[l]), h2, ih2);
+      }
     }
     const R alpha = M.alpha;
-    for (int adj = F.adjStart[bi]; adj < F.adjStart[bi + 1]; ++adj) {
+    for (int adj = F.adjStart[bi] + (P == 2 ? 1 - part : 0); adj < F.adjStart[bi + 1]; adj += P) {
       const int ji = F.adj[adj];
       const bool parent = bi == F.a[ji];
       const R s = parent ? R(1) : R(-1);
@@ -356,8 +398,9 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
       }
       R damping = E.s.damping[ji], armature = F.armature[ji];
       R delta = wrapAngle(je.angle - E.angle0[ji]);
-      R stiff = damping / h + armature / (h * h);
-      R force = damping / h * delta + armature / (h * h) * (delta - h * E.velocity0[ji]);
+      const R dh = fdivInv(damping, h, ih), ah = fdivInv(armature, h2, ih2);
+      R stiff = dh + ah;
+      R force = dh * delta + ah * (delta - h * E.velocity0[ji]);
       if (stiff > 0)
         stampAngular(H, J5, force, stiff);
       R fl = E.s.frictionloss[ji];
@@ -367,7 +410,10 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
       }
     }
     // Ground contacts of this body, in list order.
-    for (uint64_t m = E.gmask[bi]; m; m &= m - 1) {
+    int nth = 0;
+    for (uint64_t m = E.gmask[bi]; m; m &= m - 1, ++nth) {
+      if (P == 2 && (nth & 1) == part)
+        continue;
       const GroundContact<R> &c = E.s.gc[__builtin_ctzll(m)];
       V3<R> ra;
       V3<R> C = groundC(c, ra);
@@ -380,7 +426,10 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
       }
     }
     // Body-body contacts touching this body, in list order.
-    for (uint32_t m = E.smask[bi]; m; m &= m - 1) {
+    nth = 0;
+    for (uint32_t m = E.smask[bi]; m; m &= m - 1, ++nth) {
+      if (P == 2 && (nth & 1) == part)
+        continue;
       const SelfContact<R> &c = E.s.sc[__builtin_ctz(m)];
       V3<R> ra, rb;
       V3<R> C = selfC(c, ra, rb);
@@ -402,13 +451,24 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
         geometricAdd(H, r, fw * sign);
       }
     }
+    if constexpr (P == 2) {
+#pragma unroll
+      for (int k = 0; k < 21; ++k)
+        H.h[k] += pairSwap(H.h[k]);
+#pragma unroll
+      for (int k = 0; k < 6; ++k)
+        H.g[k] += pairSwap(H.g[k]);
+    }
     R st[6];
     solve6(H, st);
     V3<R> tx{st[0], st[1], st[2]}, rx{st[3], st[4], st[5]};
-    R scale = mn(R(1), mn(R(.1) / mx(norm(tx), R(1e-30)), R(.25) / mx(norm(rx), R(1e-30))));
-    setX(bi, x + scale * tx);
-    setQ(bi, normalized(expmap(scale * rx) * q));
-    return mx(norm(tx), norm(rx)) * scale;
+    const R ntx = fnorm(tx), nrx = fnorm(rx);
+    R scale = mn(R(1), mn(fdiv(R(.1), mx(ntx, R(1e-30))), fdiv(R(.25), mx(nrx, R(1e-30)))));
+    if (part == 0) {
+      setX(bi, x + scale * tx);
+      setQ(bi, fnormalized(fexpmap(scale * rx) * q));
+    }
+    return mx(ntx, nrx) * scale;
   }
 };
 

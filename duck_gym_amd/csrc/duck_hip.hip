@@ -434,12 +434,19 @@ const char *kMicroDuckJoints[14] = {
     "head_roll",       "right_hip_yaw",  "right_hip_roll", "right_hip_pitch",
     "right_knee",      "right_ankle"};
 
+// MicroDuck-sized models: float runs 4 environments per wave with two lanes
+// per block solve (16 lanes per env); double runs 8 environments per wave
+// with one lane per block solve, which keeps the reference's accumulation
+// order (DUCK_FLAG_SPLIT selects the float layout for double too).
 template <class R>
-BatchBase *makeBatch(HostModel &&m, int n, double dt, int iterations, int device) {
+BatchBase *makeBatch(HostModel &&m, int n, double dt, int iterations, int device, bool split) {
   const int nb = m.bodies.size(), nj = m.joints.size(), ns = m.shapes.size(),
             np = m.pairs.size();
-  if (nb <= 16 && nj <= 16 && ns <= 16 && np <= 8 && m.groundCapacity <= 64)
+  if (nb <= 16 && nj <= 16 && ns <= 16 && np <= 8 && m.groundCapacity <= 64) {
+    if (split || sizeof(R) == sizeof(float))
+      return new Batch<R, 16, 16, 64, 8, 16>(std::move(m), n, dt, iterations, device);
     return new Batch<R, 16, 16, 64, 8, 8>(std::move(m), n, dt, iterations, device);
+  }
   // Per-body contact masks are 64-bit: at most 64 ground contacts per env.
   if (m.groundCapacity > 64)
     throw DuckError(DUCK_ERR_MODEL, "Model exceeds selected state contact capacity");
@@ -501,8 +508,10 @@ int duck_create(const char *model_path, int num_envs, double dt, int iterations,
         require(label == kMicroDuckJoints[i], "Unsupported MicroDuck joint layout");
       }
     }
-    BatchBase *b = fp_bits == 64 ? makeBatch<double>(std::move(m), num_envs, dt, iterations, device)
-                                 : makeBatch<float>(std::move(m), num_envs, dt, iterations, device);
+    const bool split = flags & DUCK_FLAG_SPLIT;
+    BatchBase *b =
+        fp_bits == 64 ? makeBatch<double>(std::move(m), num_envs, dt, iterations, device, split)
+                      : makeBatch<float>(std::move(m), num_envs, dt, iterations, device, split);
     *out_handle = b;
   });
 }

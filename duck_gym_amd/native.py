@@ -122,14 +122,17 @@ class CudaBatch:
     """Batched AVBD environments on one MI355X (gfx950) device."""
 
     def __init__(self, model, num_envs, dt=0.001, iterations=200, device=0, fp64=False,
-                 specialized=False, shared_memory=False):
+                 specialized=False, shared_memory=False, split_solve=False):
         # `shared_memory` is accepted for signature compatibility: the gfx950
-        # kernel always stages environment state in LDS.
+        # kernel always stages environment state in LDS.  `split_solve` (an
+        # extension) runs float64 batches in the float layout: two lanes per
+        # body block solve, whose partial systems are summed in another order.
         lib = library()
         self._h = None
         handle = ctypes.c_void_p()
         code = lib.duck_create(str(model).encode(), int(num_envs), float(dt), int(iterations),
-                               int(device), 64 if fp64 else 32, 1 if specialized else 0,
+                               int(device), 64 if fp64 else 32,
+                               (1 if specialized else 0) | (2 if split_solve else 0),
                                ctypes.byref(handle))
         if code:
             _raise(code, "CudaBatch")

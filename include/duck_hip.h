@@ -31,6 +31,8 @@ enum {
 
 /* Flags of duck_create. */
 #define DUCK_FLAG_SPECIALIZED 1u /* require the MicroDuck 16-body/14-hinge layout */
+#define DUCK_FLAG_SPLIT 2u       /* float64: use the float layout (two lanes per body
+                                    block solve) instead of one lane per solve */
 
 /* CudaBatch(model, num_envs, dt, iterations, device, fp64, specialized)
  * (extension.cu:216-265, 423-441).  num_envs in [1, 65536]. */

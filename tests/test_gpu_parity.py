@@ -21,11 +21,12 @@ DT, ITER, KP = 0.005, 10, 8.0
 DEV = "cuda:0"
 
 
-def _run_pair(model, targets, steps, fp64, limit=0.0, forces=None, root=None, substeps=1):
+def _run_pair(model, targets, steps, fp64, limit=0.0, forces=None, root=None, substeps=1,
+              split=False):
     """Reset GPU and oracle envs to the same seeded state, then step both."""
     E = len(targets)
     dtype = torch.float64 if fp64 else torch.float32
-    batch = CudaBatch(model, E, DT, ITER, 0, fp64)
+    batch = CudaBatch(model, E, DT, ITER, 0, fp64, split_solve=split)
     oracles = oracle_envs(model, E, DT, ITER, fp64)
     q0 = targets[:, :] if root is None else targets
     for o, q in zip(oracles, q0):
@@ -54,16 +55,19 @@ def _legs_together(home, rng, n):
     return targets
 
 
+@pytest.mark.parametrize("split", [False, True], ids=["one-lane", "split"])
 @pytest.mark.parametrize("name", ["standing", "friction", "selfc"])
-def test_fp64_trajectory_matches_oracle(models, home, name):
+def test_fp64_trajectory_matches_oracle(models, home, name, split):
     """Ground and body-body contact (MPR, fresh colours), PD drive with a
     torque limit, active hinge limits, damping, dry friction: the float64
-    kernel follows the oracle to rounding over 40 steps."""
+    kernel follows the oracle to rounding over 40 steps, both with one lane
+    per block solve (the oracle's accumulation order) and with the float
+    layout's two-lane split (partial systems summed in another order)."""
     rng = np.random.default_rng(7)
     targets = home + rng.uniform(-0.3, 0.3, (6, 14))
     if name == "selfc":
         targets = _legs_together(home, rng, 6)  # drives hip rolls past their limits
-    _, _, history = _run_pair(models[name], targets, 40, True, limit=0.5)
+    _, _, history = _run_pair(models[name], targets, 40, True, limit=0.5, split=split)
     worst = 0.0
     for step, envs in enumerate(history):
         for e, (gpu, ref) in enumerate(envs):
