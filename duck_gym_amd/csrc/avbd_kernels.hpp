@@ -4,19 +4,54 @@
 
 namespace duckhip {
 
+// Lane (i + N) mod 16 of the same 16-lane row (DPP row_ror:N).
+template <int N> __device__ __forceinline__ int rowRor(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, 0x120 + N, 0xF, 0xF, false);
+}
+template <int N> __device__ __forceinline__ float rowRor(float v) {
+  return __int_as_float(rowRor<N>(__float_as_int(v)));
+}
+template <int N> __device__ __forceinline__ double rowRor(double v) {
+  const unsigned long long b = static_cast<unsigned long long>(__double_as_longlong(v));
+  const unsigned lo = rowRor<N>(int(unsigned(b))), hi = rowRor<N>(int(unsigned(b >> 32)));
+  return __longlong_as_double(static_cast<long long>((static_cast<unsigned long long>(hi) << 32) | lo));
+}
+
+// Maximum over the L lanes of an environment, on every one of them.  For
+// L == 16 (one DPP row) four row rotations replace the LDS-crossbar shuffles.
 template <int L, class T> __device__ __forceinline__ T groupMax(T v) {
-#pragma unroll
-  for (int o = L / 2; o > 0; o /= 2) {
-    T u = __shfl_xor(v, o, L);
+  if constexpr (L == 16) {
+    T u = rowRor<8>(v);
     v = v > u ? v : u;
+    u = rowRor<4>(v);
+    v = v > u ? v : u;
+    u = rowRor<2>(v);
+    v = v > u ? v : u;
+    u = rowRor<1>(v);
+    v = v > u ? v : u;
+    return v;
+  } else {
+#pragma unroll
+    for (int o = L / 2; o > 0; o /= 2) {
+      T u = __shfl_xor(v, o, L);
+      v = v > u ? v : u;
+    }
+    return v;
   }
-  return v;
 }
 template <int L> __device__ __forceinline__ int groupOr(int v) {
+  if constexpr (L == 16) {
+    v |= rowRor<8>(v);
+    v |= rowRor<4>(v);
+    v |= rowRor<2>(v);
+    v |= rowRor<1>(v);
+    return v;
+  } else {
 #pragma unroll
-  for (int o = L / 2; o > 0; o /= 2)
-    v |= __shfl_xor(v, o, L);
-  return v;
+    for (int o = L / 2; o > 0; o /= 2)
+      v |= __shfl_xor(v, o, L);
+    return v;
+  }
 }
 __device__ __forceinline__ int waveMaxInt(int v) {
 #pragma unroll
@@ -26,6 +61,10 @@ __device__ __forceinline__ int waveMaxInt(int v) {
   }
   return v;
 }
+
+// Shapes with at most this many points keep their candidate heights in
+// registers during ground-contact selection.
+constexpr int kCachedPoints = 8;
 
 template <class S> __device__ __forceinline__ S &blobAt(unsigned char *base, long long bytes, int e) {
   return *reinterpret_cast<S *>(base + bytes * e);
@@ -301,12 +340,29 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
     F.adj[i] = M.adj[i];
   for (int i = t; i < ns; i += 64)
     F.shapeFriction[i] = M.sfriction[i];
+  if (t == 0) {
+    int pos = 0;
+    F.colorStart[0] = 0;
+    for (int c = 0; c < 2; ++c) {
+      for (int b = 0; b < nb; ++b)
+        if (M.mass[b] > 0 && M.colors[b] == c)
+          F.order[pos++] = b;
+      F.colorStart[c + 1] = pos;
+    }
+  }
 
   State *gs = valid ? &blobAt<State>(args.states, args.blobBytes, e) : nullptr;
   if (valid)
     copyEnv<State>(reinterpret_cast<unsigned *>(&E.s), reinterpret_cast<const unsigned *>(gs), lane,
                    L, gs->ngc, gs->nsc);
   __syncthreads();
+  // The staged default schedule applies to this env while no body-body
+  // contact recolours it and its dynamic bodies are the model's.
+  int massPattern = 0;
+  if (valid)
+    for (int b = lane; b < nb; b += L)
+      massPattern |= (E.s.mass[b] > 0) != (M.mass[b] > 0);
+  const bool defaultSchedule = groupOr<L>(massPattern) == 0;
 
   // ---- controls (extension.cu:87-110 / kernel.cuh:448-466) ----
   int bad = 0;
@@ -427,36 +483,83 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
       };
       V3<R> chosen[4];
       int n = 0;
+      if (count <= kCachedPoints) {
+        // Predicted heights and world xy of every point, evaluated once and
+        // scanned by the four passes (same expressions, same order of scan).
+        R wz[kCachedPoints], wx[kCachedPoints], wy[kCachedPoints];
 #pragma unroll
-      for (int pk = 0; pk < 4; ++pk) {
-        if (n < pk)
-          break;
-        int best = -1;
-        R lowest = R(INFINITY);
-        V3<R> bestLocal{0, 0, 0}, bestWorld{0, 0, 0};
-        for (int k = 0; k < count; ++k) {
-          V3<R> local = pointOf(k), world = x + rotate(q, local);
-          V3<R> vel = v + cross(w, world - x);
-          R z = mn(world.z, world.z + h * vel.z + h * h * gz);
-          if (double(z) >= .003 || z >= lowest)
-            continue;
-          bool dup = false;
-#pragma unroll
-          for (int cc = 0; cc < 4; ++cc)
-            if (cc < pk && double(mhypot(chosen[cc].x - world.x, chosen[cc].y - world.y)) < .005)
-              dup = true;
-          if (dup)
-            continue;
-          best = k;
-          lowest = z;
-          bestLocal = local;
-          bestWorld = world;
+        for (int k = 0; k < kCachedPoints; ++k) {
+          if (k < count) {
+            V3<R> world = x + rotate(q, pointOf(k));
+            V3<R> vel = v + cross(w, world - x);
+            wz[k] = mn(world.z, world.z + h * vel.z + h * h * gz);
+            wx[k] = world.x;
+            wy[k] = world.y;
+          }
         }
-        if (best >= 0) {
-          picks[r][pk] = best;
-          pickLocal[r][pk] = bestLocal;
-          chosen[pk] = bestWorld;
-          n = pk + 1;
+#pragma unroll
+        for (int pk = 0; pk < 4; ++pk) {
+          if (n < pk)
+            break;
+          int best = -1;
+          R lowest = R(INFINITY), bx = 0, by = 0;
+#pragma unroll
+          for (int k = 0; k < kCachedPoints; ++k) {
+            if (k >= count)
+              break;
+            if (double(wz[k]) >= .003 || wz[k] >= lowest)
+              continue;
+            bool dup = false;
+#pragma unroll
+            for (int cc = 0; cc < 4; ++cc)
+              if (cc < pk && double(mhypot(chosen[cc].x - wx[k], chosen[cc].y - wy[k])) < .005)
+                dup = true;
+            if (dup)
+              continue;
+            best = k;
+            lowest = wz[k];
+            bx = wx[k];
+            by = wy[k];
+          }
+          if (best >= 0) {
+            picks[r][pk] = best;
+            pickLocal[r][pk] = pointOf(best);
+            chosen[pk] = V3<R>{bx, by, lowest};
+            n = pk + 1;
+          }
+        }
+      } else {
+#pragma unroll
+        for (int pk = 0; pk < 4; ++pk) {
+          if (n < pk)
+            break;
+          int best = -1;
+          R lowest = R(INFINITY);
+          V3<R> bestLocal{0, 0, 0}, bestWorld{0, 0, 0};
+          for (int k = 0; k < count; ++k) {
+            V3<R> local = pointOf(k), world = x + rotate(q, local);
+            V3<R> vel = v + cross(w, world - x);
+            R z = mn(world.z, world.z + h * vel.z + h * h * gz);
+            if (double(z) >= .003 || z >= lowest)
+              continue;
+            bool dup = false;
+#pragma unroll
+            for (int cc = 0; cc < 4; ++cc)
+              if (cc < pk && double(mhypot(chosen[cc].x - world.x, chosen[cc].y - world.y)) < .005)
+                dup = true;
+            if (dup)
+              continue;
+            best = k;
+            lowest = z;
+            bestLocal = local;
+            bestWorld = world;
+          }
+          if (best >= 0) {
+            picks[r][pk] = best;
+            pickLocal[r][pk] = bestLocal;
+            chosen[pk] = bestWorld;
+            n = pk + 1;
+          }
         }
       }
       npick[r] = n;
@@ -629,10 +732,25 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
     }
     __syncthreads();
     // ---------------- colours (kernel.cuh:596-598, 717-720) -------------
-    if (active && lane == 0) {
-      int nsc = 0;
-      for (int pi = 0; pi < np; ++pi)
-        nsc += E.pairHit[pi];
+    int pairHits = 0;
+    for (int pi = 0; pi < np; ++pi)
+      pairHits += E.pairHit[pi];
+    if (active && pairHits == 0 && defaultSchedule) {
+      for (int b = lane; b < nb; b += L) {
+        E.s.colors[b] = M.colors[b];
+        E.order[b] = F.order[b];
+      }
+      if (lane < 3)
+        E.colorStart[lane] = F.colorStart[lane];
+      if (lane < 8)
+        E.stepDiag[lane] = 0;
+      if (lane == 0) {
+        E.s.nsc = 0;
+        E.s.colorCount = 2;
+        E.done = 0;
+      }
+    } else if (active && lane == 0) {
+      int nsc = pairHits;
       E.s.nsc = nsc < CS ? nsc : CS;
       for (int b = 0; b < nb; ++b)
         E.s.colors[b] = M.colors[b];

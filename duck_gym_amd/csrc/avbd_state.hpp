@@ -59,6 +59,9 @@ template <class R, int B, int J> struct Frames {
   R lo[J], hi[J], armature[J];
   int adjStart[B + 1], adj[2 * J];
   R shapeFriction[kMaxModelShapes];
+  // Colour schedule without body-body contacts (model colours, bodies of
+  // non-zero model mass in index order within each colour).
+  int order[B], colorStart[3];
 };
 
 // Ground contact (normal = +z, anchor on the plane).  id packs
