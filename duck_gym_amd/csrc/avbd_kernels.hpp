@@ -809,6 +809,12 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
         E.q0[1][b] = q.x;
         E.q0[2][b] = q.y;
         E.q0[3][b] = q.z;
+        {
+          R iw[6];
+          inertiaWorld(q, stp.Inertia(b), iw);
+          for (int k = 0; k < 6; ++k)
+            E.Iw[k][b] = iw[k];
+        }
         uint64_t gm = 0;
         for (int i = 0; i < E.s.ngc; ++i)
           if (gcBody(E.s.gc[i].id) == b)

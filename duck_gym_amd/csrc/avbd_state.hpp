@@ -116,6 +116,7 @@ template <class R, int B, int J, int CG, int CS> struct EnvLds {
   EnvState<R, B, J, CG, CS> s;
   // per-step scratch
   R x0[3][B], q0[4][B], xp[3][B], qp[4][B];
+  R Iw[6][B]; // world inertia at q0 (xx yy zz xy xz yz)
   R c0[7][J], angle0[J], velocity0[J];
   R stepDiag[8];
   uint64_t gmask[B];

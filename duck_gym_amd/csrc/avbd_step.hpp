@@ -39,25 +39,6 @@ template <class R> struct Hess {
   R g[6];
 };
 
-// Row (t, r) with t = s e_k: g += J f, H += (k J) J^T on the lower triangle.
-// Entries multiplied by an exact zero of J are skipped (they add +-0).
-template <class R> DUCK_HD void stampLinear(Hess<R> &H, int k, R s, V3<R> r, R f, R kk) {
-  H.g[k] += s * f;
-  H.g[3] += r.x * f;
-  H.g[4] += r.y * f;
-  H.g[5] += r.z * f;
-  H.h[tri(k, k)] += kk * s * s;
-  R r0 = kk * r.x, r1 = kk * r.y, r2 = kk * r.z;
-  H.h[tri(3, k)] += r0 * s;
-  H.h[tri(4, k)] += r1 * s;
-  H.h[tri(5, k)] += r2 * s;
-  H.h[tri(3, 3)] += r0 * r.x;
-  H.h[tri(4, 3)] += r1 * r.x;
-  H.h[tri(4, 4)] += r1 * r.y;
-  H.h[tri(5, 3)] += r2 * r.x;
-  H.h[tri(5, 4)] += r2 * r.y;
-  H.h[tri(5, 5)] += r2 * r.z;
-}
 // Row (0, r).
 template <class R> DUCK_HD void stampAngular(Hess<R> &H, V3<R> r, R f, R kk) {
   H.g[3] += r.x * f;
@@ -83,6 +64,57 @@ template <class R> DUCK_HD void stampFull(Hess<R> &H, V3<R> t, V3<R> r, R f, R k
       H.h[tri(i, j)] += ki * J[j];
   }
 }
+// Row with t = s e_k and r x e_k (a hinge anchor row or a ground-contact
+// row): only the entries the unit axis makes non-zero are formed.
+template <class R> DUCK_HD void stampAxisRow(Hess<R> &H, int k, R s, V3<R> r, R f, R kk) {
+  // r x e_k = (0, z, -y), (-z, 0, x), (y, -x, 0) for k = 0, 1, 2
+  R u0 = k == 0 ? R(0) : (k == 1 ? -r.z : r.y);
+  R u1 = k == 1 ? R(0) : (k == 0 ? r.z : -r.x);
+  R u2 = k == 2 ? R(0) : (k == 0 ? -r.y : r.x);
+  H.g[k] += s * f;
+  H.h[tri(k, k)] += kk;
+  R ks = kk * s;
+  if (k != 0) {
+    H.g[3] += u0 * f;
+    H.h[tri(3, k)] += ks * u0;
+    H.h[tri(3, 3)] += (kk * u0) * u0;
+  }
+  if (k != 1) {
+    H.g[4] += u1 * f;
+    H.h[tri(4, k)] += ks * u1;
+    H.h[tri(4, 4)] += (kk * u1) * u1;
+  }
+  if (k != 2) {
+    H.g[5] += u2 * f;
+    H.h[tri(5, k)] += ks * u2;
+    H.h[tri(5, 5)] += (kk * u2) * u2;
+  }
+  // the one off-diagonal rotational entry between the two non-zero components
+  if (k == 0)
+    H.h[tri(5, 4)] += (kk * u2) * u1;
+  else if (k == 1)
+    H.h[tri(5, 3)] += (kk * u2) * u0;
+  else
+    H.h[tri(4, 3)] += (kk * u1) * u0;
+}
+
+// Column norms, per unit |f|, of 0.5 (r f^T + f r^T) - (r.f) I for f along
+// e_k (k = 0, 1, 2): with {i, j} the other two axes, column k is
+// 0.5 sqrt(r_i^2 + r_j^2) and column i is sqrt(r_i^2 / 4 + r_k^2).
+template <class R> DUCK_HD void axisGeometricNorms(V3<R> r, R g[3][3]) {
+  const R q0 = r.x * r.x, q1 = r.y * r.y, q2 = r.z * r.z;
+  const R h0 = R(0.25) * q0, h1 = R(0.25) * q1, h2 = R(0.25) * q2;
+  g[0][0] = R(0.5) * fsqrt(q1 + q2);
+  g[0][1] = fsqrt(h1 + q0);
+  g[0][2] = fsqrt(h2 + q0);
+  g[1][0] = fsqrt(h0 + q1);
+  g[1][1] = R(0.5) * fsqrt(q0 + q2);
+  g[1][2] = fsqrt(h2 + q1);
+  g[2][0] = fsqrt(h0 + q2);
+  g[2][1] = fsqrt(h1 + q2);
+  g[2][2] = R(0.5) * fsqrt(q0 + q1);
+}
+
 // Diagonal majorisation of the rotational geometric stiffness
 // (kernel.cuh:283-301).  For float, 0.5*x - y in float equals the reference's
 // double evaluation rounded to float (no double rounding can occur).
@@ -168,8 +200,6 @@ template <class R> DUCK_HD R logJacobianCoef(R a) {
 template <class R> DUCK_HD V3<R> unitAxis(int k) {
   return V3<R>{k == 0 ? R(1) : R(0), k == 1 ? R(1) : R(0), k == 2 ? R(1) : R(0)};
 }
-// r x e_k with the exact zero the general cross product produces.
-template <class R> DUCK_HD V3<R> crossUnit(V3<R> r, int k) { return cross(r, unitAxis<R>(k)); }
 
 // Coulomb-projected contact force (kernel.cuh:304-315).
 template <class R> DUCK_HD V3<R> contactForce(V3<R> C, const R lambda[3], const R penalty[3],
@@ -200,6 +230,26 @@ __device__ __forceinline__ double pairSwap(double v) {
   const unsigned lo = __builtin_amdgcn_update_dpp(0, int(unsigned(b)), 0x128, 0xF, 0xF, false);
   const unsigned hi = __builtin_amdgcn_update_dpp(0, int(unsigned(b >> 32)), 0x128, 0xF, 0xF, false);
   return __longlong_as_double(static_cast<long long>((static_cast<unsigned long long>(hi) << 32) | lo));
+}
+
+// R diag(I) R^T of the body inertia at orientation q, as its six entries
+// (xx, yy, zz, xy, xz, yz), and the product of such a matrix with v.
+template <class R> DUCK_HD void inertiaWorld(Q4<R> q, V3<R> I, R out[6]) {
+  V3<R> c0 = rotate(q, V3<R>{1, 0, 0}), c1 = rotate(q, V3<R>{0, 1, 0}),
+        c2 = rotate(q, V3<R>{0, 0, 1}); // columns of R
+  auto entry = [&](R a0, R a1, R a2, R b0, R b1, R b2) {
+    return (a0 * I.x * b0 + a1 * I.y * b1) + a2 * I.z * b2;
+  };
+  out[0] = entry(c0.x, c1.x, c2.x, c0.x, c1.x, c2.x);
+  out[1] = entry(c0.y, c1.y, c2.y, c0.y, c1.y, c2.y);
+  out[2] = entry(c0.z, c1.z, c2.z, c0.z, c1.z, c2.z);
+  out[3] = entry(c0.x, c1.x, c2.x, c0.y, c1.y, c2.y);
+  out[4] = entry(c0.x, c1.x, c2.x, c0.z, c1.z, c2.z);
+  out[5] = entry(c0.y, c1.y, c2.y, c0.z, c1.z, c2.z);
+}
+template <class R> DUCK_HD V3<R> symApply(const R m[6], V3<R> v) {
+  return {(m[0] * v.x + m[3] * v.y) + m[4] * v.z, (m[3] * v.x + m[1] * v.y) + m[5] * v.z,
+          (m[4] * v.x + m[5] * v.y) + m[2] * v.z};
 }
 
 template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
@@ -340,9 +390,10 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
         V3<R> e = unitAxis<R>(k);
         rotJ[k] = (e - R(0.5) * cross(theta, e)) + coef * cross(theta, cross(theta, e));
       }
-      V3<R> It = inertiaApply(q0, I, theta, false);
-      V3<R> IJ[3] = {inertiaApply(q0, I, rotJ[0], false), inertiaApply(q0, I, rotJ[1], false),
-                     inertiaApply(q0, I, rotJ[2], false)};
+      // World inertia at q0, formed once per step by the predictor.
+      const R Iw[6] = {E.Iw[0][bi], E.Iw[1][bi], E.Iw[2][bi], E.Iw[3][bi], E.Iw[4][bi], E.Iw[5][bi]};
+      V3<R> It = symApply(Iw, theta);
+      V3<R> IJ[3] = {symApply(Iw, rotJ[0]), symApply(Iw, rotJ[1]), symApply(Iw, rotJ[2])};
 #pragma unroll
       for (int k = 0; k < 3; ++k) {
         H.g[3 + k] = fdivInv(dot(rotJ[k], It), h2, ih2);
@@ -358,6 +409,11 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
       const R s = parent ? R(1) : R(-1);
       JointEval je = evalJoint(ji);
       const int rows = F.limited[ji] ? 7 : 5;
+      // Anchor rows: J_k = [s e_k, r x e_k] with r = ra (parent) or -rb
+      // (child); their geometric terms share r.
+      const V3<R> r = parent ? je.ra : -je.rb;
+      R geo[3][3];
+      axisGeometricNorms(r, geo);
 #pragma unroll
       for (int k = 0; k < 7; ++k) {
         if (k >= rows)
@@ -370,10 +426,11 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
           f = mn(f, R(0));
         if (k < 5 || f < 0) {
           if (k < 3) {
-            V3<R> rrow = parent ? crossUnit(je.ra, k) : -crossUnit(je.rb, k);
-            stampLinear(H, k, s, rrow, f, pen);
-            V3<R> e{k == 0 ? f : R(0), k == 1 ? f : R(0), k == 2 ? f : R(0)};
-            geometricAdd(H, parent ? je.ra : -je.rb, e);
+            stampAxisRow(H, k, s, r, f, pen);
+            const R af = mabs(f);
+            H.h[tri(3, 3)] += af * geo[k][0];
+            H.h[tri(4, 4)] += af * geo[k][1];
+            H.h[tri(5, 5)] += af * geo[k][2];
           } else if (k < 5) {
             V3<R> t = k == 3 ? je.t1 : je.t2;
             stampAngular(H, parent ? cross(t, je.axisB) : cross(je.axisB, t), f, pen);
@@ -383,9 +440,12 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
           }
         }
       }
+      // Rows along the hinge axis (kernel.cuh:893-913): implicit torque-
+      // limited PD potential, damping/armature, dry friction -- one stamp
+      // with the summed force and stiffness.
       const V3<R> J5 = parent ? -je.axis : je.axis;
+      R axisForce = 0, axisStiff = 0;
       if (implicitDrive) {
-        // Implicit torque-limited PD potential (kernel.cuh:893-902).
         R kp = E.s.kp[ji], maxT = E.s.maxTorque[ji];
         R drive = kp * wrapAngle(je.angle - E.s.target[ji]) - E.s.torque[ji];
         R ks = kp;
@@ -394,20 +454,25 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
             ks = 0;
           drive = clampv(drive, -maxT, maxT);
         }
-        stampAngular(H, J5, drive, ks);
+        axisForce = drive;
+        axisStiff = ks;
       }
       R damping = E.s.damping[ji], armature = F.armature[ji];
       R delta = wrapAngle(je.angle - E.angle0[ji]);
       const R dh = fdivInv(damping, h, ih), ah = fdivInv(armature, h2, ih2);
       R stiff = dh + ah;
-      R force = dh * delta + ah * (delta - h * E.velocity0[ji]);
-      if (stiff > 0)
-        stampAngular(H, J5, force, stiff);
+      if (stiff > 0) {
+        axisForce += dh * delta + ah * (delta - h * E.velocity0[ji]);
+        axisStiff += stiff;
+      }
       R fl = E.s.frictionloss[ji];
       if (fl > 0) {
         R trial = E.s.lambdaF[ji] + E.s.penaltyF[ji] * delta;
-        stampAngular(H, J5, clampv(trial, -fl, fl), mabs(trial) < fl ? E.s.penaltyF[ji] : R(0));
+        axisForce += clampv(trial, -fl, fl);
+        if (mabs(trial) < fl)
+          axisStiff += E.s.penaltyF[ji];
       }
+      stampAngular(H, J5, axisForce, axisStiff);
     }
     // Ground contacts of this body, in list order.
     int nth = 0;
@@ -419,9 +484,9 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
       V3<R> C = groundC(c, ra);
       V3<R> f = contactForce(C, c.lambda, c.penalty, groundFriction(gcShape(c.id)));
       if (f.z < 0) {
-        stampLinear(H, 0, R(1), crossUnit(ra, 0), f.x, c.penalty[0]);
-        stampLinear(H, 1, R(1), crossUnit(ra, 1), f.y, c.penalty[1]);
-        stampLinear(H, 2, R(1), crossUnit(ra, 2), f.z, c.penalty[2]);
+        stampAxisRow(H, 0, R(1), ra, f.x, c.penalty[0]);
+        stampAxisRow(H, 1, R(1), ra, f.y, c.penalty[1]);
+        stampAxisRow(H, 2, R(1), ra, f.z, c.penalty[2]);
         geometricAdd(H, ra, f);
       }
     }
