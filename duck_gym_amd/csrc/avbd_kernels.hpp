@@ -72,14 +72,17 @@ template <class S> __device__ __forceinline__ S &blobAt(unsigned char *base, lon
 
 // Copy one environment's blob (header + live contacts) between HBM and LDS
 // with the L lanes of its group.
+// `from` skips the leading header words (the step's write-back starts at x:
+// mass, inertia and friction only change on reset).
 template <class S>
-__device__ void copyEnv(unsigned *dst, const unsigned *src, int lane, int L, int ngc, int nsc) {
+__device__ void copyEnv(unsigned *dst, const unsigned *src, int lane, int L, int ngc, int nsc,
+                        int from = 0) {
   constexpr int header = int(headerBytes<S>() / 4);
   constexpr int CGcap = int(sizeof(S::gc) / sizeof(S::gc[0]));
   constexpr int CScap = int(sizeof(S::sc) / sizeof(S::sc[0]));
   ngc = ngc < 0 ? 0 : (ngc > CGcap ? CGcap : ngc);
   nsc = nsc < 0 ? 0 : (nsc > CScap ? CScap : nsc);
-  for (int i = lane; i < header; i += L)
+  for (int i = from + lane; i < header; i += L)
     dst[i] = src[i];
   constexpr int gcWords = int(sizeof(decltype(S::gc[0])) / 4);
   const int gcStart = header, gcEnd = header + ngc * gcWords;
@@ -1006,7 +1009,7 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
   }
   if (valid)
     copyEnv<State>(reinterpret_cast<unsigned *>(gs), reinterpret_cast<const unsigned *>(&E.s), lane,
-                   L, E.s.ngc, E.s.nsc);
+                   L, E.s.ngc, E.s.nsc, int(offsetof(State, x) / 4));
 }
 
 } // namespace duckhip

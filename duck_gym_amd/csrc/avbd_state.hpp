@@ -98,14 +98,16 @@ enum DiagSlot { kJointError, kPenetration, kContacts, kConverged, kAxisError, kI
 
 // Persistent per-env state; the HBM blob is exactly this struct.
 template <class R, int B, int J, int CG, int CS> struct EnvState {
-  R x[3][B], q[4][B], v[3][B], w[3][B];
+  // Set by reset only (the step reads them and never writes them back).
   R mass[B], inertia[3][B];
+  R friction; // per-env ground friction; < 0 selects the shape friction
+  // Advanced by every step.
+  R x[3][B], q[4][B], v[3][B], w[3][B];
   R force[3];
   R lambda[7][J], penalty[7][J];
   R lambdaF[J], penaltyF[J];
   R target[J], kp[J], maxTorque[J], torque[J], frictionloss[J], damping[J];
   R diag[8];
-  R friction; // per-env ground friction; < 0 selects the shape friction
   int failed, ngc, nsc, colorCount;
   int colors[B]; // colouring of the last step (model colours + fresh ones)
   GroundContact<R> gc[CG];
