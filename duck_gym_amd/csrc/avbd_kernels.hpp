@@ -340,7 +340,7 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
   for (int i = t; i <= nb; i += 64)
     F.adjStart[i] = M.adjStart[i];
   for (int i = t; i < 2 * nj; i += 64)
-    F.adj[i] = M.adj[i];
+    F.adj[i] = M.adj[i] | (M.ja[M.adj[i]] << 8) | (M.jb[M.adj[i]] << 16);
   for (int i = t; i < ns; i += 64)
     F.shapeFriction[i] = M.sfriction[i];
   if (t == 0) {
@@ -851,6 +851,18 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
     }
     int colours = waveMaxInt(active ? E.s.colorCount : 0);
     __syncthreads();
+    // When each of the first two colours fits in one pass of the block-solve
+    // slots, every lane's body for them is fixed for the whole step.
+    bool twoColourSlots = false;
+    int mine0 = -1, mine1 = -1;
+    if (active) {
+      const int c0 = E.colorStart[0], c1 = E.colorStart[1], c2 = E.colorStart[2];
+      twoColourSlots = c1 - c0 <= L / P && c2 - c1 <= L / P;
+      if (c0 + slot < c1)
+        mine0 = E.order[c0 + slot];
+      if (c1 + slot < c2)
+        mine1 = E.order[c1 + slot];
+    }
     // ---------------- AVBD iterations (kernel.cuh:979-1063) ---------------
     for (int it = 0; it < M.iterations; ++it) {
       const bool work = active && !E.done;
@@ -858,9 +870,16 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
         break;
       R maxUpdate = 0;
       for (int c = 0; c < colours; ++c) {
-        if (work && c < E.s.colorCount)
-          for (int k = E.colorStart[c] + slot; k < E.colorStart[c + 1]; k += L / P)
-            maxUpdate = mx(maxUpdate, stp.updateBody(E.order[k], true, part));
+        if (work && c < E.s.colorCount) {
+          if (c < 2 && twoColourSlots) {
+            const int bi = c == 0 ? mine0 : mine1;
+            if (bi >= 0)
+              maxUpdate = mx(maxUpdate, stp.updateBody(bi, true, part));
+          } else {
+            for (int k = E.colorStart[c] + slot; k < E.colorStart[c + 1]; k += L / P)
+              maxUpdate = mx(maxUpdate, stp.updateBody(E.order[k], true, part));
+          }
+        }
         __syncthreads();
       }
       maxUpdate = groupMax<L>(maxUpdate);

@@ -57,7 +57,8 @@ template <class R, int B, int J> struct Frames {
   int a[J], b[J], limited[J];
   R ra[3][J], rb[3][J], axisA[3][J], axisB[3][J], tangentA[3][J], tangentB[3][J];
   R lo[J], hi[J], armature[J];
-  int adjStart[B + 1], adj[2 * J];
+  int adjStart[B + 1];
+  int adj[2 * J]; // hinge | body a << 8 | body b << 16, grouped by body
   R shapeFriction[kMaxModelShapes];
   // Colour schedule without body-body contacts (model colours, bodies of
   // non-zero model mass in index order within each colour).

@@ -313,9 +313,9 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
     R C[7], angle;
     V3<R> ra, rb, axis, axisB, t1, t2;
   };
-  DUCK_HD JointEval evalJoint(int ji) const {
+  DUCK_HD JointEval evalJoint(int ji) const { return evalJoint(ji, F.a[ji], F.b[ji]); }
+  DUCK_HD JointEval evalJoint(int ji, int a, int b) const {
     JointEval o;
-    int a = F.a[ji], b = F.b[ji];
     Q4<R> qa = Q(a), qb = Q(b);
     o.ra = rotate(qa, frame(F.ra, ji));
     o.rb = rotate(qb, frame(F.rb, ji));
@@ -403,11 +403,19 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
       }
     }
     const R alpha = M.alpha;
-    for (int adj = F.adjStart[bi] + (P == 2 ? 1 - part : 0); adj < F.adjStart[bi + 1]; adj += P) {
-      const int ji = F.adj[adj];
-      const bool parent = bi == F.a[ji];
+    // Adjacency entries pack (hinge, body a, body b); the next entry is
+    // fetched while the current hinge is assembled.
+    const int adjEnd = F.adjStart[bi + 1];
+    int adj = F.adjStart[bi] + (P == 2 ? 1 - part : 0);
+    int packed = adj < adjEnd ? F.adj[adj] : 0;
+    for (; adj < adjEnd; adj += P) {
+      const int cur = packed;
+      if (adj + P < adjEnd)
+        packed = F.adj[adj + P];
+      const int ji = cur & 255, ja = (cur >> 8) & 255, jb = (cur >> 16) & 255;
+      const bool parent = bi == ja;
       const R s = parent ? R(1) : R(-1);
-      JointEval je = evalJoint(ji);
+      JointEval je = evalJoint(ji, ja, jb);
       const int rows = F.limited[ji] ? 7 : 5;
       // Anchor rows: J_k = [s e_k, r x e_k] with r = ra (parent) or -rb
       // (child); their geometric terms share r.
