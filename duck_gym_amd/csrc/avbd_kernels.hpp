@@ -325,6 +325,7 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
     F.a[j] = M.ja[j];
     F.b[j] = M.jb[j];
     F.limited[j] = M.limited[j];
+#pragma unroll
     for (int k = 0; k < 3; ++k) {
       F.ra[k][j] = M.ra[k][j];
       F.rb[k][j] = M.rb[k][j];
@@ -787,6 +788,7 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
     if (active) {
       for (int ji = lane; ji < nj; ji += L) {
         auto je = stp.evalJoint(ji);
+#pragma unroll
         for (int k = 0; k < 7; ++k)
           E.c0[k][ji] = je.C[k];
         E.angle0[ji] = je.angle;
@@ -794,6 +796,7 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
         E.s.penaltyF[ji] = clampv(E.s.penaltyF[ji] * gamma, R(1), R(1e7));
         const int a = F.a[ji], b = F.b[ji];
         E.velocity0[ji] = dot(stp.Omega(b) - stp.Omega(a), je.axis);
+#pragma unroll
         for (int k = 0; k < 7; ++k) {
           E.s.lambda[k][ji] *= ag;
           E.s.penalty[k][ji] =
@@ -806,6 +809,7 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
       for (int b = lane; b < nb; b += L) {
         V3<R> x = stp.X(b);
         Q4<R> q = stp.Q(b);
+#pragma unroll
         for (int k = 0; k < 3; ++k)
           E.x0[k][b] = comp(x, k);
         E.q0[0][b] = q.w;
@@ -839,6 +843,7 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
         V3<R> spin = -cross(w, stp.inertiaApply(q, I, w, false));
         V3<R> wp = w + h * stp.inertiaApply(q, I, spin, true);
         Q4<R> qp = fexpmap(h * wp) * q;
+#pragma unroll
         for (int k = 0; k < 3; ++k)
           E.xp[k][b] = comp(xp, k);
         E.qp[0][b] = qp.w;
@@ -888,7 +893,10 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
         for (int ji = lane; ji < nj; ji += L) {
           auto je = stp.evalJoint(ji);
           const int rows = F.limited[ji] ? 7 : 5;
-          for (int k = 0; k < rows; ++k) {
+#pragma unroll
+          for (int k = 0; k < 7; ++k) {
+            if (k >= rows)
+              break;
             R c0 = E.c0[k][ji];
             R c = je.C[k] - alpha * (k < 5 ? c0 : mn(c0, R(0)));
             R f = E.s.lambda[k][ji] + E.s.penalty[k][ji] * c;
@@ -920,6 +928,7 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
           bool stick = trial <= -mu * f.z && double(mhypot(C.x, C.y)) < 1e-5;
           c.id = (c.id & 0x7fffffff) | (stick ? int(0x80000000u) : 0);
           R fk[3] = {f.x, f.y, f.z}, Ck[3] = {C.x, C.y, C.z};
+#pragma unroll
           for (int k = 0; k < 3; ++k) {
             c.lambda[k] = fk[k];
             if (f.z < 0 && (k == 2 || trial <= -mu * f.z))
@@ -936,6 +945,7 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
           bool stick = trial <= -c.friction * f.z && double(mhypot(C.x, C.y)) < 1e-5;
           c.id = (c.id & 0x7fffffff) | (stick ? int(0x80000000u) : 0);
           R fk[3] = {f.x, f.y, f.z}, Ck[3] = {C.x, C.y, C.z};
+#pragma unroll
           for (int k = 0; k < 3; ++k) {
             c.lambda[k] = fk[k];
             if (f.z < 0 && (k == 2 || trial <= -c.friction * f.z))
@@ -963,6 +973,7 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
         V3<R> x = stp.X(b), x0{E.x0[0][b], E.x0[1][b], E.x0[2][b]};
         V3<R> v = (x - x0) * invh;
         V3<R> w = flogmap(stp.Q(b) * conj(stp.Q0(b))) * invh;
+#pragma unroll
         for (int k = 0; k < 3; ++k) {
           E.s.v[k][b] = comp(v, k);
           E.s.w[k][b] = comp(w, k);
@@ -979,8 +990,10 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
     if (active) {
       for (int ji = lane; ji < nj; ji += L) {
         auto je = stp.evalJoint(ji);
+#pragma unroll
         for (int k = 0; k < 3; ++k)
           jointErr = mx(jointErr, mabs(je.C[k]));
+#pragma unroll
         for (int k = 3; k < 5; ++k)
           axisErr = mx(axisErr, mabs(je.C[k]));
       }
