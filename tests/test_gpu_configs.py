@@ -1,0 +1,189 @@
+"""The workload configurations beyond the fixed-HOME benchmark, at their full
+sizes on the GPU, with parity against the CPU oracle on sampled
+environments:
+
+* servo-target sweep (4096 envs, float32): targets HOME + U(-0.3, 0.3)
+  redrawn every 4 steps per env, 8-vertex foot hulls, body-body contact
+  between the leg chains, per-env ground friction U(0.5, 1.2);
+* drop/jump stress (16384 envs, float32, 15 iterations): base height
+  U(0.15, 0.35) m, base rotation +-0.5 rad, base velocity N(0, 0.5),
+  masses x U(0.9, 1.1);
+* tensor-env rollout (32768 envs, float32): 48-wide observation,
+  locomotion reward, reset on falls below 0.08 m, actions from a randomly
+  initialised 48-256-128-14 ELU policy.
+
+Parity on sampled envs follows the one-step contract: the sampled GPU envs
+are seeded with the oracle's state mid-trajectory and stepped once; contact
+sets and colours must be identical and poses within 1e-5.  The full-size
+runs check what holds at any size: finite states, no numerical failures,
+contact counts within capacity, and the tensor-env bookkeeping."""
+
+import numpy as np
+import pytest
+import torch
+
+from duck_gym_amd import CudaBatch
+from duck_gym_amd import workloads as W
+from duck_gym_amd.microduck import model_text, write_model
+from oracle import task_oracle as T
+from parity_support import compare_env, oracle_envs, oracle_state, seed_batch
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+DT, KP, SEED = 0.005, 8.0, 20260927
+SAMPLE = np.array([0, 1, 77, 1023, 2048, 3001, 4094, 4095])
+
+
+def _ext_friction(envs, seed):
+    ext = np.zeros((len(envs), 5))
+    ext[:, 0] = W.ground_friction(envs, seed)
+    ext[:, 1] = 1.0
+    return ext
+
+
+def _reset(batch, q, root, ext):
+    n = batch.num_envs
+    dt = batch.dtype
+    batch.reset(torch.ones(n, dtype=torch.bool, device=DEV), torch.tensor(q, dtype=dt, device=DEV),
+                torch.tensor(root, dtype=dt, device=DEV), torch.tensor(ext, dtype=dt, device=DEV))
+
+
+def _oracle_reset(o, q, root, ext):
+    o.reset(q, root)
+    o.set_mass_scale(ext[1])
+    o.set_root_velocity(ext[2:5])
+    o.set_friction(ext[0])
+
+
+def _one_step_parity(model, iterations, q, root, ext, targets_at, steps, checkpoints):
+    """Sampled envs: oracles run the trajectory; at each checkpoint a GPU batch
+    of the sampled envs is seeded with the oracle states and stepped once."""
+    E = len(q)
+    oracles = oracle_envs(model, E, DT, iterations, False)
+    for o, qe, re, xe in zip(oracles, q, root, ext):
+        _oracle_reset(o, qe, re, xe)
+    batch = CudaBatch(model, E, DT, iterations, 0, False)
+    _reset(batch, q, root, ext)  # per-env friction and masses
+    codec = batch.codec()
+    fg = torch.zeros(E, 3, device=DEV)
+    checked = contacts = 0
+    for step in range(steps):
+        targets = targets_at(step)
+        if step in checkpoints:
+            seed_batch(batch, oracles)
+            batch.step(torch.tensor(targets, dtype=torch.float32, device=DEV), fg, 1, KP, 0.0)
+        for o, t in zip(oracles, targets):
+            o.step(t, None, 1, KP, 0.0)
+        if step in checkpoints:
+            raw = batch.export_state().cpu().numpy()
+            for e, o in enumerate(oracles):
+                ref = oracle_state(o)
+                compare_env(codec.decode(raw[e]), ref, 1e-5, f"step {step} env {e}")
+                contacts += len(ref["gc"]) + len(ref["sc"])
+                checked += 1
+    return checked, contacts, oracles
+
+
+def test_servo_sweep_with_body_contacts(tmp_path):
+    model = write_model(tmp_path / "selfc", self_contact=True)
+    home = np.array(model_text()[1]["home"])
+    E = 4096
+    envs = np.arange(E)
+    batch = CudaBatch(model, E, DT, 10, 0, False)
+    _reset(batch, np.tile(home, (E, 1)), np.zeros((E, 6)), _ext_friction(envs, SEED))
+    fg = torch.zeros(E, 3, device=DEV)
+    body_contacts = 0
+    for step in range(48):
+        t = W.servo_targets(home, envs, step, SEED)
+        batch.step(torch.tensor(t, dtype=torch.float32, device=DEV), fg, 1, KP, 0.0)
+        if step % 8 == 7:
+            counts = batch.contact_counts()
+            body_contacts += int(counts[:, 1].sum())
+            assert int(counts[:, 0].max()) <= batch.contact_capacity
+    b, j, d = batch.state()
+    assert bool(torch.isfinite(b).all()) and int((d[:, 5] != 0).sum()) == 0
+    assert body_contacts > 0, "the sweep produced no body-body contacts"
+
+    checked, contacts, _ = _one_step_parity(
+        model, 10, np.tile(home, (len(SAMPLE), 1)), np.zeros((len(SAMPLE), 6)),
+        _ext_friction(SAMPLE, SEED), lambda s: W.servo_targets(home, SAMPLE, s, SEED), 48,
+        {3, 11, 19, 27, 35, 47})
+    assert checked == 6 * len(SAMPLE) and contacts > 0
+
+
+def test_drop_and_jump_stress(tmp_path):
+    model = write_model(tmp_path / "standing")
+    meta = model_text()[1]
+    home = np.array(meta["home"])
+    E = 16384
+    envs = np.arange(E)
+    q, root, ext = W.drop_start(envs, SEED, home, meta["root_height"])
+    batch = CudaBatch(model, E, DT, 15, 0, False)
+    _reset(batch, q, root, ext)
+    target = torch.tensor(np.tile(home, (E, 1)), dtype=torch.float32, device=DEV)
+    fg = torch.zeros(E, 3, device=DEV)
+    peak = 0
+    for step in range(80):
+        batch.step(target, fg, 1, KP, 0.0)
+        if step % 10 == 9:
+            peak = max(peak, int(batch.contact_counts()[:, 0].max()))
+    b, j, d = batch.state()
+    assert bool(torch.isfinite(b).all())
+    assert int((d[:, 5] != 0).sum()) == 0
+    assert 8 <= peak <= batch.contact_capacity
+    # Everything has landed: the lowest body point rests near the ground.
+    assert float(b[:, 1:, 2].min()) > -0.01
+
+    sample = SAMPLE * 4  # spread over the 16384 envs
+    sq, sroot, sext = W.drop_start(sample, SEED, home, meta["root_height"])
+    checked, contacts, _ = _one_step_parity(
+        model, 15, sq, sroot, sext, lambda s: np.tile(home, (len(sample), 1)), 80,
+        {0, 10, 20, 30, 40, 50, 60, 79})
+    assert checked == 8 * len(sample) and contacts > 0
+
+
+def test_tensor_env_rollout_with_policy(tmp_path):
+    from duck_gym_amd.tensor_env import TensorEnv
+
+    write_model(tmp_path)
+    E = 32768
+    env = TensorEnv(tmp_path, E, 10, DT, 4, seed=SEED, task="rollout", episode_seconds=10.0)
+    assert env.obs_dim == 48
+    torch.manual_seed(SEED)
+    policy = torch.nn.Sequential(torch.nn.Linear(48, 256), torch.nn.ELU(), torch.nn.Linear(256, 128),
+                                 torch.nn.ELU(), torch.nn.Linear(128, 14)).to(DEV)
+    obs, _ = env.get_observations()
+    resets = 0
+    with torch.no_grad():
+        for step in range(24):
+            actions = policy(obs)
+            last = env.actions.clone()
+            episode = env.episode_length_buf.clone()
+            obs, reward, done, info = env.step(actions)
+            # Sampled rows of the terminal observation and reward against the
+            # oracle on the post-step state (before the auto-reset).
+            if step % 6 == 5:
+                term = info["terminal_observation"][SAMPLE].cpu().double().numpy()
+                rew = reward[SAMPLE].cpu().double().numpy()
+                # the physics state of non-reset sampled envs is still the post-step one
+                keep = ~done[SAMPLE].cpu().numpy()
+                b, j, d = (x[SAMPLE].cpu().double().numpy() for x in env.native.state())
+                a = torch.clamp(actions[SAMPLE], -1, 1).cpu().double().numpy()
+                failed, r, _, _, _, _ = T.step_outputs(
+                    T.ROLLOUT, b, j, d, a, last[SAMPLE].cpu().double().numpy(), env.meta,
+                    control_dt=env.control_dt, episode=episode[SAMPLE].cpu().numpy(),
+                    max_episode_length=env.max_episode_length,
+                    commands=env.commands[SAMPLE].cpu().double().numpy(),
+                    tracking_sigma=env.tracking_sigma)
+                o = T.observe(T.ROLLOUT, b, j, a, env.meta)
+                np.testing.assert_allclose(term[keep], o[keep], rtol=2e-5, atol=2e-5)
+                np.testing.assert_allclose(rew[keep], r[keep], rtol=2e-5, atol=2e-7)
+                assert not failed[keep].any()
+            resets += int(done.sum())
+            assert bool(torch.isfinite(obs).all()) and bool(torch.isfinite(reward).all())
+            # failures end the episode; reset envs restart their counters
+            assert bool((done >= info["failed"]).all())
+            assert int(env.episode_length_buf[done].abs().sum()) == 0
+    # Reset envs restart with zero episode length; the rest count 24 steps.
+    assert int(env.episode_length_buf.max()) <= 24
+    print(f"rollout: {resets} resets over 24 x {E} env-steps")
