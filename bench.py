@@ -112,6 +112,90 @@ def cpu_baseline(model, home, seconds_budget=12.0):
             "kind": kind, "sample": sample}
 
 
+def other_workload(args):
+    """env-steps/s of the non-headline workloads (same timing protocol)."""
+    import numpy as np
+    import torch
+
+    from duck_gym_amd import CudaBatch
+    from duck_gym_amd import workloads as W
+    from duck_gym_amd.microduck import model_text, write_model
+
+    seed, kp = 20260927, KP
+    meta = model_text()[1]
+    home = np.array(meta["home"])
+    tmp = tempfile.TemporaryDirectory()
+    dev = torch.device("cuda:0")
+    config = {}
+    if args.workload in ("sweep", "drop"):
+        sweep = args.workload == "sweep"
+        E = 4096 if sweep else 16384
+        iterations = 10 if sweep else 15
+        model = write_model(Path(tmp.name) / "m", self_contact=sweep)
+        batch = CudaBatch(model, E, DT, iterations, 0, False)
+        envs = np.arange(E)
+        if sweep:
+            q, root = np.tile(home, (E, 1)), np.zeros((E, 6))
+            ext = np.zeros((E, 5))
+            ext[:, 0], ext[:, 1] = W.ground_friction(envs, seed), 1.0
+        else:
+            q, root, ext = W.drop_start(envs, seed, home, meta["root_height"])
+        t = lambda a: torch.tensor(a, dtype=torch.float32, device=dev)  # noqa: E731
+        batch.reset(torch.ones(E, dtype=torch.bool, device=dev), t(q), t(root), t(ext))
+        forces = torch.zeros(E, 3, device=dev)
+        # Targets for every step, resident in HBM before timing.
+        blocks = [t(W.servo_targets(home, envs, 4 * k, seed) if sweep else np.tile(home, (E, 1)))
+                  for k in range((args.warmup + args.steps) // 4 + 1)]
+        for s in range(args.warmup):
+            batch.step(blocks[s // 4], forces, 1, kp, 0.0)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for s in range(args.warmup, args.warmup + args.steps):
+            batch.step(blocks[s // 4], forces, 1, kp, 0.0)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        failed = int((batch.state()[2][:, 5] != 0).sum())
+        value = E * args.steps / wall
+        config = {"workload": "servo-target sweep, HOME + U(-0.3, 0.3) every 4 steps, body "
+                              "contacts between the leg chains, friction U(0.5, 1.2)" if sweep
+                  else "drop/jump stress: base height U(0.15, 0.35) m, rotation +-0.5 rad, "
+                       "velocity N(0, 0.5), masses x U(0.9, 1.1)",
+                  "envs": E, "iterations": iterations, "dt_s": DT, "failed_envs": failed}
+        ms = wall / args.steps * 1e3
+    else:
+        from duck_gym_amd.tensor_env import TensorEnv
+
+        write_model(Path(tmp.name))
+        E, substeps = 32768, 4
+        env = TensorEnv(Path(tmp.name), E, ITERATIONS, DT, substeps, seed=seed, task="rollout",
+                        episode_seconds=10.0)
+        torch.manual_seed(seed)
+        policy = torch.nn.Sequential(
+            torch.nn.Linear(48, 256), torch.nn.ELU(), torch.nn.Linear(256, 128), torch.nn.ELU(),
+            torch.nn.Linear(128, 14)).to(dev)
+        obs, _ = env.get_observations()
+        with torch.no_grad():
+            for _ in range(args.warmup):
+                obs, _, _, _ = env.step(policy(obs))
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(args.steps):
+                obs, _, _, _ = env.step(policy(obs))
+            torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        value = E * args.steps * substeps / wall
+        ms = wall / args.steps * 1e3
+        config = {"workload": "tensor-env rollout: 48-wide observation, locomotion reward, reset "
+                              "below 0.08 m, random-init 48-256-128-14 ELU policy",
+                  "envs": E, "iterations": ITERATIONS, "dt_s": DT,
+                  "physics_steps_per_control_step": substeps,
+                  "control_steps_per_s": E * args.steps / wall}
+    return {"metric": f"physics env-steps/s ({args.workload} workload)", "value": value,
+            "unit": "env-steps/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "fp32", "data": "synthetic", "config": config}
+
+
 def main():
     p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     p.add_argument("--gpus", type=int, default=1)
@@ -119,6 +203,11 @@ def main():
     p.add_argument("--warmup", type=int, default=100)
     p.add_argument("--envs", type=int, default=ENVS)
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--workload", choices=("home", "sweep", "drop", "rollout"), default="home",
+                   help="home: fixed HOME, 4096 envs (default, the headline line); sweep: "
+                        "servo-target sweep with body contacts and per-env friction; drop: "
+                        "drop/jump stress, 16384 envs, 15 iterations; rollout: tensor-env "
+                        "rollout with a random MLP policy, 32768 envs")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                    help="only run a plain device copy of MIB MiB (three times): the "
                         "reference dispatch for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE")
@@ -140,6 +229,10 @@ def main():
               "exchange, and this build runs on a single-GPU box (use --gpus 1).",
               file=sys.stderr)
         sys.exit(2)
+
+    if args.workload != "home":
+        print(json.dumps(other_workload(args)), flush=True)
+        return
 
     import numpy as np
     import torch
