@@ -19,8 +19,21 @@ template <int N> __device__ __forceinline__ double rowRor(double v) {
 
 // Maximum over the L lanes of an environment, on every one of them.  For
 // L == 16 (one DPP row) four row rotations replace the LDS-crossbar shuffles.
+template <class T> __device__ __forceinline__ T swizzle16(T v);
+template <> __device__ __forceinline__ int swizzle16(int v) {
+  return __builtin_amdgcn_ds_swizzle(v, 0x401F); // lane ^ 16 within 32-lane groups
+}
+template <> __device__ __forceinline__ float swizzle16(float v) {
+  return __int_as_float(swizzle16(__float_as_int(v)));
+}
+template <> __device__ __forceinline__ double swizzle16(double v) {
+  const unsigned long long b = static_cast<unsigned long long>(__double_as_longlong(v));
+  const unsigned lo = swizzle16(int(unsigned(b))), hi = swizzle16(int(unsigned(b >> 32)));
+  return __longlong_as_double(static_cast<long long>((static_cast<unsigned long long>(hi) << 32) | lo));
+}
+
 template <int L, class T> __device__ __forceinline__ T groupMax(T v) {
-  if constexpr (L == 16) {
+  if constexpr (L == 16 || L == 32) {
     T u = rowRor<8>(v);
     v = v > u ? v : u;
     u = rowRor<4>(v);
@@ -29,6 +42,10 @@ template <int L, class T> __device__ __forceinline__ T groupMax(T v) {
     v = v > u ? v : u;
     u = rowRor<1>(v);
     v = v > u ? v : u;
+    if constexpr (L == 32) {
+      u = swizzle16(v);
+      v = v > u ? v : u;
+    }
     return v;
   } else {
 #pragma unroll
@@ -40,11 +57,13 @@ template <int L, class T> __device__ __forceinline__ T groupMax(T v) {
   }
 }
 template <int L> __device__ __forceinline__ int groupOr(int v) {
-  if constexpr (L == 16) {
+  if constexpr (L == 16 || L == 32) {
     v |= rowRor<8>(v);
     v |= rowRor<4>(v);
     v |= rowRor<2>(v);
     v |= rowRor<1>(v);
+    if constexpr (L == 32)
+      v |= swizzle16(v);
     return v;
   } else {
 #pragma unroll
@@ -60,6 +79,23 @@ __device__ __forceinline__ int waveMaxInt(int v) {
     v = v > u ? v : u;
   }
   return v;
+}
+
+// Candidate point k of ground shape si in body coordinates: hull or box
+// corners are stored points; a sphere offers its lowest point and a capsule
+// the lowest points of its two end spheres under the body orientation q.
+template <class R>
+__device__ __forceinline__ V3<R> groundPoint(const DeviceModel<R> &M, const V3<R> *points, int si,
+                                              int k, Q4<R> q) {
+  const int type = M.stype[si];
+  if (type == 1 || type == 3)
+    return points[M.soffset[si] + k];
+  V3<R> c{M.center[0][si], M.center[1][si], M.center[2][si]};
+  V3<R> down = rotate(conj(q), V3<R>{0, 0, -M.size[0][si]});
+  if (type == 0)
+    return c + down;
+  Q4<R> sq{M.sq[0][si], M.sq[1][si], M.sq[2][si], M.sq[3][si]};
+  return (c + rotate(sq, V3<R>{0, 0, (k ? R(1) : R(-1)) * M.size[1][si]})) + down;
 }
 
 // Shapes with at most this many points keep their candidate heights in
@@ -443,17 +479,18 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
   // Block-solve lanes: with P == 2, lanes l and l ^ 8 (same 16-lane DPP row)
   // share a body; `slot` numbers the bodies a colour pass runs at once.
   constexpr int P = Stepper<R, B, J, CG, CS, L>::P;
-  static_assert(P == 1 || L % 16 == 0, "split block solves need 16-lane groups");
-  const int part = P == 2 ? (lane >> 3) & 1 : 0;
-  const int slot = P == 2 ? (lane & 7) + 8 * (lane >> 4) : lane;
+  static_assert(P == 1 || L % (8 * P) == 0, "split block solves need 8 P-lane groups");
+  const int part = (lane >> 3) & (P - 1);
+  const int slot = P == 1 ? lane : (lane & 7) + 8 * (lane / (8 * P));
   const R h = M.dt, alpha = M.alpha, gamma = M.gamma, ag = alpha * gamma;
 
   for (int sub = 0; sub < args.substeps; ++sub) {
     if (!__any(active))
       break;
     // ---------------- detection: ground manifolds (kernel.cuh:601-653) ----
-    int picks[SPL][4], npick[SPL], src[SPL][4];
-    V3<R> pickLocal[SPL][4];
+    // Per pick: point index | (warm-start source + 1) << 20, so that only
+    // four registers per shape live across the barrier into compaction.
+    int picks[SPL][4], npick[SPL];
 #pragma unroll
     for (int r = 0; r < SPL; ++r) {
       npick[r] = 0;
@@ -474,17 +511,8 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
         E.shapeCount[si] = 0;
         continue;
       }
-      const int type = M.stype[si], count = M.scount[si], off = M.soffset[si];
-      V3<R> c{M.center[0][si], M.center[1][si], M.center[2][si]};
-      auto pointOf = [&](int k) {
-        if (type == 1 || type == 3)
-          return points[off + k];
-        V3<R> down = rotate(conj(q), V3<R>{0, 0, -M.size[0][si]});
-        if (type == 0)
-          return c + down;
-        Q4<R> sq{M.sq[0][si], M.sq[1][si], M.sq[2][si], M.sq[3][si]};
-        return (c + rotate(sq, V3<R>{0, 0, (k ? R(1) : R(-1)) * M.size[1][si]})) + down;
-      };
+      const int count = M.scount[si];
+      auto pointOf = [&](int k) { return groundPoint(M, points, si, k, q); };
       V3<R> chosen[4];
       int n = 0;
       if (count <= kCachedPoints) {
@@ -527,7 +555,6 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
           }
           if (best >= 0) {
             picks[r][pk] = best;
-            pickLocal[r][pk] = pointOf(best);
             chosen[pk] = V3<R>{bx, by, lowest};
             n = pk + 1;
           }
@@ -539,7 +566,7 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
             break;
           int best = -1;
           R lowest = R(INFINITY);
-          V3<R> bestLocal{0, 0, 0}, bestWorld{0, 0, 0};
+          V3<R> bestWorld{0, 0, 0};
           for (int k = 0; k < count; ++k) {
             V3<R> local = pointOf(k), world = x + rotate(q, local);
             V3<R> vel = v + cross(w, world - x);
@@ -555,12 +582,10 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
               continue;
             best = k;
             lowest = z;
-            bestLocal = local;
             bestWorld = world;
           }
           if (best >= 0) {
             picks[r][pk] = best;
-            pickLocal[r][pk] = bestLocal;
             chosen[pk] = bestWorld;
             n = pk + 1;
           }
@@ -571,13 +596,12 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
       // Warm-start source in the previous list (still in LDS).
 #pragma unroll
       for (int p = 0; p < 4; ++p) {
-        src[r][p] = -1;
         if (p >= n)
           continue;
         for (int i = 0; i < E.s.ngc; ++i) {
           int id = E.s.gc[i].id;
           if (gcShape(id) == si && gcFeature(id) == picks[r][p]) {
-            src[r][p] = i;
+            picks[r][p] |= (i + 1) << 20;
             break;
           }
         }
@@ -659,11 +683,12 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
           if (p >= npick[r] || offset + p >= CG)
             break;
           GroundContact<R> c;
-          V3<R> local = pickLocal[r][p], world = x + rotate(q, local);
+          const int feature = picks[r][p] & 0xFFFFF, src = (picks[r][p] >> 20) - 1;
+          V3<R> local = groundPoint(M, points, si, feature, q), world = x + rotate(q, local);
           R lam[3] = {0, 0, 0}, pen[3] = {1000, 1000, 1000};
           R anchor[2] = {world.x, world.y};
-          if (src[r][p] >= 0) {
-            const GroundContact<R> &old = gs->gc[src[r][p]];
+          if (src >= 0) {
+            const GroundContact<R> &old = gs->gc[src];
             for (int d = 0; d < 3; ++d) {
               lam[d] = old.lambda[d];
               pen[d] = old.penalty[d];
@@ -674,7 +699,7 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
               anchor[1] = old.anchor[1];
             }
           }
-          c.id = gcPack(si, b, picks[r][p], false);
+          c.id = gcPack(si, b, feature, false);
           c.local[0] = local.x;
           c.local[1] = local.y;
           c.local[2] = local.z;

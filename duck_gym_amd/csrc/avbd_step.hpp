@@ -231,6 +231,16 @@ __device__ __forceinline__ double pairSwap(double v) {
   const unsigned hi = __builtin_amdgcn_update_dpp(0, int(unsigned(b >> 32)), 0x128, 0xF, 0xF, false);
   return __longlong_as_double(static_cast<long long>((static_cast<unsigned long long>(hi) << 32) | lo));
 }
+// Value of lane ^ 16 (ds_swizzle, 32-lane groups: and 0x1f, xor 0x10).
+__device__ __forceinline__ float halfSwap(float v) {
+  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));
+}
+__device__ __forceinline__ double halfSwap(double v) {
+  const unsigned long long b = static_cast<unsigned long long>(__double_as_longlong(v));
+  const unsigned lo = __builtin_amdgcn_ds_swizzle(int(unsigned(b)), 0x401F);
+  const unsigned hi = __builtin_amdgcn_ds_swizzle(int(unsigned(b >> 32)), 0x401F);
+  return __longlong_as_double(static_cast<long long>((static_cast<unsigned long long>(hi) << 32) | lo));
+}
 
 // R diag(I) R^T of the body inertia at orientation q, as its six entries
 // (xx, yy, zz, xy, xz, yz), and the product of such a matrix with v.
@@ -260,9 +270,10 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
   const Fr &F;
   Env &E;
   int lane; // 0..L-1 within the environment
-  // Lanes per block solve: with 16 or more lanes per environment two lanes
-  // (lane and lane ^ 8) share each body's assembly and combine it by DPP.
-  static constexpr int P = L >= 16 ? 2 : 1;
+  // Lanes per block solve: with 16 lanes per environment two lanes (lane,
+  // lane ^ 8), with 32 lanes four (lane ^ 8, ^ 16, ^ 24) share each body's
+  // assembly and sum it by DPP row rotation / swizzle.
+  static constexpr int P = L >= 32 ? 4 : (L >= 16 ? 2 : 1);
 
   // ------------------------------------------------------------ access --
   DUCK_HD V3<R> X(int b) const { return {E.s.x[0][b], E.s.x[1][b], E.s.x[2][b]}; }
@@ -356,11 +367,12 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
   }
 
   // --------------------------------------------------- 6x6 block solve --
-  // kernel.cuh:828-936 for one dynamic body.  With P == 2 the two lanes of
-  // a pair call this for the same body: part 0 assembles the inertia block,
-  // the odd-position hinges and the odd-position contacts, part 1 the even
-  // ones; the partial systems are summed on both lanes (bitwise the same
-  // sum), both solve, part 0 writes the pose.
+  // kernel.cuh:828-936 for one dynamic body.  With P > 1 the P lanes of a
+  // group call this for the same body: part 0 assembles the inertia block,
+  // and the i-th hinge and the n-th contact of the body go to part
+  // (i + 1) mod P and (n + 1) mod P; the partial systems are summed on every
+  // lane of the group (bitwise the same sum: the pairwise sums commute), all
+  // factor, part 0 writes the pose.
   __device__ R updateBody(int bi, bool implicitDrive, int part) {
     const R h = M.dt;
     V3<R> x = X(bi), xp{E.xp[0][bi], E.xp[1][bi], E.xp[2][bi]};
@@ -406,7 +418,7 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
     // Adjacency entries pack (hinge, body a, body b); the next entry is
     // fetched while the current hinge is assembled.
     const int adjEnd = F.adjStart[bi + 1];
-    int adj = F.adjStart[bi] + (P == 2 ? 1 - part : 0);
+    int adj = F.adjStart[bi] + (part + P - 1) % P;
     int packed = adj < adjEnd ? F.adj[adj] : 0;
     for (; adj < adjEnd; adj += P) {
       const int cur = packed;
@@ -485,7 +497,7 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
     // Ground contacts of this body, in list order.
     int nth = 0;
     for (uint64_t m = E.gmask[bi]; m; m &= m - 1, ++nth) {
-      if (P == 2 && (nth & 1) == part)
+      if (P > 1 && (nth + 1) % P != part)
         continue;
       const GroundContact<R> &c = E.s.gc[__builtin_ctzll(m)];
       V3<R> ra;
@@ -501,7 +513,7 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
     // Body-body contacts touching this body, in list order.
     nth = 0;
     for (uint32_t m = E.smask[bi]; m; m &= m - 1, ++nth) {
-      if (P == 2 && (nth & 1) == part)
+      if (P > 1 && (nth + 1) % P != part)
         continue;
       const SelfContact<R> &c = E.s.sc[__builtin_ctz(m)];
       V3<R> ra, rb;
@@ -524,13 +536,21 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
         geometricAdd(H, r, fw * sign);
       }
     }
-    if constexpr (P == 2) {
+    if constexpr (P >= 2) {
 #pragma unroll
       for (int k = 0; k < 21; ++k)
         H.h[k] += pairSwap(H.h[k]);
 #pragma unroll
       for (int k = 0; k < 6; ++k)
         H.g[k] += pairSwap(H.g[k]);
+    }
+    if constexpr (P == 4) {
+#pragma unroll
+      for (int k = 0; k < 21; ++k)
+        H.h[k] += halfSwap(H.h[k]);
+#pragma unroll
+      for (int k = 0; k < 6; ++k)
+        H.g[k] += halfSwap(H.g[k]);
     }
     R st[6];
     solve6(H, st);

@@ -437,7 +437,10 @@ const char *kMicroDuckJoints[14] = {
 // MicroDuck-sized models: float runs 4 environments per wave with two lanes
 // per block solve (16 lanes per env); double runs 8 environments per wave
 // with one lane per block solve, which keeps the reference's accumulation
-// order (DUCK_FLAG_SPLIT selects the float layout for double too).
+// order (DUCK_FLAG_SPLIT selects the float layout for double too).  Four
+// lanes per block solve (32 lanes per env, 20 KB of LDS per workgroup)
+// would let two waves share a SIMD only below 256 registers per lane, which
+// this kernel exceeds; with register spills it measured slower.
 template <class R>
 BatchBase *makeBatch(HostModel &&m, int n, double dt, int iterations, int device, bool split) {
   const int nb = m.bodies.size(), nj = m.joints.size(), ns = m.shapes.size(),
