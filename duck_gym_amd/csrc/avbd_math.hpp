@@ -193,6 +193,26 @@ template <class R> DUCK_HD V3<R> flogmap(Q4<R> q) {
   }
 }
 
+// Rotation matrix (row-major) of a unit quaternion, and its product with v.
+template <class R> DUCK_HD void quatMatrix(Q4<R> q, R m[9]) {
+  const R xx = q.x * q.x, yy = q.y * q.y, zz = q.z * q.z;
+  const R xy = q.x * q.y, xz = q.x * q.z, yz = q.y * q.z;
+  const R wx = q.w * q.x, wy = q.w * q.y, wz = q.w * q.z;
+  m[0] = R(1) - R(2) * (yy + zz);
+  m[1] = R(2) * (xy - wz);
+  m[2] = R(2) * (xz + wy);
+  m[3] = R(2) * (xy + wz);
+  m[4] = R(1) - R(2) * (xx + zz);
+  m[5] = R(2) * (yz - wx);
+  m[6] = R(2) * (xz - wy);
+  m[7] = R(2) * (yz + wx);
+  m[8] = R(1) - R(2) * (xx + yy);
+}
+template <class R> DUCK_HD V3<R> matApply(const R m[9], V3<R> v) {
+  return {(m[0] * v.x + m[1] * v.y) + m[2] * v.z, (m[3] * v.x + m[4] * v.y) + m[5] * v.z,
+          (m[6] * v.x + m[7] * v.y) + m[8] * v.z};
+}
+
 // IEEE remainder(a, 2*pi) in double: n = nearest integer of a/(2 pi), then the
 // exactly representable a - n 2pi by one fused operation.  [double]
 template <class R> DUCK_HD R wrapAngle(R a) {

@@ -328,14 +328,28 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
   DUCK_HD JointEval evalJoint(int ji, int a, int b) const {
     JointEval o;
     Q4<R> qa = Q(a), qb = Q(b);
-    o.ra = rotate(qa, frame(F.ra, ji));
-    o.rb = rotate(qb, frame(F.rb, ji));
+    V3<R> u;
+    if constexpr (sizeof(R) == sizeof(float)) {
+      // Six frame vectors by two rotation matrices (the float solver).
+      R ma[9], mb[9];
+      quatMatrix(qa, ma);
+      quatMatrix(qb, mb);
+      o.ra = matApply(ma, frame(F.ra, ji));
+      o.axis = matApply(ma, frame(F.axisA, ji));
+      o.t1 = matApply(ma, frame(F.tangentA, ji));
+      o.rb = matApply(mb, frame(F.rb, ji));
+      o.axisB = matApply(mb, frame(F.axisB, ji));
+      u = matApply(mb, frame(F.tangentB, ji));
+    } else {
+      o.ra = rotate(qa, frame(F.ra, ji));
+      o.rb = rotate(qb, frame(F.rb, ji));
+      o.axis = rotate(qa, frame(F.axisA, ji));
+      o.axisB = rotate(qb, frame(F.axisB, ji));
+      o.t1 = rotate(qa, frame(F.tangentA, ji));
+      u = rotate(qb, frame(F.tangentB, ji));
+    }
     V3<R> d = ((X(a) + o.ra) - X(b)) - o.rb;
-    o.axis = rotate(qa, frame(F.axisA, ji));
-    o.axisB = rotate(qb, frame(F.axisB, ji));
-    o.t1 = rotate(qa, frame(F.tangentA, ji));
     o.t2 = cross(o.axis, o.t1);
-    V3<R> u = rotate(qb, frame(F.tangentB, ji));
     o.angle = matan2(dot(o.axis, cross(o.t1, u)), dot(o.t1, u));
     o.C[0] = d.x;
     o.C[1] = d.y;
@@ -386,15 +400,13 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
     for (int k = 0; k < 6; ++k)
       H.g[k] = 0;
     const R h2 = h * h, ih2 = frcp(h2), ih = frcp(h);
-    if (part == 0) {
-      V3<R> dx = x - xp, theta = flogmap(q * conj(qp));
-      R mh = fdivInv(E.s.mass[bi], h2, ih2);
-      H.h[tri(0, 0)] = mh;
-      H.h[tri(1, 1)] = mh;
-      H.h[tri(2, 2)] = mh;
-      H.g[0] = mh * dx.x;
-      H.g[1] = mh * dx.y;
-      H.g[2] = mh * dx.z;
+    // Inertia block (kernel.cuh:837-855).  With P >= 2 the first two lanes
+    // share it: both form theta, the log-Jacobian and rotJ; part 0 applies
+    // the world inertia to theta and rotJ[0] (the g rows and the first
+    // rotational column, plus the linear block), part 1 to rotJ[1] and
+    // rotJ[2] (the other three rotational entries).
+    if (part < 2) {
+      V3<R> theta = flogmap(q * conj(qp));
       R coef = logJacobianCoef(fnorm(theta));
       V3<R> rotJ[3];
 #pragma unroll
@@ -404,14 +416,45 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
       }
       // World inertia at q0, formed once per step by the predictor.
       const R Iw[6] = {E.Iw[0][bi], E.Iw[1][bi], E.Iw[2][bi], E.Iw[3][bi], E.Iw[4][bi], E.Iw[5][bi]};
-      V3<R> It = symApply(Iw, theta);
-      V3<R> IJ[3] = {symApply(Iw, rotJ[0]), symApply(Iw, rotJ[1]), symApply(Iw, rotJ[2])};
+      if (part == 0) {
+        V3<R> dx = x - xp;
+        R mh = fdivInv(E.s.mass[bi], h2, ih2);
+        H.h[tri(0, 0)] = mh;
+        H.h[tri(1, 1)] = mh;
+        H.h[tri(2, 2)] = mh;
+        H.g[0] = mh * dx.x;
+        H.g[1] = mh * dx.y;
+        H.g[2] = mh * dx.z;
+      }
+      if constexpr (P == 1) {
+        V3<R> It = symApply(Iw, theta);
+        V3<R> IJ[3] = {symApply(Iw, rotJ[0]), symApply(Iw, rotJ[1]), symApply(Iw, rotJ[2])};
 #pragma unroll
-      for (int k = 0; k < 3; ++k) {
-        H.g[3 + k] = fdivInv(dot(rotJ[k], It), h2, ih2);
+        for (int k = 0; k < 3; ++k) {
+          H.g[3 + k] = fdivInv(dot(rotJ[k], It), h2, ih2);
 #pragma unroll
-        for (int l = 0; l <= k; ++l)
-          H.h[tri(3 + k, 3 + l)] = fdivInv(dot(rotJ[k], IJ[l]), h2, ih2);
+          for (int l = 0; l <= k; ++l)
+            H.h[tri(3 + k, 3 + l)] = fdivInv(dot(rotJ[k], IJ[l]), h2, ih2);
+        }
+      } else {
+        const bool first = part == 0;
+        const V3<R> A = symApply(Iw, first ? theta : rotJ[1]);
+        const V3<R> Bv = symApply(Iw, first ? rotJ[0] : rotJ[2]);
+        const R d0 = fdivInv(dot(rotJ[0], A), h2, ih2), d1 = fdivInv(dot(rotJ[1], A), h2, ih2),
+                d2 = fdivInv(dot(rotJ[2], A), h2, ih2);
+        const R e1 = fdivInv(dot(rotJ[1], Bv), h2, ih2), e2 = fdivInv(dot(rotJ[2], Bv), h2, ih2);
+        if (first) {
+          H.g[3] = d0;
+          H.g[4] = d1;
+          H.g[5] = d2;
+          H.h[tri(3, 3)] = fdivInv(dot(rotJ[0], Bv), h2, ih2);
+          H.h[tri(4, 3)] = e1;
+          H.h[tri(5, 3)] = e2;
+        } else {
+          H.h[tri(4, 4)] = d1;
+          H.h[tri(5, 4)] = d2;
+          H.h[tri(5, 5)] = e2;
+        }
       }
     }
     const R alpha = M.alpha;
