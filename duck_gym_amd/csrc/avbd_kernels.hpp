@@ -884,14 +884,55 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
     // When each of the first two colours fits in one pass of the block-solve
     // slots, every lane's body for them is fixed for the whole step.
     bool twoColourSlots = false;
-    int mine0 = -1, mine1 = -1;
+    int mine[2] = {-1, -1}, partOf[2] = {part, part}, partsOf[2] = {P, P}, partner[2] = {0, 0};
     if (active) {
       const int c0 = E.colorStart[0], c1 = E.colorStart[1], c2 = E.colorStart[2];
       twoColourSlots = c1 - c0 <= L / P && c2 - c1 <= L / P;
       if (c0 + slot < c1)
-        mine0 = E.order[c0 + slot];
+        mine[0] = E.order[c0 + slot];
       if (c1 + slot < c2)
-        mine1 = E.order[c1 + slot];
+        mine[1] = E.order[c1 + slot];
+    }
+    if constexpr (P == 2) {
+      // A colour with a free slot lends it to its body with the most hinges
+      // or ground contacts (three or more: two lanes would need two rounds);
+      // that body's group becomes four lanes (both slots, lane and lane ^ 8).
+      if (active && twoColourSlots) {
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          const int cs = E.colorStart[c], n = E.colorStart[c + 1] - cs;
+          if (n >= L / P)
+            continue;
+          int best = -1, bestUnits = 2;
+          for (int k = 0; k < n; ++k) {
+            const int b = E.order[cs + k];
+            const int hinges = F.adjStart[b + 1] - F.adjStart[b];
+            const int ground = __popcll(E.gmask[b]);
+            const int units = hinges > ground ? hinges : ground;
+            if (units > bestUnits) {
+              bestUnits = units;
+              best = k;
+            }
+          }
+          if (best < 0)
+            continue;
+          // The busy body moves to slot 0 (order within a colour is free:
+          // same-colour bodies do not interact) and borrows slot 7, so the
+          // two slots' pair sums meet through fixed DPP row rotations.
+          if (slot == 0) {
+            mine[c] = E.order[cs + best];
+            partsOf[c] = 4;
+            partner[c] = 1; // takes the sum of slot 7
+          } else if (slot == best) {
+            mine[c] = E.order[cs];
+          } else if (slot == 7) {
+            mine[c] = E.order[cs + best];
+            partOf[c] = part + 2;
+            partsOf[c] = 4;
+            partner[c] = 0; // takes the sum of slot 0
+          }
+        }
+      }
     }
     // ---------------- AVBD iterations (kernel.cuh:979-1063) ---------------
     for (int it = 0; it < M.iterations; ++it) {
@@ -900,11 +941,16 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
         break;
       R maxUpdate = 0;
       for (int c = 0; c < colours; ++c) {
+        const bool quadPass = P == 2 && c < 2 &&
+                              __any(work && twoColourSlots && (c == 0 ? partsOf[0] : partsOf[1]) == 4);
         if (work && c < E.s.colorCount) {
           if (c < 2 && twoColourSlots) {
-            const int bi = c == 0 ? mine0 : mine1;
+            const bool c0 = c == 0;
+            const int bi = c0 ? mine[0] : mine[1];
             if (bi >= 0)
-              maxUpdate = mx(maxUpdate, stp.updateBody(bi, true, part));
+              maxUpdate = mx(maxUpdate, stp.updateBody(bi, true, c0 ? partOf[0] : partOf[1],
+                                                       c0 ? partsOf[0] : partsOf[1],
+                                                       c0 ? partner[0] : partner[1], quadPass));
           } else {
             for (int k = E.colorStart[c] + slot; k < E.colorStart[c + 1]; k += L / P)
               maxUpdate = mx(maxUpdate, stp.updateBody(E.order[k], true, part));

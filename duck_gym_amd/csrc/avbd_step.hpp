@@ -262,6 +262,17 @@ template <class R> DUCK_HD V3<R> symApply(const R m[6], V3<R> v) {
           (m[4] * v.x + m[5] * v.y) + m[2] * v.z};
 }
 
+// Lane (i - N) mod 16 of the same 16-lane row (DPP row_ror:N).
+template <int N> __device__ __forceinline__ float rowRotate(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x120 + N, 0xF, 0xF, false));
+}
+template <int N> __device__ __forceinline__ double rowRotate(double v) {
+  const unsigned long long b = static_cast<unsigned long long>(__double_as_longlong(v));
+  const unsigned lo = __builtin_amdgcn_update_dpp(0, int(unsigned(b)), 0x120 + N, 0xF, 0xF, false);
+  const unsigned hi = __builtin_amdgcn_update_dpp(0, int(unsigned(b >> 32)), 0x120 + N, 0xF, 0xF, false);
+  return __longlong_as_double(static_cast<long long>((static_cast<unsigned long long>(hi) << 32) | lo));
+}
+
 template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
   using Env = EnvLds<R, B, J, CG, CS>;
   using Fr = Frames<R, B, J>;
@@ -387,7 +398,12 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
   // (i + 1) mod P and (n + 1) mod P; the partial systems are summed on every
   // lane of the group (bitwise the same sum: the pairwise sums commute), all
   // factor, part 0 writes the pose.
-  __device__ R updateBody(int bi, bool implicitDrive, int part) {
+  // nParts (<= 4) is the size of this body's lane group when a colour pass
+  // gives one body two slots (slots 0 and 7, lane and lane ^ 8 in each);
+  // `partner` is 1 in slot 0 and 0 in slot 7, and `quad` tells every lane of
+  // the wave that such a group exists in this pass.
+  __device__ R updateBody(int bi, bool implicitDrive, int part, int nParts = P, int partner = 0,
+                          bool quad = false) {
     const R h = M.dt;
     V3<R> x = X(bi), xp{E.xp[0][bi], E.xp[1][bi], E.xp[2][bi]};
     Q4<R> q = Q(bi), qp{E.qp[0][bi], E.qp[1][bi], E.qp[2][bi], E.qp[3][bi]}, q0 = Q0(bi);
@@ -461,12 +477,12 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
     // Adjacency entries pack (hinge, body a, body b); the next entry is
     // fetched while the current hinge is assembled.
     const int adjEnd = F.adjStart[bi + 1];
-    int adj = F.adjStart[bi] + (part + P - 1) % P;
+    int adj = F.adjStart[bi] + (part + nParts - 1) % nParts;
     int packed = adj < adjEnd ? F.adj[adj] : 0;
-    for (; adj < adjEnd; adj += P) {
+    for (; adj < adjEnd; adj += nParts) {
       const int cur = packed;
-      if (adj + P < adjEnd)
-        packed = F.adj[adj + P];
+      if (adj + nParts < adjEnd)
+        packed = F.adj[adj + nParts];
       const int ji = cur & 255, ja = (cur >> 8) & 255, jb = (cur >> 16) & 255;
       const bool parent = bi == ja;
       const R s = parent ? R(1) : R(-1);
@@ -540,7 +556,7 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
     // Ground contacts of this body, in list order.
     int nth = 0;
     for (uint64_t m = E.gmask[bi]; m; m &= m - 1, ++nth) {
-      if (P > 1 && (nth + 1) % P != part)
+      if (nParts > 1 && (nth + 1) % nParts != part)
         continue;
       const GroundContact<R> &c = E.s.gc[__builtin_ctzll(m)];
       V3<R> ra;
@@ -556,7 +572,7 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
     // Body-body contacts touching this body, in list order.
     nth = 0;
     for (uint32_t m = E.smask[bi]; m; m &= m - 1, ++nth) {
-      if (P > 1 && (nth + 1) % P != part)
+      if (nParts > 1 && (nth + 1) % nParts != part)
         continue;
       const SelfContact<R> &c = E.s.sc[__builtin_ctz(m)];
       V3<R> ra, rb;
@@ -594,6 +610,24 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
 #pragma unroll
       for (int k = 0; k < 6; ++k)
         H.g[k] += halfSwap(H.g[k]);
+    } else if constexpr (P == 2) {
+      if (quad) {
+        // A two-slot group (slots 0 and 7 of the row) adds the other slot's
+        // pair sum: lane i reads lane i - 9 (mod 16) in slot 0 and lane
+        // i - 7 in slot 7.  Both slots then hold (a + b) + (c + d) and
+        // (c + d) + (a + b): bitwise equal.
+        const bool four = nParts == 4, fromSeven = partner == 1;
+#pragma unroll
+        for (int k = 0; k < 21; ++k) {
+          const R a = rowRotate<9>(H.h[k]), b = rowRotate<7>(H.h[k]);
+          H.h[k] = four ? H.h[k] + (fromSeven ? a : b) : H.h[k];
+        }
+#pragma unroll
+        for (int k = 0; k < 6; ++k) {
+          const R a = rowRotate<9>(H.g[k]), b = rowRotate<7>(H.g[k]);
+          H.g[k] = four ? H.g[k] + (fromSeven ? a : b) : H.g[k];
+        }
+      }
     }
     R st[6];
     solve6(H, st);
