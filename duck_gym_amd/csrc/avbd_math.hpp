@@ -226,6 +226,18 @@ template <class R> DUCK_HD R wrapAngle(R a) {
   return R(fma(-n, twoPi, d));
 }
 
+// Both angles wrapped, with one test for the common case of both already
+// inside (-pi, pi).
+template <class R> DUCK_HD void wrapAngle2(R a, R b, R &wa, R &wb) {
+  if (mabs(a) < R(3.14159) && mabs(b) < R(3.14159)) {
+    wa = a + R(0);
+    wb = b + R(0);
+  } else {
+    wa = wrapAngle(a);
+    wb = wrapAngle(b);
+  }
+}
+
 template <class R> DUCK_HD R mn(R a, R b) { return a < b ? a : b; }
 template <class R> DUCK_HD R mx(R a, R b) { return a > b ? a : b; }
 template <class R> DUCK_HD R clampv(R v, R a, R b) { return mn(mx(v, a), b); }

@@ -487,70 +487,66 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
       const bool parent = bi == ja;
       const R s = parent ? R(1) : R(-1);
       JointEval je = evalJoint(ji, ja, jb);
-      const int rows = F.limited[ji] ? 7 : 5;
-      // Anchor rows: J_k = [s e_k, r x e_k] with r = ra (parent) or -rb
-      // (child); their geometric terms share r.
+      // Anchor rows (k = 0..2): J_k = [s e_k, r x e_k] with r = ra (parent)
+      // or -rb (child); their geometric terms share r.  Anchor and axis
+      // rows are always active; the limit rows only on limited hinges.  The
+      // rows are straight-line code so that independent chains overlap.
       const V3<R> r = parent ? je.ra : -je.rb;
       R geo[3][3];
       axisGeometricNorms(r, geo);
+      R fr[5], pr[5];
 #pragma unroll
-      for (int k = 0; k < 7; ++k) {
-        if (k >= rows)
-          break;
-        R c0 = E.c0[k][ji];
-        R c = je.C[k] - alpha * (k < 5 ? c0 : mn(c0, R(0)));
-        R pen = E.s.penalty[k][ji];
-        R f = E.s.lambda[k][ji] + pen * c;
-        if (k >= 5)
-          f = mn(f, R(0));
-        if (k < 5 || f < 0) {
-          if (k < 3) {
-            stampAxisRow(H, k, s, r, f, pen);
-            const R af = mabs(f);
-            H.h[tri(3, 3)] += af * geo[k][0];
-            H.h[tri(4, 4)] += af * geo[k][1];
-            H.h[tri(5, 5)] += af * geo[k][2];
-          } else if (k < 5) {
-            V3<R> t = k == 3 ? je.t1 : je.t2;
-            stampAngular(H, parent ? cross(t, je.axisB) : cross(je.axisB, t), f, pen);
-            geometricAdd(H, parent ? t : je.axisB, (parent ? je.axisB : t) * f);
-          } else {
+      for (int k = 0; k < 5; ++k) {
+        const R c = je.C[k] - alpha * E.c0[k][ji];
+        pr[k] = E.s.penalty[k][ji];
+        fr[k] = E.s.lambda[k][ji] + pr[k] * c;
+      }
+#pragma unroll
+      for (int k = 0; k < 3; ++k) {
+        stampAxisRow(H, k, s, r, fr[k], pr[k]);
+        const R af = mabs(fr[k]);
+        H.h[tri(3, 3)] += af * geo[k][0];
+        H.h[tri(4, 4)] += af * geo[k][1];
+        H.h[tri(5, 5)] += af * geo[k][2];
+      }
+#pragma unroll
+      for (int k = 3; k < 5; ++k) {
+        const V3<R> t = k == 3 ? je.t1 : je.t2;
+        stampAngular(H, parent ? cross(t, je.axisB) : cross(je.axisB, t), fr[k], pr[k]);
+        geometricAdd(H, parent ? t : je.axisB, (parent ? je.axisB : t) * fr[k]);
+      }
+      if (F.limited[ji]) {
+#pragma unroll
+        for (int k = 5; k < 7; ++k) {
+          const R c = je.C[k] - alpha * mn(E.c0[k][ji], R(0));
+          const R pen = E.s.penalty[k][ji];
+          const R f = mn(E.s.lambda[k][ji] + pen * c, R(0));
+          if (f < 0)
             stampAngular(H, (k == 5) == parent ? -je.axis : je.axis, f, pen);
-          }
         }
       }
       // Rows along the hinge axis (kernel.cuh:893-913): implicit torque-
       // limited PD potential, damping/armature, dry friction -- one stamp
-      // with the summed force and stiffness.
+      // with the summed force and stiffness, selected without branches.
       const V3<R> J5 = parent ? -je.axis : je.axis;
-      R axisForce = 0, axisStiff = 0;
-      if (implicitDrive) {
-        R kp = E.s.kp[ji], maxT = E.s.maxTorque[ji];
-        R drive = kp * wrapAngle(je.angle - E.s.target[ji]) - E.s.torque[ji];
-        R ks = kp;
-        if (maxT > 0) {
-          if (mabs(drive) >= maxT)
-            ks = 0;
-          drive = clampv(drive, -maxT, maxT);
-        }
-        axisForce = drive;
-        axisStiff = ks;
-      }
-      R damping = E.s.damping[ji], armature = F.armature[ji];
-      R delta = wrapAngle(je.angle - E.angle0[ji]);
+      R wTarget, delta;
+      wrapAngle2(je.angle - E.s.target[ji], je.angle - E.angle0[ji], wTarget, delta);
+      const R kp = E.s.kp[ji], maxT = E.s.maxTorque[ji];
+      R drive = kp * wTarget - E.s.torque[ji];
+      const bool capped = maxT > 0;
+      const R ks = capped && mabs(drive) >= maxT ? R(0) : kp;
+      drive = capped ? clampv(drive, -maxT, maxT) : drive;
+      R axisForce = implicitDrive ? drive : R(0), axisStiff = implicitDrive ? ks : R(0);
+      const R damping = E.s.damping[ji], armature = F.armature[ji];
       const R dh = fdivInv(damping, h, ih), ah = fdivInv(armature, h2, ih2);
-      R stiff = dh + ah;
-      if (stiff > 0) {
-        axisForce += dh * delta + ah * (delta - h * E.velocity0[ji]);
-        axisStiff += stiff;
-      }
-      R fl = E.s.frictionloss[ji];
-      if (fl > 0) {
-        R trial = E.s.lambdaF[ji] + E.s.penaltyF[ji] * delta;
-        axisForce += clampv(trial, -fl, fl);
-        if (mabs(trial) < fl)
-          axisStiff += E.s.penaltyF[ji];
-      }
+      const R stiff = dh + ah;
+      const bool damped = stiff > 0;
+      axisForce += damped ? dh * delta + ah * (delta - h * E.velocity0[ji]) : R(0);
+      axisStiff += damped ? stiff : R(0);
+      const R fl = E.s.frictionloss[ji];
+      const R trial = E.s.lambdaF[ji] + E.s.penaltyF[ji] * delta;
+      axisForce += fl > 0 ? clampv(trial, -fl, fl) : R(0);
+      axisStiff += fl > 0 && mabs(trial) < fl ? E.s.penaltyF[ji] : R(0);
       stampAngular(H, J5, axisForce, axisStiff);
     }
     // Ground contacts of this body, in list order.
@@ -562,12 +558,15 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
       V3<R> ra;
       V3<R> C = groundC(c, ra);
       V3<R> f = contactForce(C, c.lambda, c.penalty, groundFriction(gcShape(c.id)));
-      if (f.z < 0) {
-        stampAxisRow(H, 0, R(1), ra, f.x, c.penalty[0]);
-        stampAxisRow(H, 1, R(1), ra, f.y, c.penalty[1]);
-        stampAxisRow(H, 2, R(1), ra, f.z, c.penalty[2]);
-        geometricAdd(H, ra, f);
-      }
+      // A separating contact (f.z = 0) contributes nothing: its rows are
+      // stamped with zero force and stiffness rather than branched around.
+      const bool on = f.z < 0;
+      if (!on)
+        f = V3<R>{0, 0, 0};
+      stampAxisRow(H, 0, R(1), ra, f.x, on ? c.penalty[0] : R(0));
+      stampAxisRow(H, 1, R(1), ra, f.y, on ? c.penalty[1] : R(0));
+      stampAxisRow(H, 2, R(1), ra, f.z, on ? c.penalty[2] : R(0));
+      geometricAdd(H, ra, f);
     }
     // Body-body contacts touching this body, in list order.
     nth = 0;
