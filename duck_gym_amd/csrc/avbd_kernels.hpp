@@ -963,20 +963,26 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
       if (work) {
         for (int ji = lane; ji < nj; ji += L) {
           auto je = stp.evalJoint(ji);
-          const int rows = F.limited[ji] ? 7 : 5;
+          // Anchor and axis rows (always active), straight-line.
 #pragma unroll
-          for (int k = 0; k < 7; ++k) {
-            if (k >= rows)
-              break;
-            R c0 = E.c0[k][ji];
-            R c = je.C[k] - alpha * (k < 5 ? c0 : mn(c0, R(0)));
-            R f = E.s.lambda[k][ji] + E.s.penalty[k][ji] * c;
-            E.s.lambda[k][ji] = k >= 5 ? mn(f, R(0)) : f;
-            if (k < 5 || f < 0)
-              E.s.penalty[k][ji] =
-                  mn(E.s.penalty[k][ji] + (k < 3 ? M.betaLinear : M.betaAngular) * mabs(c),
-                     k < 3 ? R(1e9) : R(1e7));
-            error = mx(error, k < 5 ? mabs(c) : mx(R(0), -c));
+          for (int k = 0; k < 5; ++k) {
+            const R c = je.C[k] - alpha * E.c0[k][ji];
+            const R pen = E.s.penalty[k][ji];
+            E.s.lambda[k][ji] = E.s.lambda[k][ji] + pen * c;
+            E.s.penalty[k][ji] =
+                mn(pen + (k < 3 ? M.betaLinear : M.betaAngular) * mabs(c), k < 3 ? R(1e9) : R(1e7));
+            error = mx(error, mabs(c));
+          }
+          if (F.limited[ji]) {
+#pragma unroll
+            for (int k = 5; k < 7; ++k) {
+              const R c = je.C[k] - alpha * mn(E.c0[k][ji], R(0));
+              const R f = E.s.lambda[k][ji] + E.s.penalty[k][ji] * c;
+              E.s.lambda[k][ji] = mn(f, R(0));
+              if (f < 0)
+                E.s.penalty[k][ji] = mn(E.s.penalty[k][ji] + M.betaAngular * mabs(c), R(1e7));
+              error = mx(error, mx(R(0), -c));
+            }
           }
           const R fl = E.s.frictionloss[ji];
           if (fl > 0) {
@@ -995,8 +1001,8 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
           V3<R> C = stp.groundC(c, ra);
           const R mu = stp.groundFriction(gcShape(c.id));
           V3<R> f = contactForce(C, c.lambda, c.penalty, mu);
-          R trial = mhypot(c.lambda[0] + c.penalty[0] * C.x, c.lambda[1] + c.penalty[1] * C.y);
-          bool stick = trial <= -mu * f.z && double(mhypot(C.x, C.y)) < 1e-5;
+          R trial = fhypot(c.lambda[0] + c.penalty[0] * C.x, c.lambda[1] + c.penalty[1] * C.y);
+          bool stick = trial <= -mu * f.z && double(fhypot(C.x, C.y)) < 1e-5;
           c.id = (c.id & 0x7fffffff) | (stick ? int(0x80000000u) : 0);
           R fk[3] = {f.x, f.y, f.z}, Ck[3] = {C.x, C.y, C.z};
 #pragma unroll
@@ -1012,8 +1018,8 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
           V3<R> ra, rb;
           V3<R> C = stp.selfC(c, ra, rb);
           V3<R> f = contactForce(C, c.lambda, c.penalty, c.friction);
-          R trial = mhypot(c.lambda[0] + c.penalty[0] * C.x, c.lambda[1] + c.penalty[1] * C.y);
-          bool stick = trial <= -c.friction * f.z && double(mhypot(C.x, C.y)) < 1e-5;
+          R trial = fhypot(c.lambda[0] + c.penalty[0] * C.x, c.lambda[1] + c.penalty[1] * C.y);
+          bool stick = trial <= -c.friction * f.z && double(fhypot(C.x, C.y)) < 1e-5;
           c.id = (c.id & 0x7fffffff) | (stick ? int(0x80000000u) : 0);
           R fk[3] = {f.x, f.y, f.z}, Ck[3] = {C.x, C.y, C.z};
 #pragma unroll

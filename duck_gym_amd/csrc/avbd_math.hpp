@@ -61,6 +61,10 @@ DUCK_HD float frsqrt(float x) {
 #endif
 }
 DUCK_HD double frsqrt(double x) { return 1.0 / sqrt(x); }
+// |(x, y)|: the hardware square root of x^2 + y^2 in float (solver
+// magnitudes are far from overflow), hypot in double.
+DUCK_HD float fhypot(float x, float y) { return fsqrt(x * x + y * y); }
+DUCK_HD double fhypot(double x, double y) { return hypot(x, y); }
 // a / b: a * rcp(b) in float, a true division in double.
 DUCK_HD float fdiv(float a, float b) { return a * frcp(b); }
 DUCK_HD double fdiv(double a, double b) { return a / b; }

@@ -207,11 +207,7 @@ template <class R> DUCK_HD V3<R> contactForce(V3<R> C, const R lambda[3], const 
   V3<R> f{lambda[0] + penalty[0] * C.x, lambda[1] + penalty[1] * C.y,
           lambda[2] + penalty[2] * C.z};
   f.z = mn(f.z, R(0));
-  R t, bound = -friction * f.z;
-  if constexpr (sizeof(R) == sizeof(float))
-    t = fsqrt(f.x * f.x + f.y * f.y); // magnitudes here are far from overflow
-  else
-    t = mhypot(f.x, f.y);
+  R t = fhypot(f.x, f.y), bound = -friction * f.z;
   if (t > bound && t > 0) {
     R ratio = fdiv(bound, t);
     f.x *= ratio;
