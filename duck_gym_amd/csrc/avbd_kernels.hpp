@@ -863,11 +863,11 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
         if (mass == 0)
           continue;
         V3<R> v = stp.Vel(b), w = stp.Omega(b), I = stp.Inertia(b);
-        V3<R> xp = (x + h * v) + (h * h) * (V3<R>{M.gravity[0], M.gravity[1], M.gravity[2]} +
-                                            divide(stp.force(b), mass));
+        V3<R> xp = faxpy(h * h, V3<R>{M.gravity[0], M.gravity[1], M.gravity[2]} + divide(stp.force(b), mass),
+                         faxpy(h, v, x));
         V3<R> spin = -cross(w, stp.inertiaApply(q, I, w, false));
-        V3<R> wp = w + h * stp.inertiaApply(q, I, spin, true);
-        Q4<R> qp = fexpmap(h * wp) * q;
+        V3<R> wp = faxpy(h, stp.inertiaApply(q, I, spin, true), w);
+        Q4<R> qp = fqmul(fexpmap(h * wp), q);
 #pragma unroll
         for (int k = 0; k < 3; ++k)
           E.xp[k][b] = comp(xp, k);
@@ -966,32 +966,32 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
           // Anchor and axis rows (always active), straight-line.
 #pragma unroll
           for (int k = 0; k < 5; ++k) {
-            const R c = je.C[k] - alpha * E.c0[k][ji];
+            const R c = fmad(-alpha, E.c0[k][ji], je.C[k]);
             const R pen = E.s.penalty[k][ji];
-            E.s.lambda[k][ji] = E.s.lambda[k][ji] + pen * c;
+            E.s.lambda[k][ji] = fmad(pen, c, E.s.lambda[k][ji]);
             E.s.penalty[k][ji] =
-                mn(pen + (k < 3 ? M.betaLinear : M.betaAngular) * mabs(c), k < 3 ? R(1e9) : R(1e7));
+                mn(fmad(k < 3 ? M.betaLinear : M.betaAngular, mabs(c), pen), k < 3 ? R(1e9) : R(1e7));
             error = mx(error, mabs(c));
           }
           if (F.limited[ji]) {
 #pragma unroll
             for (int k = 5; k < 7; ++k) {
-              const R c = je.C[k] - alpha * mn(E.c0[k][ji], R(0));
-              const R f = E.s.lambda[k][ji] + E.s.penalty[k][ji] * c;
+              const R c = fmad(-alpha, mn(E.c0[k][ji], R(0)), je.C[k]);
+              const R f = fmad(E.s.penalty[k][ji], c, E.s.lambda[k][ji]);
               E.s.lambda[k][ji] = mn(f, R(0));
               if (f < 0)
-                E.s.penalty[k][ji] = mn(E.s.penalty[k][ji] + M.betaAngular * mabs(c), R(1e7));
+                E.s.penalty[k][ji] = mn(fmad(M.betaAngular, mabs(c), E.s.penalty[k][ji]), R(1e7));
               error = mx(error, mx(R(0), -c));
             }
           }
           const R fl = E.s.frictionloss[ji];
           if (fl > 0) {
             R delta = wrapAngle(je.angle - E.angle0[ji]);
-            R trial = E.s.lambdaF[ji] + E.s.penaltyF[ji] * delta;
+            R trial = fmad(E.s.penaltyF[ji], delta, E.s.lambdaF[ji]);
             E.s.lambdaF[ji] = clampv(trial, -fl, fl);
             if (mabs(trial) < fl)
-              E.s.penaltyF[ji] = mn(E.s.penaltyF[ji] + M.betaAngular * mabs(delta), R(1e7));
-            R residual = E.s.lambdaF[ji] + E.s.penaltyF[ji] * delta;
+              E.s.penaltyF[ji] = mn(fmad(M.betaAngular, mabs(delta), E.s.penaltyF[ji]), R(1e7));
+            R residual = fmad(E.s.penaltyF[ji], delta, E.s.lambdaF[ji]);
             error = mx(error, mabs(E.s.lambdaF[ji] - clampv(residual, -fl, fl)) / E.s.penaltyF[ji]);
           }
         }
@@ -1001,7 +1001,7 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
           V3<R> C = stp.groundC(c, ra);
           const R mu = stp.groundFriction(gcShape(c.id));
           V3<R> f = contactForce(C, c.lambda, c.penalty, mu);
-          R trial = fhypot(c.lambda[0] + c.penalty[0] * C.x, c.lambda[1] + c.penalty[1] * C.y);
+          R trial = fhypot(fmad(c.penalty[0], C.x, c.lambda[0]), fmad(c.penalty[1], C.y, c.lambda[1]));
           bool stick = trial <= -mu * f.z && double(fhypot(C.x, C.y)) < 1e-5;
           c.id = (c.id & 0x7fffffff) | (stick ? int(0x80000000u) : 0);
           R fk[3] = {f.x, f.y, f.z}, Ck[3] = {C.x, C.y, C.z};
@@ -1009,7 +1009,7 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
           for (int k = 0; k < 3; ++k) {
             c.lambda[k] = fk[k];
             if (f.z < 0 && (k == 2 || trial <= -mu * f.z))
-              c.penalty[k] = mn(c.penalty[k] + M.betaLinear * mabs(Ck[k]), R(1e9));
+              c.penalty[k] = mn(fmad(M.betaLinear, mabs(Ck[k]), c.penalty[k]), R(1e9));
           }
           error = mx(error, mx(R(0), -C.z));
         }
@@ -1018,7 +1018,7 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
           V3<R> ra, rb;
           V3<R> C = stp.selfC(c, ra, rb);
           V3<R> f = contactForce(C, c.lambda, c.penalty, c.friction);
-          R trial = fhypot(c.lambda[0] + c.penalty[0] * C.x, c.lambda[1] + c.penalty[1] * C.y);
+          R trial = fhypot(fmad(c.penalty[0], C.x, c.lambda[0]), fmad(c.penalty[1], C.y, c.lambda[1]));
           bool stick = trial <= -c.friction * f.z && double(fhypot(C.x, C.y)) < 1e-5;
           c.id = (c.id & 0x7fffffff) | (stick ? int(0x80000000u) : 0);
           R fk[3] = {f.x, f.y, f.z}, Ck[3] = {C.x, C.y, C.z};
@@ -1026,7 +1026,7 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
           for (int k = 0; k < 3; ++k) {
             c.lambda[k] = fk[k];
             if (f.z < 0 && (k == 2 || trial <= -c.friction * f.z))
-              c.penalty[k] = mn(c.penalty[k] + M.betaLinear * mabs(Ck[k]), R(1e9));
+              c.penalty[k] = mn(fmad(M.betaLinear, mabs(Ck[k]), c.penalty[k]), R(1e9));
           }
           error = mx(error, mx(R(0), -C.z));
         }
@@ -1049,7 +1049,7 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
           continue;
         V3<R> x = stp.X(b), x0{E.x0[0][b], E.x0[1][b], E.x0[2][b]};
         V3<R> v = (x - x0) * invh;
-        V3<R> w = flogmap(stp.Q(b) * conj(stp.Q0(b))) * invh;
+        V3<R> w = flogmap(fqmul(stp.Q(b), conj(stp.Q0(b)))) * invh;
 #pragma unroll
         for (int k = 0; k < 3; ++k) {
           E.s.v[k][b] = comp(v, k);

@@ -61,9 +61,15 @@ DUCK_HD float frsqrt(float x) {
 #endif
 }
 DUCK_HD double frsqrt(double x) { return 1.0 / sqrt(x); }
+// a * b + c.  The float solver fuses it (one rounding, v_fma_f32 -- nvcc
+// contracts the reference's kernel the same way by default); in double it is
+// the separately rounded a * b + c, so every solver expression written with
+// fmad keeps the float64 oracle's operation order and rounding exactly.
+DUCK_HD float fmad(float a, float b, float c) { return __builtin_fmaf(a, b, c); }
+DUCK_HD double fmad(double a, double b, double c) { return a * b + c; }
 // |(x, y)|: the hardware square root of x^2 + y^2 in float (solver
 // magnitudes are far from overflow), hypot in double.
-DUCK_HD float fhypot(float x, float y) { return fsqrt(x * x + y * y); }
+DUCK_HD float fhypot(float x, float y) { return fsqrt(fmad(x, x, y * y)); }
 DUCK_HD double fhypot(double x, double y) { return hypot(x, y); }
 // a / b: a * rcp(b) in float, a true division in double.
 DUCK_HD float fdiv(float a, float b) { return a * frcp(b); }
@@ -139,14 +145,35 @@ template <class R> DUCK_HD V3<R> logmap(Q4<R> q) {
   return v * k;
 }
 
+// Solver forms of dot, cross, x + s v, rotation and the quaternion product,
+// written with fmad: fused in float; in double the same operations in the
+// same order as dot / cross / operator* / rotate above, so bitwise equal.
+template <class R> DUCK_HD R fdot(V3<R> a, V3<R> b) { return fmad(a.z, b.z, fmad(a.y, b.y, a.x * b.x)); }
+template <class R> DUCK_HD V3<R> fcross(V3<R> a, V3<R> b) {
+  return {fmad(a.y, b.z, -(a.z * b.y)), fmad(a.z, b.x, -(a.x * b.z)), fmad(a.x, b.y, -(a.y * b.x))};
+}
+template <class R> DUCK_HD V3<R> faxpy(R s, V3<R> v, V3<R> x) {
+  return {fmad(s, v.x, x.x), fmad(s, v.y, x.y), fmad(s, v.z, x.z)};
+}
+template <class R> DUCK_HD V3<R> frotate(Q4<R> q, V3<R> v) {
+  V3<R> u{q.x, q.y, q.z};
+  return faxpy(R(2), fcross(u, faxpy(q.w, v, fcross(u, v))), v);
+}
+template <class R> DUCK_HD Q4<R> fqmul(Q4<R> a, Q4<R> b) {
+  return {fmad(-a.z, b.z, fmad(-a.y, b.y, fmad(-a.x, b.x, a.w * b.w))),
+          fmad(-a.z, b.y, fmad(a.y, b.z, fmad(a.x, b.w, a.w * b.x))),
+          fmad(a.z, b.x, fmad(a.y, b.w, fmad(-a.x, b.z, a.w * b.y))),
+          fmad(a.z, b.w, fmad(-a.y, b.x, fmad(a.x, b.y, a.w * b.z)))};
+}
+
 // Fast forms of norm / normalized / expmap / logmap for the float solver
 // (exact forms for double).  Small rotations, the common case inside the
 // block solve, use truncated Taylor series whose first omitted term is below
 // 1e-11 relative on the stated ranges.
-template <class R> DUCK_HD R fnorm(V3<R> a) { return fsqrt(dot(a, a)); }
+template <class R> DUCK_HD R fnorm(V3<R> a) { return fsqrt(fdot(a, a)); }
 template <class R> DUCK_HD Q4<R> fnormalized(Q4<R> q) {
   if constexpr (sizeof(R) == sizeof(float)) {
-    R n2 = q.w * q.w + q.x * q.x + q.y * q.y + q.z * q.z;
+    R n2 = fmad(q.z, q.z, fmad(q.y, q.y, fmad(q.x, q.x, q.w * q.w)));
     if (double(n2) < 1e-30)
       return {R(NAN), R(NAN), R(NAN), R(NAN)};
     R inv = frsqrt(n2);
@@ -161,9 +188,10 @@ template <class R> DUCK_HD Q4<R> fexpmap(V3<R> v) {
     if (a < R(0.25)) {
       R a2 = a * a;
       // sin(a/2)/a and cos(a/2)
-      s = R(0.5) + a2 * (R(-1.0 / 48) + a2 * (R(1.0 / 3840) + a2 * R(-1.0 / 645120)));
-      c = R(1) + a2 * (R(-0.125) + a2 * (R(1.0 / 384) + a2 * (R(-1.0 / 46080) +
-                                                               a2 * R(1.0 / 10321920))));
+      s = fmad(a2, fmad(a2, fmad(a2, R(-1.0 / 645120), R(1.0 / 3840)), R(-1.0 / 48)), R(0.5));
+      c = fmad(a2, fmad(a2, fmad(a2, fmad(a2, R(1.0 / 10321920), R(-1.0 / 46080)), R(1.0 / 384)),
+                        R(-0.125)),
+               R(1));
     } else {
       s = msin(a / R(2)) / a;
       c = mcos(a / R(2));
@@ -185,8 +213,9 @@ template <class R> DUCK_HD V3<R> flogmap(Q4<R> q) {
     } else if (q.w > R(0.99)) {
       // 2 atan(s/w)/s = (2/w) atan(t)/t with t = s/w < 0.143
       R iw = frcp(q.w), t = s * iw, t2 = t * t;
-      R p = R(1) + t2 * (R(-1.0 / 3) + t2 * (R(0.2) + t2 * (R(-1.0 / 7) +
-                                                            t2 * (R(1.0 / 9) + t2 * R(-1.0 / 11)))));
+      R p = fmad(t2, fmad(t2, fmad(t2, fmad(t2, fmad(t2, R(-1.0 / 11), R(1.0 / 9)), R(-1.0 / 7)), R(0.2)),
+                          R(-1.0 / 3)),
+                 R(1));
       k = (R(2) * iw) * p;
     } else {
       k = R(2) * matan2(s, q.w) / s;
@@ -197,24 +226,24 @@ template <class R> DUCK_HD V3<R> flogmap(Q4<R> q) {
   }
 }
 
-// Rotation matrix (row-major) of a unit quaternion, and its product with v.
+// Rotation matrix (row-major) of a unit quaternion, and its product with v
+// (float solver only, fused).
 template <class R> DUCK_HD void quatMatrix(Q4<R> q, R m[9]) {
   const R xx = q.x * q.x, yy = q.y * q.y, zz = q.z * q.z;
   const R xy = q.x * q.y, xz = q.x * q.z, yz = q.y * q.z;
-  const R wx = q.w * q.x, wy = q.w * q.y, wz = q.w * q.z;
-  m[0] = R(1) - R(2) * (yy + zz);
-  m[1] = R(2) * (xy - wz);
-  m[2] = R(2) * (xz + wy);
-  m[3] = R(2) * (xy + wz);
-  m[4] = R(1) - R(2) * (xx + zz);
-  m[5] = R(2) * (yz - wx);
-  m[6] = R(2) * (xz - wy);
-  m[7] = R(2) * (yz + wx);
-  m[8] = R(1) - R(2) * (xx + yy);
+  m[0] = fmad(R(-2), yy + zz, R(1));
+  m[1] = R(2) * fmad(-q.w, q.z, xy);
+  m[2] = R(2) * fmad(q.w, q.y, xz);
+  m[3] = R(2) * fmad(q.w, q.z, xy);
+  m[4] = fmad(R(-2), xx + zz, R(1));
+  m[5] = R(2) * fmad(-q.w, q.x, yz);
+  m[6] = R(2) * fmad(-q.w, q.y, xz);
+  m[7] = R(2) * fmad(q.w, q.x, yz);
+  m[8] = fmad(R(-2), xx + yy, R(1));
 }
 template <class R> DUCK_HD V3<R> matApply(const R m[9], V3<R> v) {
-  return {(m[0] * v.x + m[1] * v.y) + m[2] * v.z, (m[3] * v.x + m[4] * v.y) + m[5] * v.z,
-          (m[6] * v.x + m[7] * v.y) + m[8] * v.z};
+  return {fmad(m[2], v.z, fmad(m[1], v.y, m[0] * v.x)), fmad(m[5], v.z, fmad(m[4], v.y, m[3] * v.x)),
+          fmad(m[8], v.z, fmad(m[7], v.y, m[6] * v.x))};
 }
 
 // IEEE remainder(a, 2*pi) in double: n = nearest integer of a/(2 pi), then the

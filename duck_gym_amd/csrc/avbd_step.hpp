@@ -41,27 +41,27 @@ template <class R> struct Hess {
 
 // Row (0, r).
 template <class R> DUCK_HD void stampAngular(Hess<R> &H, V3<R> r, R f, R kk) {
-  H.g[3] += r.x * f;
-  H.g[4] += r.y * f;
-  H.g[5] += r.z * f;
+  H.g[3] = fmad(r.x, f, H.g[3]);
+  H.g[4] = fmad(r.y, f, H.g[4]);
+  H.g[5] = fmad(r.z, f, H.g[5]);
   R r0 = kk * r.x, r1 = kk * r.y, r2 = kk * r.z;
-  H.h[tri(3, 3)] += r0 * r.x;
-  H.h[tri(4, 3)] += r1 * r.x;
-  H.h[tri(4, 4)] += r1 * r.y;
-  H.h[tri(5, 3)] += r2 * r.x;
-  H.h[tri(5, 4)] += r2 * r.y;
-  H.h[tri(5, 5)] += r2 * r.z;
+  H.h[tri(3, 3)] = fmad(r0, r.x, H.h[tri(3, 3)]);
+  H.h[tri(4, 3)] = fmad(r1, r.x, H.h[tri(4, 3)]);
+  H.h[tri(4, 4)] = fmad(r1, r.y, H.h[tri(4, 4)]);
+  H.h[tri(5, 3)] = fmad(r2, r.x, H.h[tri(5, 3)]);
+  H.h[tri(5, 4)] = fmad(r2, r.y, H.h[tri(5, 4)]);
+  H.h[tri(5, 5)] = fmad(r2, r.z, H.h[tri(5, 5)]);
 }
 // General row (t, r).
 template <class R> DUCK_HD void stampFull(Hess<R> &H, V3<R> t, V3<R> r, R f, R kk) {
   R J[6] = {t.x, t.y, t.z, r.x, r.y, r.z};
 #pragma unroll
   for (int i = 0; i < 6; ++i) {
-    H.g[i] += J[i] * f;
+    H.g[i] = fmad(J[i], f, H.g[i]);
     R ki = kk * J[i];
 #pragma unroll
     for (int j = 0; j <= i; ++j)
-      H.h[tri(i, j)] += ki * J[j];
+      H.h[tri(i, j)] = fmad(ki, J[j], H.h[tri(i, j)]);
   }
 }
 // Row with t = s e_k and r x e_k (a hinge anchor row or a ground-contact
@@ -71,31 +71,31 @@ template <class R> DUCK_HD void stampAxisRow(Hess<R> &H, int k, R s, V3<R> r, R 
   R u0 = k == 0 ? R(0) : (k == 1 ? -r.z : r.y);
   R u1 = k == 1 ? R(0) : (k == 0 ? r.z : -r.x);
   R u2 = k == 2 ? R(0) : (k == 0 ? -r.y : r.x);
-  H.g[k] += s * f;
+  H.g[k] = fmad(s, f, H.g[k]);
   H.h[tri(k, k)] += kk;
   R ks = kk * s;
   if (k != 0) {
-    H.g[3] += u0 * f;
-    H.h[tri(3, k)] += ks * u0;
-    H.h[tri(3, 3)] += (kk * u0) * u0;
+    H.g[3] = fmad(u0, f, H.g[3]);
+    H.h[tri(3, k)] = fmad(ks, u0, H.h[tri(3, k)]);
+    H.h[tri(3, 3)] = fmad(kk * u0, u0, H.h[tri(3, 3)]);
   }
   if (k != 1) {
-    H.g[4] += u1 * f;
-    H.h[tri(4, k)] += ks * u1;
-    H.h[tri(4, 4)] += (kk * u1) * u1;
+    H.g[4] = fmad(u1, f, H.g[4]);
+    H.h[tri(4, k)] = fmad(ks, u1, H.h[tri(4, k)]);
+    H.h[tri(4, 4)] = fmad(kk * u1, u1, H.h[tri(4, 4)]);
   }
   if (k != 2) {
-    H.g[5] += u2 * f;
-    H.h[tri(5, k)] += ks * u2;
-    H.h[tri(5, 5)] += (kk * u2) * u2;
+    H.g[5] = fmad(u2, f, H.g[5]);
+    H.h[tri(5, k)] = fmad(ks, u2, H.h[tri(5, k)]);
+    H.h[tri(5, 5)] = fmad(kk * u2, u2, H.h[tri(5, 5)]);
   }
   // the one off-diagonal rotational entry between the two non-zero components
   if (k == 0)
-    H.h[tri(5, 4)] += (kk * u2) * u1;
+    H.h[tri(5, 4)] = fmad(kk * u2, u1, H.h[tri(5, 4)]);
   else if (k == 1)
-    H.h[tri(5, 3)] += (kk * u2) * u0;
+    H.h[tri(5, 3)] = fmad(kk * u2, u0, H.h[tri(5, 3)]);
   else
-    H.h[tri(4, 3)] += (kk * u1) * u0;
+    H.h[tri(4, 3)] = fmad(kk * u1, u0, H.h[tri(4, 3)]);
 }
 
 // Column norms, per unit |f|, of 0.5 (r f^T + f r^T) - (r.f) I for f along
@@ -103,16 +103,15 @@ template <class R> DUCK_HD void stampAxisRow(Hess<R> &H, int k, R s, V3<R> r, R 
 // 0.5 sqrt(r_i^2 + r_j^2) and column i is sqrt(r_i^2 / 4 + r_k^2).
 template <class R> DUCK_HD void axisGeometricNorms(V3<R> r, R g[3][3]) {
   const R q0 = r.x * r.x, q1 = r.y * r.y, q2 = r.z * r.z;
-  const R h0 = R(0.25) * q0, h1 = R(0.25) * q1, h2 = R(0.25) * q2;
-  g[0][0] = R(0.5) * fsqrt(q1 + q2);
-  g[0][1] = fsqrt(h1 + q0);
-  g[0][2] = fsqrt(h2 + q0);
-  g[1][0] = fsqrt(h0 + q1);
-  g[1][1] = R(0.5) * fsqrt(q0 + q2);
-  g[1][2] = fsqrt(h2 + q1);
-  g[2][0] = fsqrt(h0 + q2);
-  g[2][1] = fsqrt(h1 + q2);
-  g[2][2] = R(0.5) * fsqrt(q0 + q1);
+  g[0][0] = R(0.5) * fsqrt(fmad(r.y, r.y, q2));
+  g[0][1] = fsqrt(fmad(R(0.25), q1, q0));
+  g[0][2] = fsqrt(fmad(R(0.25), q2, q0));
+  g[1][0] = fsqrt(fmad(R(0.25), q0, q1));
+  g[1][1] = R(0.5) * fsqrt(fmad(r.x, r.x, q2));
+  g[1][2] = fsqrt(fmad(R(0.25), q2, q1));
+  g[2][0] = fsqrt(fmad(R(0.25), q0, q2));
+  g[2][1] = fsqrt(fmad(R(0.25), q1, q2));
+  g[2][2] = R(0.5) * fsqrt(fmad(r.x, r.x, q1));
 }
 
 // Diagonal majorisation of the rotational geometric stiffness
@@ -121,16 +120,17 @@ template <class R> DUCK_HD void axisGeometricNorms(V3<R> r, R g[3][3]) {
 // The 3x3 matrix is symmetric (its off-diagonal entries are bitwise equal:
 // IEEE + and * commute), so six entries are formed; column sums keep row order.
 template <class R> DUCK_HD void geometricAdd(Hess<R> &H, V3<R> r, V3<R> f) {
-  R rf = dot(r, f);
-  R a00 = R(0.5) * (r.x * f.x + f.x * r.x) - rf;
-  R a11 = R(0.5) * (r.y * f.y + f.y * r.y) - rf;
-  R a22 = R(0.5) * (r.z * f.z + f.z * r.z) - rf;
-  R a01 = R(0.5) * (r.x * f.y + f.x * r.y);
-  R a02 = R(0.5) * (r.x * f.z + f.x * r.z);
-  R a12 = R(0.5) * (r.y * f.z + f.y * r.z);
-  H.h[tri(3, 3)] += fsqrt(((R(0) + a00 * a00) + a01 * a01) + a02 * a02);
-  H.h[tri(4, 4)] += fsqrt(((R(0) + a01 * a01) + a11 * a11) + a12 * a12);
-  H.h[tri(5, 5)] += fsqrt(((R(0) + a02 * a02) + a12 * a12) + a22 * a22);
+  R rf = fdot(r, f);
+  R a00 = fmad(R(0.5), r.x * f.x + f.x * r.x, -rf);
+  R a11 = fmad(R(0.5), r.y * f.y + f.y * r.y, -rf);
+  R a22 = fmad(R(0.5), r.z * f.z + f.z * r.z, -rf);
+  R a01 = R(0.5) * fmad(r.x, f.y, f.x * r.y);
+  R a02 = R(0.5) * fmad(r.x, f.z, f.x * r.z);
+  R a12 = R(0.5) * fmad(r.y, f.z, f.y * r.z);
+  // (0 + a^2) is a^2: a square is never -0.
+  H.h[tri(3, 3)] += fsqrt(fmad(a02, a02, fmad(a01, a01, a00 * a00)));
+  H.h[tri(4, 4)] += fsqrt(fmad(a12, a12, fmad(a11, a11, a01 * a01)));
+  H.h[tri(5, 5)] += fsqrt(fmad(a22, a22, fmad(a12, a12, a02 * a02)));
 }
 
 // Cholesky solve of H x = -g with NaN on a bad pivot (kernel.cuh:177-228).
@@ -144,7 +144,7 @@ template <class R> DUCK_HD void solve6(const Hess<R> &H, R x[6]) {
       R v = H.h[tri(i, j)];
 #pragma unroll
       for (int k = 0; k < j; ++k)
-        v -= L[tri(i, k)] * L[tri(j, k)];
+        v = fmad(-L[tri(i, k)], L[tri(j, k)], v);
       if (i == j) {
         if (!(v > 0) || !mfinite(v)) {
 #pragma unroll
@@ -165,7 +165,7 @@ template <class R> DUCK_HD void solve6(const Hess<R> &H, R x[6]) {
     y[i] = -H.g[i];
 #pragma unroll
     for (int k = 0; k < i; ++k)
-      y[i] -= L[tri(i, k)] * y[k];
+      y[i] = fmad(-L[tri(i, k)], y[k], y[i]);
     y[i] = fdivInv(y[i], L[tri(i, i)], inv[i]);
   }
 #pragma unroll
@@ -173,7 +173,7 @@ template <class R> DUCK_HD void solve6(const Hess<R> &H, R x[6]) {
     x[i] = y[i];
 #pragma unroll
     for (int k = i + 1; k < 6; ++k)
-      x[i] -= L[tri(k, i)] * x[k];
+      x[i] = fmad(-L[tri(k, i)], x[k], x[i]);
     x[i] = fdivInv(x[i], L[tri(i, i)], inv[i]);
   }
 }
@@ -186,9 +186,9 @@ template <class R> DUCK_HD R logJacobianCoef(R a) {
   if constexpr (sizeof(R) == sizeof(float)) {
     if (a < R(0.5)) {
       R a2 = a * a;
-      return R(1.0 / 12) +
-             a2 * (R(1.0 / 720) + a2 * (R(1.0 / 30240) + a2 * (R(1.0 / 1209600) +
-                                                                a2 * R(1.0 / 47900160))));
+      return fmad(a2, fmad(a2, fmad(a2, fmad(a2, R(1.0 / 47900160), R(1.0 / 1209600)), R(1.0 / 30240)),
+                           R(1.0 / 720)),
+                  R(1.0 / 12));
     }
   }
   double ad = double(a);
@@ -204,8 +204,8 @@ template <class R> DUCK_HD V3<R> unitAxis(int k) {
 // Coulomb-projected contact force (kernel.cuh:304-315).
 template <class R> DUCK_HD V3<R> contactForce(V3<R> C, const R lambda[3], const R penalty[3],
                                               R friction) {
-  V3<R> f{lambda[0] + penalty[0] * C.x, lambda[1] + penalty[1] * C.y,
-          lambda[2] + penalty[2] * C.z};
+  V3<R> f{fmad(penalty[0], C.x, lambda[0]), fmad(penalty[1], C.y, lambda[1]),
+          fmad(penalty[2], C.z, lambda[2])};
   f.z = mn(f.z, R(0));
   R t = fhypot(f.x, f.y), bound = -friction * f.z;
   if (t > bound && t > 0) {
@@ -241,10 +241,10 @@ __device__ __forceinline__ double halfSwap(double v) {
 // R diag(I) R^T of the body inertia at orientation q, as its six entries
 // (xx, yy, zz, xy, xz, yz), and the product of such a matrix with v.
 template <class R> DUCK_HD void inertiaWorld(Q4<R> q, V3<R> I, R out[6]) {
-  V3<R> c0 = rotate(q, V3<R>{1, 0, 0}), c1 = rotate(q, V3<R>{0, 1, 0}),
-        c2 = rotate(q, V3<R>{0, 0, 1}); // columns of R
+  V3<R> c0 = frotate(q, V3<R>{1, 0, 0}), c1 = frotate(q, V3<R>{0, 1, 0}),
+        c2 = frotate(q, V3<R>{0, 0, 1}); // columns of R
   auto entry = [&](R a0, R a1, R a2, R b0, R b1, R b2) {
-    return (a0 * I.x * b0 + a1 * I.y * b1) + a2 * I.z * b2;
+    return fmad(a2 * I.z, b2, fmad(a1 * I.y, b1, a0 * I.x * b0));
   };
   out[0] = entry(c0.x, c1.x, c2.x, c0.x, c1.x, c2.x);
   out[1] = entry(c0.y, c1.y, c2.y, c0.y, c1.y, c2.y);
@@ -254,8 +254,8 @@ template <class R> DUCK_HD void inertiaWorld(Q4<R> q, V3<R> I, R out[6]) {
   out[5] = entry(c0.y, c1.y, c2.y, c0.z, c1.z, c2.z);
 }
 template <class R> DUCK_HD V3<R> symApply(const R m[6], V3<R> v) {
-  return {(m[0] * v.x + m[3] * v.y) + m[4] * v.z, (m[3] * v.x + m[1] * v.y) + m[5] * v.z,
-          (m[4] * v.x + m[5] * v.y) + m[2] * v.z};
+  return {fmad(m[4], v.z, fmad(m[3], v.y, m[0] * v.x)), fmad(m[5], v.z, fmad(m[1], v.y, m[3] * v.x)),
+          fmad(m[2], v.z, fmad(m[5], v.y, m[4] * v.x))};
 }
 
 // Lane (i - N) mod 16 of the same 16-lane row (DPP row_ror:N).
@@ -309,7 +309,7 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
   }
   // Inertia frozen at q0 (kernel.cuh:275-280).
   DUCK_HD V3<R> inertiaApply(Q4<R> q0, V3<R> I, V3<R> w, bool inverse) const {
-    V3<R> l = rotate(conj(q0), w);
+    V3<R> l = frotate(conj(q0), w);
     if (inverse) {
       l.x *= R(1) / I.x;
       l.y *= R(1) / I.y;
@@ -319,7 +319,7 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
       l.y *= I.y;
       l.z *= I.z;
     }
-    return rotate(q0, l);
+    return frotate(q0, l);
   }
   DUCK_HD R groundFriction(int shape) const {
     return E.s.friction >= 0 ? E.s.friction : F.shapeFriction[shape];
@@ -348,21 +348,21 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
       o.axisB = matApply(mb, frame(F.axisB, ji));
       u = matApply(mb, frame(F.tangentB, ji));
     } else {
-      o.ra = rotate(qa, frame(F.ra, ji));
-      o.rb = rotate(qb, frame(F.rb, ji));
-      o.axis = rotate(qa, frame(F.axisA, ji));
-      o.axisB = rotate(qb, frame(F.axisB, ji));
-      o.t1 = rotate(qa, frame(F.tangentA, ji));
-      u = rotate(qb, frame(F.tangentB, ji));
+      o.ra = frotate(qa, frame(F.ra, ji));
+      o.rb = frotate(qb, frame(F.rb, ji));
+      o.axis = frotate(qa, frame(F.axisA, ji));
+      o.axisB = frotate(qb, frame(F.axisB, ji));
+      o.t1 = frotate(qa, frame(F.tangentA, ji));
+      u = frotate(qb, frame(F.tangentB, ji));
     }
     V3<R> d = ((X(a) + o.ra) - X(b)) - o.rb;
-    o.t2 = cross(o.axis, o.t1);
-    o.angle = matan2(dot(o.axis, cross(o.t1, u)), dot(o.t1, u));
+    o.t2 = fcross(o.axis, o.t1);
+    o.angle = matan2(fdot(o.axis, fcross(o.t1, u)), fdot(o.t1, u));
     o.C[0] = d.x;
     o.C[1] = d.y;
     o.C[2] = d.z;
-    o.C[3] = dot(o.t1, o.axisB);
-    o.C[4] = dot(o.t2, o.axisB);
+    o.C[3] = fdot(o.t1, o.axisB);
+    o.C[4] = fdot(o.t2, o.axisB);
     o.C[5] = o.angle - F.lo[ji];
     o.C[6] = F.hi[ji] - o.angle;
     return o;
@@ -371,19 +371,19 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
   // Ground contact values in the fixed world basis (kernel.cuh:805-827).
   DUCK_HD V3<R> groundC(const GroundContact<R> &c, V3<R> &ra) const {
     int b = gcBody(c.id);
-    ra = rotate(Q(b), V3<R>{c.local[0], c.local[1], c.local[2]});
+    ra = frotate(Q(b), V3<R>{c.local[0], c.local[1], c.local[2]});
     V3<R> delta = (X(b) + ra) - V3<R>{c.anchor[0], c.anchor[1], R(0)};
-    delta.z -= M.alpha * c.c0;
+    delta.z = fmad(-M.alpha, c.c0, delta.z);
     return delta;
   }
   DUCK_HD V3<R> selfC(const SelfContact<R> &c, V3<R> &ra, V3<R> &rb) const {
     int a = scBody(c.id), b = scOther(c.id);
-    ra = rotate(Q(a), V3<R>{c.local[0], c.local[1], c.local[2]});
-    rb = rotate(Q(b), V3<R>{c.localB[0], c.localB[1], c.localB[2]});
+    ra = frotate(Q(a), V3<R>{c.local[0], c.local[1], c.local[2]});
+    rb = frotate(Q(b), V3<R>{c.localB[0], c.localB[1], c.localB[2]});
     V3<R> delta = ((X(a) + ra) - X(b)) - rb;
     V3<R> t1{c.t1[0], c.t1[1], c.t1[2]}, t2{c.t2[0], c.t2[1], c.t2[2]}, n{c.n[0], c.n[1], c.n[2]};
-    V3<R> C{dot(delta, t1), dot(delta, t2), dot(delta, n)};
-    C.z -= M.alpha * c.c0;
+    V3<R> C{fdot(delta, t1), fdot(delta, t2), fdot(delta, n)};
+    C.z = fmad(-M.alpha, c.c0, C.z);
     return C;
   }
 
@@ -418,13 +418,13 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
     // rotational column, plus the linear block), part 1 to rotJ[1] and
     // rotJ[2] (the other three rotational entries).
     if (part < 2) {
-      V3<R> theta = flogmap(q * conj(qp));
+      V3<R> theta = flogmap(fqmul(q, conj(qp)));
       R coef = logJacobianCoef(fnorm(theta));
       V3<R> rotJ[3];
 #pragma unroll
       for (int k = 0; k < 3; ++k) {
         V3<R> e = unitAxis<R>(k);
-        rotJ[k] = (e - R(0.5) * cross(theta, e)) + coef * cross(theta, cross(theta, e));
+        rotJ[k] = faxpy(coef, fcross(theta, fcross(theta, e)), faxpy(R(-0.5), fcross(theta, e), e));
       }
       // World inertia at q0, formed once per step by the predictor.
       const R Iw[6] = {E.Iw[0][bi], E.Iw[1][bi], E.Iw[2][bi], E.Iw[3][bi], E.Iw[4][bi], E.Iw[5][bi]};
@@ -443,23 +443,23 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
         V3<R> IJ[3] = {symApply(Iw, rotJ[0]), symApply(Iw, rotJ[1]), symApply(Iw, rotJ[2])};
 #pragma unroll
         for (int k = 0; k < 3; ++k) {
-          H.g[3 + k] = fdivInv(dot(rotJ[k], It), h2, ih2);
+          H.g[3 + k] = fdivInv(fdot(rotJ[k], It), h2, ih2);
 #pragma unroll
           for (int l = 0; l <= k; ++l)
-            H.h[tri(3 + k, 3 + l)] = fdivInv(dot(rotJ[k], IJ[l]), h2, ih2);
+            H.h[tri(3 + k, 3 + l)] = fdivInv(fdot(rotJ[k], IJ[l]), h2, ih2);
         }
       } else {
         const bool first = part == 0;
         const V3<R> A = symApply(Iw, first ? theta : rotJ[1]);
         const V3<R> Bv = symApply(Iw, first ? rotJ[0] : rotJ[2]);
-        const R d0 = fdivInv(dot(rotJ[0], A), h2, ih2), d1 = fdivInv(dot(rotJ[1], A), h2, ih2),
-                d2 = fdivInv(dot(rotJ[2], A), h2, ih2);
-        const R e1 = fdivInv(dot(rotJ[1], Bv), h2, ih2), e2 = fdivInv(dot(rotJ[2], Bv), h2, ih2);
+        const R d0 = fdivInv(fdot(rotJ[0], A), h2, ih2), d1 = fdivInv(fdot(rotJ[1], A), h2, ih2),
+                d2 = fdivInv(fdot(rotJ[2], A), h2, ih2);
+        const R e1 = fdivInv(fdot(rotJ[1], Bv), h2, ih2), e2 = fdivInv(fdot(rotJ[2], Bv), h2, ih2);
         if (first) {
           H.g[3] = d0;
           H.g[4] = d1;
           H.g[5] = d2;
-          H.h[tri(3, 3)] = fdivInv(dot(rotJ[0], Bv), h2, ih2);
+          H.h[tri(3, 3)] = fdivInv(fdot(rotJ[0], Bv), h2, ih2);
           H.h[tri(4, 3)] = e1;
           H.h[tri(5, 3)] = e2;
         } else {
@@ -493,30 +493,30 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
       R fr[5], pr[5];
 #pragma unroll
       for (int k = 0; k < 5; ++k) {
-        const R c = je.C[k] - alpha * E.c0[k][ji];
+        const R c = fmad(-alpha, E.c0[k][ji], je.C[k]);
         pr[k] = E.s.penalty[k][ji];
-        fr[k] = E.s.lambda[k][ji] + pr[k] * c;
+        fr[k] = fmad(pr[k], c, E.s.lambda[k][ji]);
       }
 #pragma unroll
       for (int k = 0; k < 3; ++k) {
         stampAxisRow(H, k, s, r, fr[k], pr[k]);
         const R af = mabs(fr[k]);
-        H.h[tri(3, 3)] += af * geo[k][0];
-        H.h[tri(4, 4)] += af * geo[k][1];
-        H.h[tri(5, 5)] += af * geo[k][2];
+        H.h[tri(3, 3)] = fmad(af, geo[k][0], H.h[tri(3, 3)]);
+        H.h[tri(4, 4)] = fmad(af, geo[k][1], H.h[tri(4, 4)]);
+        H.h[tri(5, 5)] = fmad(af, geo[k][2], H.h[tri(5, 5)]);
       }
 #pragma unroll
       for (int k = 3; k < 5; ++k) {
         const V3<R> t = k == 3 ? je.t1 : je.t2;
-        stampAngular(H, parent ? cross(t, je.axisB) : cross(je.axisB, t), fr[k], pr[k]);
+        stampAngular(H, parent ? fcross(t, je.axisB) : fcross(je.axisB, t), fr[k], pr[k]);
         geometricAdd(H, parent ? t : je.axisB, (parent ? je.axisB : t) * fr[k]);
       }
       if (F.limited[ji]) {
 #pragma unroll
         for (int k = 5; k < 7; ++k) {
-          const R c = je.C[k] - alpha * mn(E.c0[k][ji], R(0));
+          const R c = fmad(-alpha, mn(E.c0[k][ji], R(0)), je.C[k]);
           const R pen = E.s.penalty[k][ji];
-          const R f = mn(E.s.lambda[k][ji] + pen * c, R(0));
+          const R f = mn(fmad(pen, c, E.s.lambda[k][ji]), R(0));
           if (f < 0)
             stampAngular(H, (k == 5) == parent ? -je.axis : je.axis, f, pen);
         }
@@ -528,7 +528,7 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
       R wTarget, delta;
       wrapAngle2(je.angle - E.s.target[ji], je.angle - E.angle0[ji], wTarget, delta);
       const R kp = E.s.kp[ji], maxT = E.s.maxTorque[ji];
-      R drive = kp * wTarget - E.s.torque[ji];
+      R drive = fmad(kp, wTarget, -E.s.torque[ji]);
       const bool capped = maxT > 0;
       const R ks = capped && mabs(drive) >= maxT ? R(0) : kp;
       drive = capped ? clampv(drive, -maxT, maxT) : drive;
@@ -537,10 +537,10 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
       const R dh = fdivInv(damping, h, ih), ah = fdivInv(armature, h2, ih2);
       const R stiff = dh + ah;
       const bool damped = stiff > 0;
-      axisForce += damped ? dh * delta + ah * (delta - h * E.velocity0[ji]) : R(0);
+      axisForce += damped ? fmad(dh, delta, ah * fmad(-h, E.velocity0[ji], delta)) : R(0);
       axisStiff += damped ? stiff : R(0);
       const R fl = E.s.frictionloss[ji];
-      const R trial = E.s.lambdaF[ji] + E.s.penaltyF[ji] * delta;
+      const R trial = fmad(E.s.penaltyF[ji], delta, E.s.lambdaF[ji]);
       axisForce += fl > 0 ? clampv(trial, -fl, fl) : R(0);
       axisStiff += fl > 0 && mabs(trial) < fl ? E.s.penaltyF[ji] : R(0);
       stampAngular(H, J5, axisForce, axisStiff);
@@ -584,7 +584,7 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
 #pragma unroll
         for (int k = 0; k < 3; ++k) {
           V3<R> e = basis[k] * sign;
-          stampFull(H, e, cross(r, e), fk[k], c.penalty[k]);
+          stampFull(H, e, fcross(r, e), fk[k], c.penalty[k]);
         }
         V3<R> fw = ((basis[0] * f.x) + (basis[1] * f.y)) + (basis[2] * f.z);
         geometricAdd(H, r, fw * sign);
@@ -630,8 +630,8 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
     const R ntx = fnorm(tx), nrx = fnorm(rx);
     R scale = mn(R(1), mn(fdiv(R(.1), mx(ntx, R(1e-30))), fdiv(R(.25), mx(nrx, R(1e-30)))));
     if (part == 0) {
-      setX(bi, x + scale * tx);
-      setQ(bi, fnormalized(fexpmap(scale * rx) * q));
+      setX(bi, faxpy(scale, tx, x));
+      setQ(bi, fnormalized(fqmul(fexpmap(scale * rx), q)));
     }
     return mx(ntx, nrx) * scale;
   }
