@@ -6,7 +6,7 @@ namespace duckhip {
 
 // Lane (i + N) mod 16 of the same 16-lane row (DPP row_ror:N).
 template <int N> __device__ __forceinline__ int rowRor(int v) {
-  return __builtin_amdgcn_update_dpp(0, v, 0x120 + N, 0xF, 0xF, false);
+  return __builtin_amdgcn_update_dpp(0, v, 0x120 + N, 0xF, 0xF, true);
 }
 template <int N> __device__ __forceinline__ float rowRor(float v) {
   return __int_as_float(rowRor<N>(__float_as_int(v)));

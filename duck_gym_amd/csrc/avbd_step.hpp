@@ -134,9 +134,12 @@ template <class R> DUCK_HD void geometricAdd(Hess<R> &H, V3<R> r, V3<R> f) {
 }
 
 // Cholesky solve of H x = -g with NaN on a bad pivot (kernel.cuh:177-228).
-// The float path multiplies by reciprocal pivots (fdivInv).
+// The float path multiplies by reciprocal pivots (fdivInv).  The factor runs
+// to the end without branching; a non-positive or non-finite pivot anywhere
+// replaces the whole solution by NaN, as the reference's early return does.
 template <class R> DUCK_HD void solve6(const Hess<R> &H, R x[6]) {
   R L[21], inv[6];
+  bool ok = true;
 #pragma unroll
   for (int i = 0; i < 6; ++i) {
 #pragma unroll
@@ -146,12 +149,7 @@ template <class R> DUCK_HD void solve6(const Hess<R> &H, R x[6]) {
       for (int k = 0; k < j; ++k)
         v = fmad(-L[tri(i, k)], L[tri(j, k)], v);
       if (i == j) {
-        if (!(v > 0) || !mfinite(v)) {
-#pragma unroll
-          for (int k = 0; k < 6; ++k)
-            x[k] = R(NAN);
-          return;
-        }
+        ok = ok && v > 0 && mfinite(v);
         L[tri(i, i)] = fsqrt(v);
         inv[i] = frcp(L[tri(i, i)]);
       } else {
@@ -176,6 +174,9 @@ template <class R> DUCK_HD void solve6(const Hess<R> &H, R x[6]) {
       x[i] = fmad(-L[tri(k, i)], x[k], x[i]);
     x[i] = fdivInv(x[i], L[tri(i, i)], inv[i]);
   }
+#pragma unroll
+  for (int k = 0; k < 6; ++k)
+    x[k] = ok ? x[k] : R(NAN);
 }
 
 // (1 - (a/2)/tan(a/2)) / a^2, the SO(3) log-Jacobian coefficient, evaluated
@@ -217,14 +218,17 @@ template <class R> DUCK_HD V3<R> contactForce(V3<R> C, const R lambda[3], const 
 }
 
 // Value of the lane 8 positions away inside the same 16-lane row (DPP
-// row_ror:8, i.e. lane ^ 8): the two halves of a split block solve.
+// row_ror:8, i.e. lane ^ 8): the two halves of a split block solve.  A row
+// rotation reads an in-range lane for every lane, so bound_ctrl (zero for
+// out-of-range sources) changes nothing; it lets the compiler fold the move
+// into the add that consumes it (v_add_f32_dpp).
 __device__ __forceinline__ float pairSwap(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, true));
 }
 __device__ __forceinline__ double pairSwap(double v) {
   const unsigned long long b = static_cast<unsigned long long>(__double_as_longlong(v));
-  const unsigned lo = __builtin_amdgcn_update_dpp(0, int(unsigned(b)), 0x128, 0xF, 0xF, false);
-  const unsigned hi = __builtin_amdgcn_update_dpp(0, int(unsigned(b >> 32)), 0x128, 0xF, 0xF, false);
+  const unsigned lo = __builtin_amdgcn_update_dpp(0, int(unsigned(b)), 0x128, 0xF, 0xF, true);
+  const unsigned hi = __builtin_amdgcn_update_dpp(0, int(unsigned(b >> 32)), 0x128, 0xF, 0xF, true);
   return __longlong_as_double(static_cast<long long>((static_cast<unsigned long long>(hi) << 32) | lo));
 }
 // Value of lane ^ 16 (ds_swizzle, 32-lane groups: and 0x1f, xor 0x10).
@@ -260,12 +264,12 @@ template <class R> DUCK_HD V3<R> symApply(const R m[6], V3<R> v) {
 
 // Lane (i - N) mod 16 of the same 16-lane row (DPP row_ror:N).
 template <int N> __device__ __forceinline__ float rowRotate(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x120 + N, 0xF, 0xF, false));
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x120 + N, 0xF, 0xF, true));
 }
 template <int N> __device__ __forceinline__ double rowRotate(double v) {
   const unsigned long long b = static_cast<unsigned long long>(__double_as_longlong(v));
-  const unsigned lo = __builtin_amdgcn_update_dpp(0, int(unsigned(b)), 0x120 + N, 0xF, 0xF, false);
-  const unsigned hi = __builtin_amdgcn_update_dpp(0, int(unsigned(b >> 32)), 0x120 + N, 0xF, 0xF, false);
+  const unsigned lo = __builtin_amdgcn_update_dpp(0, int(unsigned(b)), 0x120 + N, 0xF, 0xF, true);
+  const unsigned hi = __builtin_amdgcn_update_dpp(0, int(unsigned(b >> 32)), 0x120 + N, 0xF, 0xF, true);
   return __longlong_as_double(static_cast<long long>((static_cast<unsigned long long>(hi) << 32) | lo));
 }
 
