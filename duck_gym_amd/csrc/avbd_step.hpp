@@ -209,11 +209,11 @@ template <class R> DUCK_HD V3<R> contactForce(V3<R> C, const R lambda[3], const 
           fmad(penalty[2], C.z, lambda[2])};
   f.z = mn(f.z, R(0));
   R t = fhypot(f.x, f.y), bound = -friction * f.z;
-  if (t > bound && t > 0) {
-    R ratio = fdiv(bound, t);
-    f.x *= ratio;
-    f.y *= ratio;
-  }
+  // the cone projection, selected rather than branched around
+  const bool cap = t > bound && t > 0;
+  const R ratio = fdiv(bound, t);
+  f.x = cap ? f.x * ratio : f.x;
+  f.y = cap ? f.y * ratio : f.y;
   return f;
 }
 
@@ -326,7 +326,8 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
     return frotate(q0, l);
   }
   DUCK_HD R groundFriction(int shape) const {
-    return E.s.friction >= 0 ? E.s.friction : F.shapeFriction[shape];
+    const R own = E.s.friction, model = F.shapeFriction[shape];
+    return own >= 0 ? own : model;
   }
 
   // Hinge constraint values (kernel.cuh:732-761): anchor (3), axis (2),
@@ -402,80 +403,251 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
   // gives one body two slots (slots 0 and 7, lane and lane ^ 8 in each);
   // `partner` is 1 in slot 0 and 0 in slot 7, and `quad` tells every lane of
   // the wave that such a group exists in this pass.
-  __device__ R updateBody(int bi, bool implicitDrive, int part, int nParts = P, int partner = 0,
-                          bool quad = false) {
-    const R h = M.dt;
-    V3<R> x = X(bi), xp{E.xp[0][bi], E.xp[1][bi], E.xp[2][bi]};
-    Q4<R> q = Q(bi), qp{E.qp[0][bi], E.qp[1][bi], E.qp[2][bi], E.qp[3][bi]}, q0 = Q0(bi);
-    V3<R> I = Inertia(bi);
-    Hess<R> H;
+  // Inertia block (kernel.cuh:837-855), assigned into the zeroed H (the
+  // first terms of every sum).  With P >= 2 the first two lanes share it:
+  // both form theta, the log-Jacobian and rotJ; part 0 applies the world
+  // inertia to theta and rotJ[0] (the g rows and the first rotational
+  // column, plus the linear block), part 1 to rotJ[1] and rotJ[2] (the other
+  // three rotational entries); further parts add nothing.
+  // Fast (float): straight-line, on the small-rotation branches of flogmap
+  // and logJacobianCoef only -- bitwise their results there -- with `slow`
+  // set where a lane's rotation lies outside them.
+  template <bool Fast> __device__ void inertiaBlock(Hess<R> &H, int bi, int part, bool &slow) const {
+    const R h = M.dt, h2 = h * h, ih2 = frcp(h2);
+    const V3<R> x = X(bi), xp{E.xp[0][bi], E.xp[1][bi], E.xp[2][bi]};
+    const Q4<R> q = Q(bi), qp{E.qp[0][bi], E.qp[1][bi], E.qp[2][bi], E.qp[3][bi]};
+    if (!Fast && part >= 2)
+      return;
+    V3<R> theta;
+    R coef;
+    if constexpr (Fast) {
+      // flogmap: normalise, fold to w >= 0, 2 atan(s/w)/s by its series.
+      Q4<R> d = fqmul(q, conj(qp));
+      const R n2 = fmad(d.z, d.z, fmad(d.y, d.y, fmad(d.x, d.x, d.w * d.w)));
+      const R inv = frsqrt(n2);
+      const R sg = d.w * inv < 0 ? R(-1) : R(1);
+      d = {(d.w * inv) * sg, (d.x * inv) * sg, (d.y * inv) * sg, (d.z * inv) * sg};
+      const V3<R> v{d.x, d.y, d.z};
+      const R sv = fnorm(v);
+      const R iw = frcp(d.w), t = sv * iw, t2 = t * t;
+      const R series =
+          fmad(t2, fmad(t2, fmad(t2, fmad(t2, fmad(t2, R(-1.0 / 11), R(1.0 / 9)), R(-1.0 / 7)), R(0.2)),
+                        R(-1.0 / 3)),
+               R(1));
+      const R k = double(sv) < 1e-10 ? R(2) : (R(2) * iw) * series;
+      theta = v * k;
+      const R a = fnorm(theta), a2 = a * a;
+      coef = fmad(a2, fmad(a2, fmad(a2, fmad(a2, R(1.0 / 47900160), R(1.0 / 1209600)), R(1.0 / 30240)),
+                           R(1.0 / 720)),
+                  R(1.0 / 12));
+      slow = slow | (double(n2) < 1e-30) | !(d.w > R(0.99)) | !(a < R(0.5));
+    } else {
+      theta = flogmap(fqmul(q, conj(qp)));
+      coef = logJacobianCoef(fnorm(theta));
+    }
+    V3<R> rotJ[3];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      V3<R> e = unitAxis<R>(k);
+      rotJ[k] = faxpy(coef, fcross(theta, fcross(theta, e)), faxpy(R(-0.5), fcross(theta, e), e));
+    }
+    // World inertia at q0, formed once per step by the predictor.
+    const R Iw[6] = {E.Iw[0][bi], E.Iw[1][bi], E.Iw[2][bi], E.Iw[3][bi], E.Iw[4][bi], E.Iw[5][bi]};
+    const bool first = part == 0, second = part == 1;
+    const V3<R> dx = x - xp;
+    const R mh = fdivInv(E.s.mass[bi], h2, ih2);
+    H.h[tri(0, 0)] = first ? mh : R(0);
+    H.h[tri(1, 1)] = first ? mh : R(0);
+    H.h[tri(2, 2)] = first ? mh : R(0);
+    H.g[0] = first ? mh * dx.x : R(0);
+    H.g[1] = first ? mh * dx.y : R(0);
+    H.g[2] = first ? mh * dx.z : R(0);
+    if constexpr (P == 1) {
+      V3<R> It = symApply(Iw, theta);
+      V3<R> IJ[3] = {symApply(Iw, rotJ[0]), symApply(Iw, rotJ[1]), symApply(Iw, rotJ[2])};
+#pragma unroll
+      for (int k = 0; k < 3; ++k) {
+        H.g[3 + k] = fdivInv(fdot(rotJ[k], It), h2, ih2);
+#pragma unroll
+        for (int l = 0; l <= k; ++l)
+          H.h[tri(3 + k, 3 + l)] = fdivInv(fdot(rotJ[k], IJ[l]), h2, ih2);
+      }
+    } else {
+      const V3<R> A = symApply(Iw, first ? theta : rotJ[1]);
+      const V3<R> Bv = symApply(Iw, first ? rotJ[0] : rotJ[2]);
+      const R d0 = fdivInv(fdot(rotJ[0], A), h2, ih2), d1 = fdivInv(fdot(rotJ[1], A), h2, ih2),
+              d2 = fdivInv(fdot(rotJ[2], A), h2, ih2);
+      const R e0 = fdivInv(fdot(rotJ[0], Bv), h2, ih2), e1 = fdivInv(fdot(rotJ[1], Bv), h2, ih2),
+              e2 = fdivInv(fdot(rotJ[2], Bv), h2, ih2);
+      H.g[3] = first ? d0 : R(0);
+      H.g[4] = first ? d1 : R(0);
+      H.g[5] = first ? d2 : R(0);
+      H.h[tri(3, 3)] = first ? e0 : R(0);
+      H.h[tri(4, 3)] = first ? e1 : R(0);
+      H.h[tri(5, 3)] = first ? e2 : R(0);
+      H.h[tri(4, 4)] = second ? d1 : R(0);
+      H.h[tri(5, 4)] = second ? d2 : R(0);
+      H.h[tri(5, 5)] = second ? e2 : R(0);
+    }
+  }
+
+  // Rows of one hinge adjacent to body bi (kernel.cuh:861-913); `cur` packs
+  // (hinge, body a, body b).  With valid false the rows are stamped with zero
+  // Jacobian, force and stiffness (indices clamped in range), so the same
+  // straight-line code serves a lane without a hinge in this slot.
+  // Fast: both wrapped angles on wrapAngle's |a| < 3.14159 branch, `slow`
+  // set otherwise.
+  template <bool Fast>
+  __device__ void hingeRows(Hess<R> &H, int bi, int cur, bool valid, bool implicitDrive,
+                            bool &slow) const {
+    const R h = M.dt, h2 = h * h, ih2 = frcp(h2), ih = frcp(h), alpha = M.alpha;
+    const int ji = valid ? cur & 255 : 0, ja = valid ? (cur >> 8) & 255 : 0,
+              jb = valid ? (cur >> 16) & 255 : 0;
+    const bool parent = bi == ja;
+    const R s = parent ? R(1) : R(-1);
+    JointEval je = evalJoint(ji, ja, jb);
+    if (!Fast && !valid)
+      return;
+    if (Fast) {
+      auto z = [&](V3<R> v) { return valid ? v : V3<R>{0, 0, 0}; };
+      je.ra = z(je.ra);
+      je.rb = z(je.rb);
+      je.axis = z(je.axis);
+      je.axisB = z(je.axisB);
+      je.t1 = z(je.t1);
+      je.t2 = z(je.t2);
+    }
+    // Anchor rows (k = 0..2): J_k = [s e_k, r x e_k] with r = ra (parent)
+    // or -rb (child); their geometric terms share r.  Anchor and axis rows
+    // are always active; the limit rows on limited hinges with f < 0 (the
+    // rest are stamped with zeros, which adds nothing).
+    const V3<R> r = parent ? je.ra : -je.rb;
+    R geo[3][3];
+    axisGeometricNorms(r, geo);
+    R fr[5], pr[5];
+#pragma unroll
+    for (int k = 0; k < 5; ++k) {
+      // loads first, selects after: a conditional load would be a branch
+      const R c = fmad(-alpha, E.c0[k][ji], je.C[k]);
+      const R pen = E.s.penalty[k][ji], lam = E.s.lambda[k][ji];
+      pr[k] = valid ? pen : R(0);
+      fr[k] = valid ? fmad(pen, c, lam) : R(0);
+    }
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      stampAxisRow(H, k, s, r, fr[k], pr[k]);
+      const R af = mabs(fr[k]);
+      H.h[tri(3, 3)] = fmad(af, geo[k][0], H.h[tri(3, 3)]);
+      H.h[tri(4, 4)] = fmad(af, geo[k][1], H.h[tri(4, 4)]);
+      H.h[tri(5, 5)] = fmad(af, geo[k][2], H.h[tri(5, 5)]);
+    }
+#pragma unroll
+    for (int k = 3; k < 5; ++k) {
+      const V3<R> t = k == 3 ? je.t1 : je.t2;
+      // operands selected before the product (one straight-line cross)
+      const V3<R> u = parent ? t : je.axisB, w = parent ? je.axisB : t;
+      stampAngular(H, fcross(u, w), fr[k], pr[k]);
+      geometricAdd(H, u, w * fr[k]);
+    }
+    const int lim = F.limited[ji];
+    const bool limited = valid & (lim != 0);
+#pragma unroll
+    for (int k = 5; k < 7; ++k) {
+      const R c = fmad(-alpha, mn(E.c0[k][ji], R(0)), je.C[k]);
+      const R pen = E.s.penalty[k][ji];
+      const R f = mn(fmad(pen, c, E.s.lambda[k][ji]), R(0));
+      const bool on = limited && f < 0;
+      stampAngular(H, (k == 5) == parent ? -je.axis : je.axis, on ? f : R(0), on ? pen : R(0));
+    }
+    // Rows along the hinge axis (kernel.cuh:893-913): implicit torque-
+    // limited PD potential, damping/armature, dry friction -- one stamp
+    // with the summed force and stiffness, selected without branches.
+    const V3<R> J5 = parent ? -je.axis : je.axis;
+    R wTarget, delta;
+    const R a0 = je.angle - E.s.target[ji], a1 = je.angle - E.angle0[ji];
+    if constexpr (Fast) {
+      wTarget = a0 + R(0);
+      delta = a1 + R(0);
+      slow = slow | (valid & !((mabs(a0) < R(3.14159)) & (mabs(a1) < R(3.14159))));
+    } else {
+      wrapAngle2(a0, a1, wTarget, delta);
+    }
+    const R kp = E.s.kp[ji], maxT = E.s.maxTorque[ji];
+    R drive = fmad(kp, wTarget, -E.s.torque[ji]);
+    const bool capped = maxT > 0;
+    const R ks = capped && mabs(drive) >= maxT ? R(0) : kp;
+    drive = capped ? clampv(drive, -maxT, maxT) : drive;
+    R axisForce = implicitDrive ? drive : R(0), axisStiff = implicitDrive ? ks : R(0);
+    const R damping = E.s.damping[ji], armature = F.armature[ji], w0 = E.velocity0[ji];
+    const R dh = fdivInv(damping, h, ih), ah = fdivInv(armature, h2, ih2);
+    const R stiff = dh + ah;
+    const bool damped = stiff > 0;
+    axisForce += damped ? fmad(dh, delta, ah * fmad(-h, w0, delta)) : R(0);
+    axisStiff += damped ? stiff : R(0);
+    const R fl = E.s.frictionloss[ji];
+    const R trial = fmad(E.s.penaltyF[ji], delta, E.s.lambdaF[ji]);
+    axisForce += fl > 0 ? clampv(trial, -fl, fl) : R(0);
+    axisStiff += fl > 0 && mabs(trial) < fl ? E.s.penaltyF[ji] : R(0);
+    stampAngular(H, J5, valid ? axisForce : R(0), valid ? axisStiff : R(0));
+  }
+
+  // Rows of ground contact `index` of body bi (kernel.cuh:915-931).  A
+  // separating contact (f.z = 0) is stamped with zero force and stiffness;
+  // with valid false the lever arm is zero as well (index clamped in range).
+  __device__ void groundRows(Hess<R> &H, int bi, int index, bool valid) const {
+    const GroundContact<R> &c = E.s.gc[valid ? index : 0];
+    const int id = c.id;
+    V3<R> ra = frotate(Q(bi), V3<R>{c.local[0], c.local[1], c.local[2]});
+    V3<R> C = (X(bi) + ra) - V3<R>{c.anchor[0], c.anchor[1], R(0)};
+    C.z = fmad(-M.alpha, c.c0, C.z);
+    V3<R> f = contactForce(C, c.lambda, c.penalty, groundFriction(valid ? gcShape(id) : 0));
+    const bool on = valid && f.z < 0;
+    if (!on)
+      f = V3<R>{0, 0, 0};
+    if (!valid)
+      ra = V3<R>{0, 0, 0};
+    stampAxisRow(H, 0, R(1), ra, f.x, on ? c.penalty[0] : R(0));
+    stampAxisRow(H, 1, R(1), ra, f.y, on ? c.penalty[1] : R(0));
+    stampAxisRow(H, 2, R(1), ra, f.z, on ? c.penalty[2] : R(0));
+    geometricAdd(H, ra, f);
+  }
+
+  // Rows of body-body contact `index` touching body bi (kernel.cuh:915-931).
+  __device__ void selfRows(Hess<R> &H, int bi, int index) const {
+    const SelfContact<R> &c = E.s.sc[index];
+    V3<R> ra, rb;
+    V3<R> C = selfC(c, ra, rb);
+    bool first = bi == scBody(c.id);
+    V3<R> r = first ? ra : rb;
+    R sign = first ? R(1) : R(-1);
+    V3<R> f = contactForce(C, c.lambda, c.penalty, c.friction);
+    if (f.z < 0) {
+      V3<R> basis[3] = {{c.t1[0], c.t1[1], c.t1[2]}, {c.t2[0], c.t2[1], c.t2[2]}, {c.n[0], c.n[1], c.n[2]}};
+      R fk[3] = {f.x, f.y, f.z};
+#pragma unroll
+      for (int k = 0; k < 3; ++k) {
+        V3<R> e = basis[k] * sign;
+        stampFull(H, e, fcross(r, e), fk[k], c.penalty[k]);
+      }
+      V3<R> fw = ((basis[0] * f.x) + (basis[1] * f.y)) + (basis[2] * f.z);
+      geometricAdd(H, r, fw * sign);
+    }
+  }
+
+  // The assembly of one lane's share of body bi's system, in the reference's
+  // order (inertia, hinges in adjacency order, ground contacts, body-body
+  // contacts in list order).  The i-th hinge and the n-th contact of the
+  // body go to part (i + 1) mod nParts and (n + 1) mod nParts.
+  __device__ void assembleGeneric(Hess<R> &H, int bi, bool implicitDrive, int part, int nParts) const {
+    bool slow = false;
 #pragma unroll
     for (int k = 0; k < 21; ++k)
       H.h[k] = 0;
 #pragma unroll
     for (int k = 0; k < 6; ++k)
       H.g[k] = 0;
-    const R h2 = h * h, ih2 = frcp(h2), ih = frcp(h);
-    // Inertia block (kernel.cuh:837-855).  With P >= 2 the first two lanes
-    // share it: both form theta, the log-Jacobian and rotJ; part 0 applies
-    // the world inertia to theta and rotJ[0] (the g rows and the first
-    // rotational column, plus the linear block), part 1 to rotJ[1] and
-    // rotJ[2] (the other three rotational entries).
-    if (part < 2) {
-      V3<R> theta = flogmap(fqmul(q, conj(qp)));
-      R coef = logJacobianCoef(fnorm(theta));
-      V3<R> rotJ[3];
-#pragma unroll
-      for (int k = 0; k < 3; ++k) {
-        V3<R> e = unitAxis<R>(k);
-        rotJ[k] = faxpy(coef, fcross(theta, fcross(theta, e)), faxpy(R(-0.5), fcross(theta, e), e));
-      }
-      // World inertia at q0, formed once per step by the predictor.
-      const R Iw[6] = {E.Iw[0][bi], E.Iw[1][bi], E.Iw[2][bi], E.Iw[3][bi], E.Iw[4][bi], E.Iw[5][bi]};
-      if (part == 0) {
-        V3<R> dx = x - xp;
-        R mh = fdivInv(E.s.mass[bi], h2, ih2);
-        H.h[tri(0, 0)] = mh;
-        H.h[tri(1, 1)] = mh;
-        H.h[tri(2, 2)] = mh;
-        H.g[0] = mh * dx.x;
-        H.g[1] = mh * dx.y;
-        H.g[2] = mh * dx.z;
-      }
-      if constexpr (P == 1) {
-        V3<R> It = symApply(Iw, theta);
-        V3<R> IJ[3] = {symApply(Iw, rotJ[0]), symApply(Iw, rotJ[1]), symApply(Iw, rotJ[2])};
-#pragma unroll
-        for (int k = 0; k < 3; ++k) {
-          H.g[3 + k] = fdivInv(fdot(rotJ[k], It), h2, ih2);
-#pragma unroll
-          for (int l = 0; l <= k; ++l)
-            H.h[tri(3 + k, 3 + l)] = fdivInv(fdot(rotJ[k], IJ[l]), h2, ih2);
-        }
-      } else {
-        const bool first = part == 0;
-        const V3<R> A = symApply(Iw, first ? theta : rotJ[1]);
-        const V3<R> Bv = symApply(Iw, first ? rotJ[0] : rotJ[2]);
-        const R d0 = fdivInv(fdot(rotJ[0], A), h2, ih2), d1 = fdivInv(fdot(rotJ[1], A), h2, ih2),
-                d2 = fdivInv(fdot(rotJ[2], A), h2, ih2);
-        const R e1 = fdivInv(fdot(rotJ[1], Bv), h2, ih2), e2 = fdivInv(fdot(rotJ[2], Bv), h2, ih2);
-        if (first) {
-          H.g[3] = d0;
-          H.g[4] = d1;
-          H.g[5] = d2;
-          H.h[tri(3, 3)] = fdivInv(fdot(rotJ[0], Bv), h2, ih2);
-          H.h[tri(4, 3)] = e1;
-          H.h[tri(5, 3)] = e2;
-        } else {
-          H.h[tri(4, 4)] = d1;
-          H.h[tri(5, 4)] = d2;
-          H.h[tri(5, 5)] = e2;
-        }
-      }
-    }
-    const R alpha = M.alpha;
-    // Adjacency entries pack (hinge, body a, body b); the next entry is
-    // fetched while the current hinge is assembled.
+    inertiaBlock<false>(H, bi, part, slow);
+    // The next adjacency entry is fetched while the current hinge is stamped.
     const int adjEnd = F.adjStart[bi + 1];
     int adj = F.adjStart[bi] + (part + nParts - 1) % nParts;
     int packed = adj < adjEnd ? F.adj[adj] : 0;
@@ -483,117 +655,97 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
       const int cur = packed;
       if (adj + nParts < adjEnd)
         packed = F.adj[adj + nParts];
-      const int ji = cur & 255, ja = (cur >> 8) & 255, jb = (cur >> 16) & 255;
-      const bool parent = bi == ja;
-      const R s = parent ? R(1) : R(-1);
-      JointEval je = evalJoint(ji, ja, jb);
-      // Anchor rows (k = 0..2): J_k = [s e_k, r x e_k] with r = ra (parent)
-      // or -rb (child); their geometric terms share r.  Anchor and axis
-      // rows are always active; the limit rows only on limited hinges.  The
-      // rows are straight-line code so that independent chains overlap.
-      const V3<R> r = parent ? je.ra : -je.rb;
-      R geo[3][3];
-      axisGeometricNorms(r, geo);
-      R fr[5], pr[5];
-#pragma unroll
-      for (int k = 0; k < 5; ++k) {
-        const R c = fmad(-alpha, E.c0[k][ji], je.C[k]);
-        pr[k] = E.s.penalty[k][ji];
-        fr[k] = fmad(pr[k], c, E.s.lambda[k][ji]);
-      }
-#pragma unroll
-      for (int k = 0; k < 3; ++k) {
-        stampAxisRow(H, k, s, r, fr[k], pr[k]);
-        const R af = mabs(fr[k]);
-        H.h[tri(3, 3)] = fmad(af, geo[k][0], H.h[tri(3, 3)]);
-        H.h[tri(4, 4)] = fmad(af, geo[k][1], H.h[tri(4, 4)]);
-        H.h[tri(5, 5)] = fmad(af, geo[k][2], H.h[tri(5, 5)]);
-      }
-#pragma unroll
-      for (int k = 3; k < 5; ++k) {
-        const V3<R> t = k == 3 ? je.t1 : je.t2;
-        stampAngular(H, parent ? fcross(t, je.axisB) : fcross(je.axisB, t), fr[k], pr[k]);
-        geometricAdd(H, parent ? t : je.axisB, (parent ? je.axisB : t) * fr[k]);
-      }
-      if (F.limited[ji]) {
-#pragma unroll
-        for (int k = 5; k < 7; ++k) {
-          const R c = fmad(-alpha, mn(E.c0[k][ji], R(0)), je.C[k]);
-          const R pen = E.s.penalty[k][ji];
-          const R f = mn(fmad(pen, c, E.s.lambda[k][ji]), R(0));
-          if (f < 0)
-            stampAngular(H, (k == 5) == parent ? -je.axis : je.axis, f, pen);
-        }
-      }
-      // Rows along the hinge axis (kernel.cuh:893-913): implicit torque-
-      // limited PD potential, damping/armature, dry friction -- one stamp
-      // with the summed force and stiffness, selected without branches.
-      const V3<R> J5 = parent ? -je.axis : je.axis;
-      R wTarget, delta;
-      wrapAngle2(je.angle - E.s.target[ji], je.angle - E.angle0[ji], wTarget, delta);
-      const R kp = E.s.kp[ji], maxT = E.s.maxTorque[ji];
-      R drive = fmad(kp, wTarget, -E.s.torque[ji]);
-      const bool capped = maxT > 0;
-      const R ks = capped && mabs(drive) >= maxT ? R(0) : kp;
-      drive = capped ? clampv(drive, -maxT, maxT) : drive;
-      R axisForce = implicitDrive ? drive : R(0), axisStiff = implicitDrive ? ks : R(0);
-      const R damping = E.s.damping[ji], armature = F.armature[ji];
-      const R dh = fdivInv(damping, h, ih), ah = fdivInv(armature, h2, ih2);
-      const R stiff = dh + ah;
-      const bool damped = stiff > 0;
-      axisForce += damped ? fmad(dh, delta, ah * fmad(-h, E.velocity0[ji], delta)) : R(0);
-      axisStiff += damped ? stiff : R(0);
-      const R fl = E.s.frictionloss[ji];
-      const R trial = fmad(E.s.penaltyF[ji], delta, E.s.lambdaF[ji]);
-      axisForce += fl > 0 ? clampv(trial, -fl, fl) : R(0);
-      axisStiff += fl > 0 && mabs(trial) < fl ? E.s.penaltyF[ji] : R(0);
-      stampAngular(H, J5, axisForce, axisStiff);
+      hingeRows<false>(H, bi, cur, true, implicitDrive, slow);
     }
-    // Ground contacts of this body, in list order.
     int nth = 0;
-    for (uint64_t m = E.gmask[bi]; m; m &= m - 1, ++nth) {
-      if (nParts > 1 && (nth + 1) % nParts != part)
-        continue;
-      const GroundContact<R> &c = E.s.gc[__builtin_ctzll(m)];
-      V3<R> ra;
-      V3<R> C = groundC(c, ra);
-      V3<R> f = contactForce(C, c.lambda, c.penalty, groundFriction(gcShape(c.id)));
-      // A separating contact (f.z = 0) contributes nothing: its rows are
-      // stamped with zero force and stiffness rather than branched around.
-      const bool on = f.z < 0;
-      if (!on)
-        f = V3<R>{0, 0, 0};
-      stampAxisRow(H, 0, R(1), ra, f.x, on ? c.penalty[0] : R(0));
-      stampAxisRow(H, 1, R(1), ra, f.y, on ? c.penalty[1] : R(0));
-      stampAxisRow(H, 2, R(1), ra, f.z, on ? c.penalty[2] : R(0));
-      geometricAdd(H, ra, f);
-    }
-    // Body-body contacts touching this body, in list order.
+    for (uint64_t m = E.gmask[bi]; m; m &= m - 1, ++nth)
+      if ((nth + 1) % nParts == part % nParts)
+        groundRows(H, bi, __builtin_ctzll(m), true);
     nth = 0;
-    for (uint32_t m = E.smask[bi]; m; m &= m - 1, ++nth) {
-      if (nParts > 1 && (nth + 1) % nParts != part)
-        continue;
-      const SelfContact<R> &c = E.s.sc[__builtin_ctz(m)];
-      V3<R> ra, rb;
-      V3<R> C = selfC(c, ra, rb);
-      bool first = bi == scBody(c.id);
-      V3<R> r = first ? ra : rb;
-      R sign = first ? R(1) : R(-1);
-      V3<R> f = contactForce(C, c.lambda, c.penalty, c.friction);
-      if (f.z < 0) {
-        V3<R> basis[3] = {{c.t1[0], c.t1[1], c.t1[2]},
-                          {c.t2[0], c.t2[1], c.t2[2]},
-                          {c.n[0], c.n[1], c.n[2]}};
-        R fk[3] = {f.x, f.y, f.z};
+    for (uint32_t m = E.smask[bi]; m; m &= m - 1, ++nth)
+      if ((nth + 1) % nParts == part % nParts)
+        selfRows(H, bi, __builtin_ctz(m));
+  }
+
+  // The float assembly: the inertia block, the lane's first hinge and (with
+  // Ground) its first two ground contacts as one straight-line block --
+  // independent chains the scheduler interleaves -- then any further hinges
+  // and contacts by the generic loops.  Contacts are added before further
+  // hinges (a reordering of the sums, float only).  Returns false when a
+  // lane's rotation or angle left the fast forms' range.
+  template <bool Ground>
+  __device__ bool assembleFast(Hess<R> &H, int bi, bool implicitDrive, int part, int nParts) const {
+    bool slow = false;
 #pragma unroll
-        for (int k = 0; k < 3; ++k) {
-          V3<R> e = basis[k] * sign;
-          stampFull(H, e, fcross(r, e), fk[k], c.penalty[k]);
-        }
-        V3<R> fw = ((basis[0] * f.x) + (basis[1] * f.y)) + (basis[2] * f.z);
-        geometricAdd(H, r, fw * sign);
-      }
+    for (int k = 0; k < 21; ++k)
+      H.h[k] = 0;
+#pragma unroll
+    for (int k = 0; k < 6; ++k)
+      H.g[k] = 0;
+    const int p0 = (part + nParts - 1) % nParts;
+    const int adjEnd = F.adjStart[bi + 1], adj0 = F.adjStart[bi] + p0;
+    const bool h0 = adj0 < adjEnd;
+    const int packed0 = F.adj[h0 ? adj0 : 0];
+    uint64_t m = E.gmask[bi];
+    int c0 = 0, c1 = 0;
+    bool v0 = false, v1 = false;
+    if constexpr (Ground) {
+      // positions p0 and p0 + nParts among the body's contacts
+#pragma unroll
+      for (int k = 0; k < 3; ++k)
+        m = k < p0 ? m & (m - 1) : m;
+      v0 = m != 0;
+      c0 = v0 ? __builtin_ctzll(m) : 0;
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        m = k < nParts ? m & (m - 1) : m;
+      v1 = m != 0;
+      c1 = v1 ? __builtin_ctzll(m) : 0;
     }
+    inertiaBlock<true>(H, bi, part, slow);
+    hingeRows<true>(H, bi, packed0, h0, implicitDrive, slow);
+    if constexpr (Ground) {
+      groundRows(H, bi, c0, v0);
+      groundRows(H, bi, c1, v1);
+    }
+    for (int adj = adj0 + nParts; adj < adjEnd; adj += nParts)
+      hingeRows<true>(H, bi, F.adj[adj], true, implicitDrive, slow);
+    int nth = 0;
+    for (uint64_t g = E.gmask[bi]; g; g &= g - 1, ++nth)
+      if ((!Ground || nth >= 2 * nParts) && nth % nParts == p0)
+        groundRows(H, bi, __builtin_ctzll(g), true);
+    nth = 0;
+    for (uint32_t g = E.smask[bi]; g; g &= g - 1, ++nth)
+      if (nth % nParts == p0)
+        selfRows(H, bi, __builtin_ctz(g));
+    return !slow;
+  }
+
+  // --------------------------------------------------- 6x6 block solve --
+  // kernel.cuh:828-936 for one dynamic body.  With P > 1 the P lanes of a
+  // group call this for the same body, each assembling its share; the
+  // partial systems are summed on every lane of the group (bitwise the same
+  // sum: the pairwise sums commute), all factor, part 0 writes the pose.
+  // nParts (<= 4) is the size of this body's lane group when a colour pass
+  // gives one body two slots (slots 0 and 7, lane and lane ^ 8 in each);
+  // `partner` is 1 in slot 0 and 0 in slot 7, and `quad` tells every lane of
+  // the wave that such a group exists in this pass.
+  __device__ R updateBody(int bi, bool implicitDrive, int part, int nParts = P, int partner = 0,
+                          bool quad = false) {
+    const V3<R> x = X(bi);
+    const Q4<R> q = Q(bi);
+    Hess<R> H;
+    bool done = false;
+    if constexpr (sizeof(R) == sizeof(float)) {
+      // Wave-uniform choices: with or without the straight-line contacts,
+      // and the generic assembly for every lane when any lane fell outside
+      // the fast forms.
+      const bool fast = __any(E.gmask[bi] != 0) ? assembleFast<true>(H, bi, implicitDrive, part, nParts)
+                                                 : assembleFast<false>(H, bi, implicitDrive, part, nParts);
+      done = !__any(!fast);
+    }
+    if (!done)
+      assembleGeneric(H, bi, implicitDrive, part, nParts);
     if constexpr (P >= 2) {
 #pragma unroll
       for (int k = 0; k < 21; ++k)
