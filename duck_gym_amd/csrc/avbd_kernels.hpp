@@ -521,6 +521,7 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
         R wz[kCachedPoints], wx[kCachedPoints], wy[kCachedPoints];
 #pragma unroll
         for (int k = 0; k < kCachedPoints; ++k) {
+          wz[k] = wx[k] = wy[k] = 0;
           if (k < count) {
             V3<R> world = x + rotate(q, pointOf(k));
             V3<R> vel = v + cross(w, world - x);
@@ -529,34 +530,52 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
             wy[k] = world.y;
           }
         }
+        // Pass pk takes the lowest (height, index) among the points below
+        // 3 mm that are not within 5 mm (xy) of a chosen point -- the
+        // reference's scan with ties to the lowest index.  Here a candidate
+        // is tested against the chosen points only once it is the lowest: a
+        // duplicate is dropped for good (the chosen set only grows) and the
+        // search repeats, so a pass costs pk distance tests, not 8 pk.
+        unsigned avail = 0;
+#pragma unroll
+        for (int k = 0; k < kCachedPoints; ++k)
+          avail |= (k < count && double(wz[k]) < .003) ? 1u << k : 0u;
 #pragma unroll
         for (int pk = 0; pk < 4; ++pk) {
           if (n < pk)
             break;
           int best = -1;
-          R lowest = R(INFINITY), bx = 0, by = 0;
+          R lowest = R(INFINITY);
+          for (int tries = 0; tries < kCachedPoints; ++tries) {
+            best = -1;
+            lowest = R(INFINITY);
 #pragma unroll
-          for (int k = 0; k < kCachedPoints; ++k) {
-            if (k >= count)
+            for (int k = 0; k < kCachedPoints; ++k) {
+              const bool better = ((avail >> k) & 1u) && wz[k] < lowest;
+              best = better ? k : best;
+              lowest = better ? wz[k] : lowest;
+            }
+            if (best < 0)
               break;
-            if (double(wz[k]) >= .003 || wz[k] >= lowest)
-              continue;
+            R cx = 0, cy = 0;
+#pragma unroll
+            for (int k = 0; k < kCachedPoints; ++k) {
+              cx = k == best ? wx[k] : cx;
+              cy = k == best ? wy[k] : cy;
+            }
             bool dup = false;
 #pragma unroll
-            for (int cc = 0; cc < 4; ++cc)
-              if (cc < pk && double(mhypot(chosen[cc].x - wx[k], chosen[cc].y - wy[k])) < .005)
+            for (int cc = 0; cc < 3; ++cc)
+              if (cc < pk && double(mhypot(chosen[cc].x - cx, chosen[cc].y - cy)) < .005)
                 dup = true;
-            if (dup)
-              continue;
-            best = k;
-            lowest = wz[k];
-            bx = wx[k];
-            by = wy[k];
-          }
-          if (best >= 0) {
-            picks[r][pk] = best;
-            chosen[pk] = V3<R>{bx, by, lowest};
-            n = pk + 1;
+            avail &= ~(1u << best);
+            if (!dup) {
+              picks[r][pk] = best;
+              chosen[pk] = V3<R>{cx, cy, lowest};
+              n = pk + 1;
+              break;
+            }
+            best = -1;
           }
         }
       } else {
@@ -593,19 +612,28 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
       }
       npick[r] = n;
       E.shapeCount[si] = n;
-      // Warm-start source in the previous list (still in LDS).
+      // Warm-start source in the previous list (still in LDS): the first
+      // entry with this shape and feature, by one pass over the list with
+      // four independent loads per round.
+      int src[4] = {0, 0, 0, 0};
+      const int ngc = E.s.ngc;
+      for (int i0 = 0; i0 < ngc; i0 += 4) {
+        int ids[4];
 #pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        if (p >= n)
-          continue;
-        for (int i = 0; i < E.s.ngc; ++i) {
-          int id = E.s.gc[i].id;
-          if (gcShape(id) == si && gcFeature(id) == picks[r][p]) {
-            picks[r][p] |= (i + 1) << 20;
-            break;
-          }
+        for (int j = 0; j < 4; ++j)
+          ids[j] = E.s.gc[i0 + j < ngc ? i0 + j : 0].id;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const bool mine = i0 + j < ngc && gcShape(ids[j]) == si;
+#pragma unroll
+          for (int p = 0; p < 4; ++p)
+            src[p] = (mine && src[p] == 0 && p < n && gcFeature(ids[j]) == picks[r][p]) ? i0 + j + 1 : src[p];
         }
       }
+#pragma unroll
+      for (int p = 0; p < 4; ++p)
+        if (p < n)
+          picks[r][p] |= src[p] << 20;
     }
     // ---------------- detection: body-body pairs (kernel.cuh:656-722) ----
     struct PairGeom {
