@@ -989,58 +989,23 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
       maxUpdate = groupMax<L>(maxUpdate);
       R error = 0;
       if (work) {
-        for (int ji = lane; ji < nj; ji += L) {
-          auto je = stp.evalJoint(ji);
-          // Anchor and axis rows (always active), straight-line.
-#pragma unroll
-          for (int k = 0; k < 5; ++k) {
-            const R c = fmad(-alpha, E.c0[k][ji], je.C[k]);
-            const R pen = E.s.penalty[k][ji];
-            E.s.lambda[k][ji] = fmad(pen, c, E.s.lambda[k][ji]);
-            E.s.penalty[k][ji] =
-                mn(fmad(k < 3 ? M.betaLinear : M.betaAngular, mabs(c), pen), k < 3 ? R(1e9) : R(1e7));
-            error = mx(error, mabs(c));
-          }
-          if (F.limited[ji]) {
-#pragma unroll
-            for (int k = 5; k < 7; ++k) {
-              const R c = fmad(-alpha, mn(E.c0[k][ji], R(0)), je.C[k]);
-              const R f = fmad(E.s.penalty[k][ji], c, E.s.lambda[k][ji]);
-              E.s.lambda[k][ji] = mn(f, R(0));
-              if (f < 0)
-                E.s.penalty[k][ji] = mn(fmad(M.betaAngular, mabs(c), E.s.penalty[k][ji]), R(1e7));
-              error = mx(error, mx(R(0), -c));
-            }
-          }
-          const R fl = E.s.frictionloss[ji];
-          if (fl > 0) {
-            R delta = wrapAngle(je.angle - E.angle0[ji]);
-            R trial = fmad(E.s.penaltyF[ji], delta, E.s.lambdaF[ji]);
-            E.s.lambdaF[ji] = clampv(trial, -fl, fl);
-            if (mabs(trial) < fl)
-              E.s.penaltyF[ji] = mn(fmad(M.betaAngular, mabs(delta), E.s.penaltyF[ji]), R(1e7));
-            R residual = fmad(E.s.penaltyF[ji], delta, E.s.lambdaF[ji]);
-            error = mx(error, mabs(E.s.lambdaF[ji] - clampv(residual, -fl, fl)) / E.s.penaltyF[ji]);
-          }
-        }
-        for (int i = lane; i < E.s.ngc; i += L) {
-          GroundContact<R> &c = E.s.gc[i];
-          V3<R> ra;
-          V3<R> C = stp.groundC(c, ra);
-          const R mu = stp.groundFriction(gcShape(c.id));
-          V3<R> f = contactForce(C, c.lambda, c.penalty, mu);
-          R trial = fhypot(fmad(c.penalty[0], C.x, c.lambda[0]), fmad(c.penalty[1], C.y, c.lambda[1]));
-          bool stick = trial <= -mu * f.z && double(fhypot(C.x, C.y)) < 1e-5;
-          c.id = (c.id & 0x7fffffff) | (stick ? int(0x80000000u) : 0);
-          R fk[3] = {f.x, f.y, f.z}, Ck[3] = {C.x, C.y, C.z};
-#pragma unroll
-          for (int k = 0; k < 3; ++k) {
-            c.lambda[k] = fk[k];
-            if (f.z < 0 && (k == 2 || trial <= -mu * f.z))
-              c.penalty[k] = mn(fmad(M.betaLinear, mabs(Ck[k]), c.penalty[k]), R(1e9));
-          }
-          error = mx(error, mx(R(0), -C.z));
-        }
+        // The lane's first hinge and first ground contact as one straight-
+        // line block (stores at its end), then any further ones; the error
+        // is folded in the reference's order (hinges, then contacts).
+        const int ngc = E.s.ngc;
+        R errC0 = 0;
+        const auto g0 = stp.groundDual(lane, lane < ngc, errC0);
+        const auto j0 = stp.jointDual(lane, lane < nj, error);
+        if (lane < ngc)
+          stp.storeGroundDual(lane, g0);
+        if (lane < nj)
+          stp.storeJointDual(lane, j0);
+        for (int ji = lane + L; ji < nj; ji += L)
+          stp.storeJointDual(ji, stp.jointDual(ji, true, error));
+        if (lane < ngc)
+          error = mx(error, errC0);
+        for (int i = lane + L; i < ngc; i += L)
+          stp.storeGroundDual(i, stp.groundDual(i, true, error));
         for (int i = lane; i < E.s.nsc; i += L) {
           SelfContact<R> &c = E.s.sc[i];
           V3<R> ra, rb;
