@@ -362,7 +362,7 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
     }
     V3<R> d = ((X(a) + o.ra) - X(b)) - o.rb;
     o.t2 = fcross(o.axis, o.t1);
-    o.angle = matan2(fdot(o.axis, fcross(o.t1, u)), fdot(o.t1, u));
+    o.angle = fatan2(fdot(o.axis, fcross(o.t1, u)), fdot(o.t1, u));
     o.C[0] = d.x;
     o.C[1] = d.y;
     o.C[2] = d.z;
