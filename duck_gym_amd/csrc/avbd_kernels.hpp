@@ -994,12 +994,13 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
         // is folded in the reference's order (hinges, then contacts).
         const int ngc = E.s.ngc;
         R errC0 = 0;
+        static_assert(L <= J && L <= CG, "a lane's first hinge and contact slots exist");
         const auto g0 = stp.groundDual(lane, lane < ngc, errC0);
         const auto j0 = stp.jointDual(lane, lane < nj, error);
-        if (lane < ngc)
-          stp.storeGroundDual(lane, g0);
-        if (lane < nj)
-          stp.storeJointDual(lane, j0);
+        // unconditional: a lane past the last hinge or contact rewrites its
+        // unused slot with the values it holds
+        stp.storeGroundDual(lane, g0);
+        stp.storeJointDual(lane, j0);
         for (int ji = lane + L; ji < nj; ji += L)
           stp.storeJointDual(ji, stp.jointDual(ji, true, error));
         if (lane < ngc)

@@ -396,43 +396,50 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
   // New multipliers and penalties of hinge ji (kernel.cuh:991-1028) and the
   // hinge's terms folded into the iteration's error, from loads only; the
   // caller stores them after computing its other items, so that loads and
-  // arithmetic of independent items form one block.  With valid false
-  // (ji clamped in range) the error is left as it was.
+  // arithmetic of independent items form one block.  With valid false the
+  // hinge geometry is evaluated for hinge 0 and the result is slot ji's own
+  // values unchanged (ji < J: an unused slot), so the store needs no branch;
+  // the error is left as it was.
   struct JointDual {
     R lambda[7], penalty[7], lambdaF, penaltyF;
   };
-  __device__ JointDual jointDual(int jIn, bool valid, R &error) const {
-    const int ji = valid ? jIn : 0;
+  __device__ JointDual jointDual(int ji, bool valid, R &error) const {
+    const int jg = valid ? ji : 0;
     const R alpha = M.alpha;
-    const JointEval je = evalJoint(ji);
+    const JointEval je = evalJoint(jg);
     JointDual o;
     R err = error;
 #pragma unroll
     for (int k = 0; k < 5; ++k) {
-      const R c = fmad(-alpha, E.c0[k][ji], je.C[k]);
+      const R c = fmad(-alpha, E.c0[k][jg], je.C[k]);
       const R pen = E.s.penalty[k][ji], lam = E.s.lambda[k][ji];
-      o.lambda[k] = fmad(pen, c, lam);
-      o.penalty[k] = mn(fmad(k < 3 ? M.betaLinear : M.betaAngular, mabs(c), pen), k < 3 ? R(1e9) : R(1e7));
+      o.lambda[k] = valid ? fmad(pen, c, lam) : lam;
+      const R ramped = mn(fmad(k < 3 ? M.betaLinear : M.betaAngular, mabs(c), pen), k < 3 ? R(1e9) : R(1e7));
+      o.penalty[k] = valid ? ramped : pen;
       err = mx(err, mabs(c));
     }
-    const bool limited = F.limited[ji] != 0;
+    const bool limited = valid & (F.limited[jg] != 0);
 #pragma unroll
     for (int k = 5; k < 7; ++k) {
-      const R c = fmad(-alpha, mn(E.c0[k][ji], R(0)), je.C[k]);
+      const R c = fmad(-alpha, mn(E.c0[k][jg], R(0)), je.C[k]);
       const R pen = E.s.penalty[k][ji], lam = E.s.lambda[k][ji];
       const R f = fmad(pen, c, lam);
       o.lambda[k] = limited ? mn(f, R(0)) : lam;
-      o.penalty[k] = limited && f < 0 ? mn(fmad(M.betaAngular, mabs(c), pen), R(1e7)) : pen;
+      const R ramped = mn(fmad(M.betaAngular, mabs(c), pen), R(1e7));
+      o.penalty[k] = (limited & (f < 0)) ? ramped : pen;
       err = limited ? mx(err, mx(R(0), -c)) : err;
     }
-    const R fl = E.s.frictionloss[ji], lamF = E.s.lambdaF[ji], penF = E.s.penaltyF[ji];
-    const R delta = wrapAngle(je.angle - E.angle0[ji]);
+    const R fl = E.s.frictionloss[jg], lamF = E.s.lambdaF[ji], penF = E.s.penaltyF[ji];
+    const R delta = wrapAngle(je.angle - E.angle0[jg]);
     const R trial = fmad(penF, delta, lamF);
-    const bool rough = fl > 0;
+    // every value formed, then selected: no branch splits the block
+    const bool rough = valid & (fl > 0);
+    const R ramped = mn(fmad(M.betaAngular, mabs(delta), penF), R(1e7));
     o.lambdaF = rough ? clampv(trial, -fl, fl) : lamF;
-    o.penaltyF = rough && mabs(trial) < fl ? mn(fmad(M.betaAngular, mabs(delta), penF), R(1e7)) : penF;
+    o.penaltyF = (rough & (mabs(trial) < fl)) ? ramped : penF;
     const R residual = fmad(o.penaltyF, delta, o.lambdaF);
-    err = rough ? mx(err, mabs(o.lambdaF - clampv(residual, -fl, fl)) / o.penaltyF) : err;
+    const R fErr = mx(err, mabs(o.lambdaF - clampv(residual, -fl, fl)) / o.penaltyF);
+    err = rough ? fErr : err;
     error = valid ? err : error;
     return o;
   }
@@ -446,13 +453,14 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
     E.s.penaltyF[ji] = o.penaltyF;
   }
   // New force, penalties and stick flag of ground contact i (kernel.cuh:
-  // 1029-1052), as jointDual does for a hinge.
+  // 1029-1052), as jointDual does for a hinge (with valid false: slot i's
+  // own values, i < CG, geometry from body 0).
   struct GroundDual {
     int id;
     R lambda[3], penalty[3];
   };
-  __device__ GroundDual groundDual(int iIn, bool valid, R &error) const {
-    const GroundContact<R> &c = E.s.gc[valid ? iIn : 0];
+  __device__ GroundDual groundDual(int i, bool valid, R &error) const {
+    const GroundContact<R> &c = E.s.gc[i];
     const int id = c.id;
     const int b = valid ? gcBody(id) : 0, shape = valid ? gcShape(id) : 0;
     const V3<R> ra = frotate(Q(b), V3<R>{c.local[0], c.local[1], c.local[2]});
@@ -464,13 +472,14 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
     const R trial = fhypot(fmad(pen[0], C.x, lam[0]), fmad(pen[1], C.y, lam[1]));
     const bool stick = trial <= -mu * f.z && double(fhypot(C.x, C.y)) < 1e-5;
     GroundDual o;
-    o.id = (id & 0x7fffffff) | (stick ? int(0x80000000u) : 0);
+    o.id = valid ? (id & 0x7fffffff) | (stick ? int(0x80000000u) : 0) : id;
     const R fk[3] = {f.x, f.y, f.z}, Ck[3] = {C.x, C.y, C.z};
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
-      o.lambda[k] = fk[k];
-      o.penalty[k] = f.z < 0 && (k == 2 || trial <= -mu * f.z) ? mn(fmad(M.betaLinear, mabs(Ck[k]), pen[k]), R(1e9))
-                                                              : pen[k];
+      o.lambda[k] = valid ? fk[k] : lam[k];
+      const bool ramp = valid & (f.z < 0) & ((k == 2) | (trial <= -mu * f.z));
+      const R ramped = mn(fmad(M.betaLinear, mabs(Ck[k]), pen[k]), R(1e9));
+      o.penalty[k] = ramp ? ramped : pen[k];
     }
     error = valid ? mx(error, mx(R(0), -C.z)) : error;
     return o;
