@@ -739,6 +739,7 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
             c.penalty[d] = clampv(pen[d] * gamma, R(1000), R(1e9));
           }
           E.s.gc[offset + p] = c;
+          clearContactPadding(E.s.gc[offset + p]);
         }
       }
       if (lane == 0)
@@ -785,6 +786,7 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
           c.penalty[d] = clampv(pen[d] * gamma, R(1000), R(1e9));
         }
         E.s.sc[slot] = c;
+        clearContactPadding(E.s.sc[slot]);
       }
     }
     __syncthreads();

@@ -78,6 +78,14 @@ template <class R> struct SelfContact {
   R local[3], localB[3], t1[3], t2[3], n[3], c0, friction, lambda[3], penalty[3];
 };
 
+// In the double layout the four bytes after `id` are alignment padding:
+// kept at zero in every contact written, so that a state blob holds no
+// indeterminate bytes (checkpoints compare and replay bit for bit).
+template <class C> DUCK_HD void clearContactPadding(C &c) {
+  if constexpr (offsetof(C, local) == 2 * sizeof(int))
+    reinterpret_cast<int *>(&c)[1] = 0;
+}
+
 DUCK_HD int gcShape(int id) { return id & 63; }
 DUCK_HD int gcBody(int id) { return (id >> 6) & 63; }
 DUCK_HD int gcFeature(int id) { return (id >> 12) & 0x7ffff; }

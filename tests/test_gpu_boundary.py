@@ -1,8 +1,8 @@
 """Boundary behaviour of `CudaBatch` on the GPU, after tests/cuda_boundary.py
 and tests/test_tensor_env.py of the reference: input validation errors,
 per-env NaN isolation and reset recovery, masked reset, output ownership,
-cross-stream ordering, batch-size invariance (bit-exact) and substep
-chunking (bit-exact)."""
+cross-stream ordering, batch-size invariance (bit-exact), substep
+chunking (bit-exact) and checkpoint replay (bit-exact)."""
 
 import numpy as np
 import pytest
@@ -144,6 +144,44 @@ def test_substep_chunking_bit_exact(models, home):
         b.step(targets, forces, 1, KP, 0.0)
     torch.testing.assert_close(a.state()[0], b.state()[0], rtol=0, atol=0)
     torch.testing.assert_close(a.state()[1], b.state()[1], rtol=0, atol=0)
+
+
+@pytest.mark.parametrize("fp64", [False, True])
+def test_checkpoint_replay_bit_exact(models, home, fp64):
+    """export_state() holds everything a step reads: importing a checkpoint
+    into the same batch, or into a fresh one, replays the trajectory bit for
+    bit (poses, joints, diagnostics, contact counts, the whole state blob),
+    including warm-started ground and body-body contacts."""
+    dtype = torch.float64 if fp64 else torch.float32
+    n = 64
+    rng = np.random.default_rng(9)
+    plan = [torch.tensor(home + rng.uniform(-0.3, 0.3, (n, 14)), dtype=dtype, device=DEV)
+            for _ in range(10)]
+    forces = torch.zeros(n, 3, dtype=dtype, device=DEV)
+    a = _batch(models["selfc"], n, fp64)
+    _reset_home(a, home, dtype)
+    for step in range(20):
+        a.step(plan[step // 4], forces, 1, KP, 0.0)
+    checkpoint = a.export_state().clone()
+
+    def run(batch):
+        seen = []
+        for step in range(20, 40):
+            batch.step(plan[step // 4], forces, 1, KP, 0.0)
+            seen.append([t.clone() for t in batch.state()] + [batch.contact_counts()])
+        return seen, batch.export_state()
+
+    first, final = run(a)
+    assert sum(int(c[-1][:, 0].sum()) for c in first) > 0
+    a.import_state(checkpoint)
+    again, final_again = run(a)
+    fresh = _batch(models["selfc"], n, fp64)
+    fresh.import_state(checkpoint)
+    other, final_other = run(fresh)
+    for x, y, z in zip(first, again, other):
+        for u, v, w in zip(x, y, z):
+            assert torch.equal(u, v) and torch.equal(u, w)
+    assert torch.equal(final, final_again) and torch.equal(final, final_other)
 
 
 def test_reference_method_matches_fresh_batch(models, home):
