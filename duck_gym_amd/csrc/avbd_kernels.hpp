@@ -106,29 +106,76 @@ template <class S> __device__ __forceinline__ S &blobAt(unsigned char *base, lon
   return *reinterpret_cast<S *>(base + bytes * e);
 }
 
-// Copy one environment's blob (header + live contacts) between HBM and LDS
-// with the L lanes of its group.
-// `from` skips the leading header words (the step's write-back starts at x:
-// mass, inertia and friction only change on reset).
-template <class S>
-__device__ void copyEnv(unsigned *dst, const unsigned *src, int lane, int L, int ngc, int nsc,
-                        int from = 0) {
+// Copy words [a, b) of one environment's blob between HBM and LDS (both
+// 16-byte aligned) with the L lanes of its group: the 16-byte interior in
+// dwordx4 chunks, up to `Chunks` per lane loaded before any is stored (one
+// memory round trip per Chunks * L chunks), the unaligned ends as words.
+// Exactly [a, b) is written.
+template <int Chunks>
+__device__ __forceinline__ void copyWords(unsigned *dst, const unsigned *src, int a, int b, int lane,
+                                          int L) {
+  if (a >= b)
+    return;
+  const int a4 = (a + 3) & ~3, b4 = b & ~3;
+  if (a4 >= b4) {
+    for (int i = a + lane; i < b; i += L)
+      dst[i] = src[i];
+    return;
+  }
+  if (lane < a4 - a)
+    dst[a + lane] = src[a + lane];
+  if (lane < b - b4)
+    dst[b4 + lane] = src[b4 + lane];
+  const uint4 *s4 = reinterpret_cast<const uint4 *>(src + a4);
+  uint4 *d4 = reinterpret_cast<uint4 *>(dst + a4);
+  const int n = (b4 - a4) / 4;
+  for (int c = lane; c < n; c += Chunks * L) {
+    // loads unconditional (index clamped to the last chunk) so that the
+    // chunks stay in registers
+    uint4 v[Chunks];
+#pragma unroll
+    for (int k = 0; k < Chunks; ++k)
+      v[k] = s4[c + k * L < n ? c + k * L : n - 1];
+#pragma unroll
+    for (int k = 0; k < Chunks; ++k)
+      if (c + k * L < n)
+        d4[c + k * L] = v[k];
+  }
+}
+
+// One environment's blob into LDS: the header and the first kWarmContacts
+// ground contacts in one round (most steps hold no more), then the rest of
+// the live contacts once the counts are known.
+constexpr int kWarmContacts = 8;
+template <class S> __device__ void loadEnv(S &dst, const S *src, int lane, int L) {
   constexpr int header = int(headerBytes<S>() / 4);
   constexpr int CGcap = int(sizeof(S::gc) / sizeof(S::gc[0]));
   constexpr int CScap = int(sizeof(S::sc) / sizeof(S::sc[0]));
+  constexpr int gcWords = int(sizeof(decltype(S::gc[0])) / 4);
+  constexpr int scStart = int(offsetof(S, sc) / 4), scWords = int(sizeof(decltype(S::sc[0])) / 4);
+  constexpr int warm = header + (kWarmContacts < CGcap ? kWarmContacts : CGcap) * gcWords;
+  int ngc = src->ngc, nsc = src->nsc;
+  unsigned *d = reinterpret_cast<unsigned *>(&dst);
+  const unsigned *s = reinterpret_cast<const unsigned *>(src);
+  copyWords<16>(d, s, 0, warm, lane, L);
   ngc = ngc < 0 ? 0 : (ngc > CGcap ? CGcap : ngc);
   nsc = nsc < 0 ? 0 : (nsc > CScap ? CScap : nsc);
-  for (int i = from + lane; i < header; i += L)
-    dst[i] = src[i];
+  copyWords<4>(d, s, warm, header + ngc * gcWords, lane, L);
+  copyWords<4>(d, s, scStart, scStart + nsc * scWords, lane, L);
+}
+
+// LDS -> HBM after a step: the header from `from` (the step's write-back
+// starts at x: mass, inertia and friction only change on reset) and exactly
+// the live contacts.
+template <class S> __device__ void storeEnv(S *dst, const S &src, int lane, int L, int from) {
+  constexpr int header = int(headerBytes<S>() / 4);
   constexpr int gcWords = int(sizeof(decltype(S::gc[0])) / 4);
-  const int gcStart = header, gcEnd = header + ngc * gcWords;
-  for (int i = gcStart + lane; i < gcEnd; i += L)
-    dst[i] = src[i];
-  constexpr int scStart = int(offsetof(S, sc) / 4);
-  constexpr int scWords = int(sizeof(decltype(S::sc[0])) / 4);
-  const int scEnd = scStart + nsc * scWords;
-  for (int i = scStart + lane; i < scEnd; i += L)
-    dst[i] = src[i];
+  constexpr int scStart = int(offsetof(S, sc) / 4), scWords = int(sizeof(decltype(S::sc[0])) / 4);
+  unsigned *d = reinterpret_cast<unsigned *>(dst);
+  const unsigned *s = reinterpret_cast<const unsigned *>(&src);
+  copyWords<16>(d, s, from, header, lane, L);
+  copyWords<4>(d, s, header, header + src.ngc * gcWords, lane, L);
+  copyWords<4>(d, s, scStart, scStart + src.nsc * scWords, lane, L);
 }
 
 // MPR narrow phase between two shapes (convex.cuh:124-217), one lane.
@@ -377,24 +424,18 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
   for (int i = t; i <= nb; i += 64)
     F.adjStart[i] = M.adjStart[i];
   for (int i = t; i < 2 * nj; i += 64)
-    F.adj[i] = M.adj[i] | (M.ja[M.adj[i]] << 8) | (M.jb[M.adj[i]] << 16);
+    F.adj[i] = M.adjPacked[i];
   for (int i = t; i < ns; i += 64)
     F.shapeFriction[i] = M.sfriction[i];
-  if (t == 0) {
-    int pos = 0;
-    F.colorStart[0] = 0;
-    for (int c = 0; c < 2; ++c) {
-      for (int b = 0; b < nb; ++b)
-        if (M.mass[b] > 0 && M.colors[b] == c)
-          F.order[pos++] = b;
-      F.colorStart[c + 1] = pos;
-    }
-  }
+  for (int i = t; i < nb; i += 64)
+    F.order[i] = M.order[i];
+  if (t < 3)
+    F.colorStart[t] = M.colorStart[t];
 
   State *gs = valid ? &blobAt<State>(args.states, args.blobBytes, e) : nullptr;
+  static_assert(L >= 4, "blob copies give each of the first three lanes an end word");
   if (valid)
-    copyEnv<State>(reinterpret_cast<unsigned *>(&E.s), reinterpret_cast<const unsigned *>(gs), lane,
-                   L, gs->ngc, gs->nsc);
+    loadEnv<State>(E.s, gs, lane, L);
   __syncthreads();
   // The staged default schedule applies to this env while no body-body
   // contact recolours it and its dynamic bodies are the model's.
@@ -1101,10 +1142,8 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
       constexpr int scStart = int(offsetof(State, sc) / 4), scWords = int(sizeof(SelfContact<R>) / 4);
       const unsigned *s = reinterpret_cast<const unsigned *>(&E.s);
       unsigned *d = reinterpret_cast<unsigned *>(gs);
-      for (int i = header + lane; i < header + E.s.ngc * gcWords; i += L)
-        d[i] = s[i];
-      for (int i = scStart + lane; i < scStart + E.s.nsc * scWords; i += L)
-        d[i] = s[i];
+      copyWords<4>(d, s, header, header + E.s.ngc * gcWords, lane, L);
+      copyWords<4>(d, s, scStart, scStart + E.s.nsc * scWords, lane, L);
       if (lane == 0) {
         gs->ngc = E.s.ngc;
         gs->nsc = E.s.nsc;
@@ -1113,8 +1152,7 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
     __syncthreads();
   }
   if (valid)
-    copyEnv<State>(reinterpret_cast<unsigned *>(gs), reinterpret_cast<const unsigned *>(&E.s), lane,
-                   L, E.s.ngc, E.s.nsc, int(offsetof(State, x) / 4));
+    storeEnv<State>(gs, E.s, lane, L, int(offsetof(State, x) / 4));
 }
 
 } // namespace duckhip

@@ -39,6 +39,9 @@ template <class R> struct DeviceModel {
       axisB[3][kMaxModelJoints], tangentA[3][kMaxModelJoints], tangentB[3][kMaxModelJoints];
   R lo[kMaxModelJoints], hi[kMaxModelJoints], armature[kMaxModelJoints];
   int adjStart[kMaxModelBodies + 1], adj[2 * kMaxModelJoints];
+  // adjacency entries packed as hinge | body a << 8 | body b << 16, and the
+  // default colour schedule (dynamic bodies of colour 0 then 1, index order)
+  int adjPacked[2 * kMaxModelJoints], order[kMaxModelBodies], colorStart[3];
   R damping[kMaxModelJoints], frictionloss[kMaxModelJoints], torque[kMaxModelJoints],
       kp[kMaxModelJoints], target[kMaxModelJoints], maxTorque[kMaxModelJoints],
       originalAngle[kMaxModelJoints];
@@ -123,7 +126,7 @@ template <class R, int B, int J, int CG, int CS> struct EnvState {
   SelfContact<R> sc[CS];
 };
 
-template <class R, int B, int J, int CG, int CS> struct EnvLds {
+template <class R, int B, int J, int CG, int CS> struct alignas(16) EnvLds {
   EnvState<R, B, J, CG, CS> s;
   // per-step scratch
   R x0[3][B], q0[4][B], xp[3][B], qp[4][B];

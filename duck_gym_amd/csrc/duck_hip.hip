@@ -113,8 +113,20 @@ template <class R> DeviceModel<R> pack(const HostModel &h, double dt, int iterat
   }
   for (size_t i = 0; i < h.adjacencyStart.size(); ++i)
     m.adjStart[i] = h.adjacencyStart[i];
-  for (size_t i = 0; i < h.adjacency.size(); ++i)
+  for (size_t i = 0; i < h.adjacency.size(); ++i) {
     m.adj[i] = h.adjacency[i];
+    m.adjPacked[i] = m.adj[i] | (m.ja[m.adj[i]] << 8) | (m.jb[m.adj[i]] << 16);
+  }
+  // Default colour schedule: dynamic bodies of colour 0, then of colour 1,
+  // each in index order.
+  int pos = 0;
+  m.colorStart[0] = 0;
+  for (int c = 0; c < 2; ++c) {
+    for (int b = 0; b < m.nb; ++b)
+      if (m.mass[b] > 0 && m.colors[b] == c)
+        m.order[pos++] = b;
+    m.colorStart[c + 1] = pos;
+  }
   for (int s = 0; s < m.ns; ++s) {
     const auto &sh = h.shapes[s];
     m.sbody[s] = sh.body;
