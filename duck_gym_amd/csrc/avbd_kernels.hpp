@@ -532,6 +532,11 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
     // Per pick: point index | (warm-start source + 1) << 20, so that only
     // four registers per shape live across the barrier into compaction.
     int picks[SPL][4], npick[SPL];
+    struct WarmGround {
+      R lambda[3], penalty[3], local[3], anchor[2];
+      bool stick;
+    };
+    WarmGround warm[SPL][4];
 #pragma unroll
     for (int r = 0; r < SPL; ++r) {
       npick[r] = 0;
@@ -553,7 +558,6 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
         continue;
       }
       const int count = M.scount[si];
-      auto pointOf = [&](int k) { return groundPoint(M, points, si, k, q); };
       V3<R> chosen[4];
       int n = 0;
       if (count <= kCachedPoints) {
@@ -564,7 +568,8 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
         for (int k = 0; k < kCachedPoints; ++k) {
           wz[k] = wx[k] = wy[k] = 0;
           if (k < count) {
-            V3<R> world = x + rotate(q, pointOf(k));
+            const V3<R> local = groundPoint(M, points, si, k, q);
+            V3<R> world = x + rotate(q, local);
             V3<R> vel = v + cross(w, world - x);
             wz[k] = mn(world.z, world.z + h * vel.z + h * h * gz);
             wx[k] = world.x;
@@ -628,7 +633,7 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
           R lowest = R(INFINITY);
           V3<R> bestWorld{0, 0, 0};
           for (int k = 0; k < count; ++k) {
-            V3<R> local = pointOf(k), world = x + rotate(q, local);
+            V3<R> local = groundPoint(M, points, si, k, q), world = x + rotate(q, local);
             V3<R> vel = v + cross(w, world - x);
             R z = mn(world.z, world.z + h * vel.z + h * h * gz);
             if (double(z) >= .003 || z >= lowest)
@@ -672,14 +677,28 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
         }
       }
 #pragma unroll
-      for (int p = 0; p < 4; ++p)
+      for (int p = 0; p < 4; ++p) {
         if (p < n)
           picks[r][p] |= src[p] << 20;
+        // the source's multipliers, penalties and stick anchor, read while
+        // the previous list is still in LDS (compaction overwrites it)
+        const GroundContact<R> &old = E.s.gc[p < n && src[p] > 0 ? src[p] - 1 : 0];
+        WarmGround &wm = warm[r][p];
+#pragma unroll
+        for (int d = 0; d < 3; ++d) {
+          wm.lambda[d] = old.lambda[d];
+          wm.penalty[d] = old.penalty[d];
+          wm.local[d] = old.local[d];
+        }
+        wm.anchor[0] = old.anchor[0];
+        wm.anchor[1] = old.anchor[1];
+        wm.stick = gcStick(old.id);
+      }
     }
     // ---------------- detection: body-body pairs (kernel.cuh:656-722) ----
     struct PairGeom {
       V3<R> n, t1, t2, local, localB;
-      R c0;
+      R c0, lambda[3], penalty[3];
       int src;
     };
     PairGeom pg[PPL];
@@ -726,6 +745,19 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
           break;
         }
       }
+      if (o.src >= 0) {
+        // the source's force in the new basis, read while the previous list
+        // is still in LDS
+        const SelfContact<R> &old = E.s.sc[o.src];
+        V3<R> f = ((V3<R>{old.t1[0], old.t1[1], old.t1[2]} * old.lambda[0]) +
+                   (V3<R>{old.t2[0], old.t2[1], old.t2[2]} * old.lambda[1])) +
+                  (V3<R>{old.n[0], old.n[1], old.n[2]} * old.lambda[2]);
+        o.lambda[0] = dot(f, o.t1);
+        o.lambda[1] = dot(f, o.t2);
+        o.lambda[2] = dot(f, o.n);
+        for (int d = 0; d < 3; ++d)
+          o.penalty[d] = old.penalty[d];
+      }
       E.pairHit[pi] = 1;
     }
     __syncthreads();
@@ -753,16 +785,17 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
             break;
           GroundContact<R> c;
           const int feature = picks[r][p] & 0xFFFFF, src = (picks[r][p] >> 20) - 1;
-          V3<R> local = groundPoint(M, points, si, feature, q), world = x + rotate(q, local);
+          V3<R> local = groundPoint(M, points, si, feature, q);
+          const V3<R> world = x + rotate(q, local);
           R lam[3] = {0, 0, 0}, pen[3] = {1000, 1000, 1000};
           R anchor[2] = {world.x, world.y};
           if (src >= 0) {
-            const GroundContact<R> &old = gs->gc[src];
+            const WarmGround &old = warm[r][p];
             for (int d = 0; d < 3; ++d) {
               lam[d] = old.lambda[d];
               pen[d] = old.penalty[d];
             }
-            if (gcStick(old.id)) {
+            if (old.stick) {
               local = {old.local[0], old.local[1], old.local[2]};
               anchor[0] = old.anchor[0];
               anchor[1] = old.anchor[1];
@@ -803,15 +836,10 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
         c.id = scPack(M.sbody[sa], M.sbody[sb], sa, sb, false);
         R lam[3] = {0, 0, 0}, pen[3] = {1000, 1000, 1000};
         if (o.src >= 0) {
-          const SelfContact<R> &old = gs->sc[o.src];
-          V3<R> f = ((V3<R>{old.t1[0], old.t1[1], old.t1[2]} * old.lambda[0]) +
-                     (V3<R>{old.t2[0], old.t2[1], old.t2[2]} * old.lambda[1])) +
-                    (V3<R>{old.n[0], old.n[1], old.n[2]} * old.lambda[2]);
-          lam[0] = dot(f, o.t1);
-          lam[1] = dot(f, o.t2);
-          lam[2] = dot(f, o.n);
-          for (int d = 0; d < 3; ++d)
-            pen[d] = old.penalty[d];
+          for (int d = 0; d < 3; ++d) {
+            lam[d] = o.lambda[d];
+            pen[d] = o.penalty[d];
+          }
         }
         V3<R> vs[5] = {o.local, o.localB, o.t1, o.t2, o.n};
         R *dst[5] = {c.local, c.localB, c.t1, c.t2, c.n};
@@ -1135,20 +1163,6 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
       d[kIterations] += E.stepDiag[kIterations];
     }
     __syncthreads();
-    // The next substep warm-starts from the HBM copy of this contact list.
-    if (active && sub + 1 < args.substeps) {
-      constexpr int header = int(headerBytes<State>() / 4);
-      constexpr int gcWords = int(sizeof(GroundContact<R>) / 4);
-      constexpr int scStart = int(offsetof(State, sc) / 4), scWords = int(sizeof(SelfContact<R>) / 4);
-      const unsigned *s = reinterpret_cast<const unsigned *>(&E.s);
-      unsigned *d = reinterpret_cast<unsigned *>(gs);
-      copyWords<4>(d, s, header, header + E.s.ngc * gcWords, lane, L);
-      copyWords<4>(d, s, scStart, scStart + E.s.nsc * scWords, lane, L);
-      if (lane == 0) {
-        gs->ngc = E.s.ngc;
-        gs->nsc = E.s.nsc;
-      }
-    }
     __syncthreads();
   }
   if (valid)
