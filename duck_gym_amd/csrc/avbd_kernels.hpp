@@ -403,6 +403,33 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
   Env &E = envs[g];
   const int nb = M.nb, nj = M.nj, ns = M.ns, np = M.np;
 
+  // Controls and the model's per-joint defaults, loaded first so that their
+  // latency overlaps the model staging and the blob copy.
+  constexpr int JPL = (J + L - 1) / L;
+  R ctl[JPL][3], defs[JPL][3], fin = 0;
+#pragma unroll
+  for (int r = 0; r < JPL; ++r) {
+    const int j = lane + r * L;
+    const bool in = valid && j < nj;
+    const int jc = j < nj ? j : 0;
+    ctl[r][0] = ctl[r][1] = ctl[r][2] = 0;
+    if (in) {
+      if (args.motorMode) {
+        const R *motor = static_cast<const R *>(args.motor) + size_t(e) * nj * 3;
+        ctl[r][0] = motor[3 * j];
+        ctl[r][1] = motor[3 * j + 1];
+        ctl[r][2] = motor[3 * j + 2];
+      } else {
+        ctl[r][0] = static_cast<const R *>(args.targets)[size_t(e) * nj + j];
+      }
+    }
+    defs[r][0] = M.torque[jc];
+    defs[r][1] = M.frictionloss[jc];
+    defs[r][2] = M.damping[jc];
+  }
+  if (valid && lane < 3)
+    fin = static_cast<const R *>(args.forces)[size_t(e) * 3 + lane];
+
   // Stage the joint model (all 64 lanes).
   for (int j = t; j < nj; j += 64) {
     F.a[j] = M.ja[j];
@@ -448,55 +475,58 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
   // ---- controls (extension.cu:87-110 / kernel.cuh:448-466) ----
   int bad = 0;
   if (valid) {
-    if (args.motorMode) {
-      const R *motor = static_cast<const R *>(args.motor) + size_t(e) * nj * 3;
-      for (int j = lane; j < nj; j += L) {
-        R m0 = motor[3 * j], m1 = motor[3 * j + 1], m2 = motor[3 * j + 2];
-        if (!mfinite(m0) || !mfinite(m1) || !mfinite(m2) || m1 < 0 || m2 < 0)
+#pragma unroll
+    for (int r = 0; r < JPL; ++r) {
+      if (lane + r * L >= nj)
+        continue;
+      if (args.motorMode) {
+        if (!mfinite(ctl[r][0]) || !mfinite(ctl[r][1]) || !mfinite(ctl[r][2]) || ctl[r][1] < 0 ||
+            ctl[r][2] < 0)
           bad = 1;
+      } else if (!mfinite(ctl[r][0])) {
+        bad = 1;
       }
-    } else {
-      const R *target = static_cast<const R *>(args.targets) + size_t(e) * nj;
-      for (int j = lane; j < nj; j += L)
-        if (!mfinite(target[j]))
-          bad = 1;
     }
-    const R *force = static_cast<const R *>(args.forces) + size_t(e) * 3;
-    if (lane < 3 && !mfinite(force[lane]))
+    if (lane < 3 && !mfinite(fin))
       bad = 1;
   }
   bad = groupOr<L>(bad);
   __syncthreads();
   bool active = false;
   if (valid) {
-    const R *force = static_cast<const R *>(args.forces) + size_t(e) * 3;
     if (args.motorMode) {
       // setMotor applies the channels even when they are invalid.
-      const R *motor = static_cast<const R *>(args.motor) + size_t(e) * nj * 3;
-      for (int j = lane; j < nj; j += L) {
+#pragma unroll
+      for (int r = 0; r < JPL; ++r) {
+        const int j = lane + r * L;
+        if (j >= nj)
+          continue;
         E.s.kp[j] = 0;
         E.s.maxTorque[j] = 0;
-        E.s.torque[j] = motor[3 * j];
-        E.s.frictionloss[j] = motor[3 * j + 1];
-        E.s.damping[j] = motor[3 * j + 2];
+        E.s.torque[j] = ctl[r][0];
+        E.s.frictionloss[j] = ctl[r][1];
+        E.s.damping[j] = ctl[r][2];
       }
       if (lane < 3)
-        E.s.force[lane] = force[lane];
+        E.s.force[lane] = fin;
       if (bad && lane == 0)
         E.s.failed = 1;
       active = !E.s.failed && !bad;
     } else if (!E.s.failed && !bad) {
-      const R *target = static_cast<const R *>(args.targets) + size_t(e) * nj;
-      for (int j = lane; j < nj; j += L) {
-        E.s.target[j] = target[j];
+#pragma unroll
+      for (int r = 0; r < JPL; ++r) {
+        const int j = lane + r * L;
+        if (j >= nj)
+          continue;
+        E.s.target[j] = ctl[r][0];
         E.s.kp[j] = R(args.kp);
         E.s.maxTorque[j] = R(args.limit);
-        E.s.torque[j] = M.torque[j];
-        E.s.frictionloss[j] = M.frictionloss[j];
-        E.s.damping[j] = M.damping[j];
+        E.s.torque[j] = defs[r][0];
+        E.s.frictionloss[j] = defs[r][1];
+        E.s.damping[j] = defs[r][2];
       }
       if (lane < 3)
-        E.s.force[lane] = force[lane];
+        E.s.force[lane] = fin;
       active = true;
     } else {
       if (lane == 0)
