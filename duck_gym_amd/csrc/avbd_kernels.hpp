@@ -98,9 +98,6 @@ __device__ __forceinline__ V3<R> groundPoint(const DeviceModel<R> &M, const V3<R
   return (c + rotate(sq, V3<R>{0, 0, (k ? R(1) : R(-1)) * M.size[1][si]})) + down;
 }
 
-// Shapes with at most this many points keep their candidate heights in
-// registers during ground-contact selection.
-constexpr int kCachedPoints = 8;
 
 template <class S> __device__ __forceinline__ S &blobAt(unsigned char *base, long long bytes, int e) {
   return *reinterpret_cast<S *>(base + bytes * e);
@@ -454,8 +451,20 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
     F.adj[i] = M.adjPacked[i];
   for (int i = t; i < ns; i += 64)
     F.shapeFriction[i] = M.sfriction[i];
-  for (int i = t; i < nb; i += 64)
+  for (int i = t; i < nb; i += 64) {
     F.order[i] = M.order[i];
+    F.mass[i] = M.mass[i];
+  }
+  for (int i = t; i < ns; i += 64) {
+    F.sbody[i] = M.sbody[i];
+    F.sflags[i] = M.sflags[i];
+    F.scount[i] = M.scount[i];
+    F.sradius[i] = M.radius[i];
+  }
+  for (int i = t; i < kCachedPoints * 3 * ns; i += 64) {
+    const int si = i % ns, c = (i / ns) % 3, k = i / (3 * ns);
+    F.spt[k][c][si] = M.spts[k][c][si];
+  }
   if (t < 3)
     F.colorStart[t] = M.colorStart[t];
 
@@ -469,7 +478,7 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
   int massPattern = 0;
   if (valid)
     for (int b = lane; b < nb; b += L)
-      massPattern |= (E.s.mass[b] > 0) != (M.mass[b] > 0);
+      massPattern |= (E.s.mass[b] > 0) != (F.mass[b] > 0);
   const bool defaultSchedule = groupOr<L>(massPattern) == 0;
 
   // ---- controls (extension.cu:87-110 / kernel.cuh:448-466) ----
@@ -573,9 +582,9 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
       const int si = lane + r * L;
       if (!active || si >= ns)
         continue;
-      const int b = M.sbody[si];
+      const int b = F.sbody[si], flags = F.sflags[si];
       const R mass = E.s.mass[b];
-      if (!M.ground || !M.sground[si] || mass == 0) {
+      if (!(flags & 1) || mass == 0) {
         E.shapeCount[si] = 0;
         continue;
       }
@@ -583,11 +592,12 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
       Q4<R> q = stp.Q(b);
       const R gz = M.gravity[2] + stp.forceZ(b) / mass;
       R low = mn(x.z, x.z + h * v.z + h * h * gz);
-      if (double(low - M.radius[si] * (R(1) + h * norm(w))) >= .003) {
+      if (double(low - F.sradius[si] * (R(1) + h * norm(w))) >= .003) {
         E.shapeCount[si] = 0;
         continue;
       }
-      const int count = M.scount[si];
+      const int count = F.scount[si];
+      const bool staged = (flags & 2) != 0;
       V3<R> chosen[4];
       int n = 0;
       if (count <= kCachedPoints) {
@@ -598,7 +608,8 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
         for (int k = 0; k < kCachedPoints; ++k) {
           wz[k] = wx[k] = wy[k] = 0;
           if (k < count) {
-            const V3<R> local = groundPoint(M, points, si, k, q);
+            const V3<R> local = staged ? V3<R>{F.spt[k][0][si], F.spt[k][1][si], F.spt[k][2][si]}
+                                       : groundPoint(M, points, si, k, q);
             V3<R> world = x + rotate(q, local);
             V3<R> vel = v + cross(w, world - x);
             wz[k] = mn(world.z, world.z + h * vel.z + h * h * gz);
@@ -806,7 +817,7 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
         int offset = 0;
         for (int k = 0; k < si; ++k)
           offset += E.shapeCount[k];
-        const int b = M.sbody[si];
+        const int b = F.sbody[si];
         V3<R> x = stp.X(b);
         Q4<R> q = stp.Q(b);
 #pragma unroll
@@ -815,7 +826,9 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
             break;
           GroundContact<R> c;
           const int feature = picks[r][p] & 0xFFFFF, src = (picks[r][p] >> 20) - 1;
-          V3<R> local = groundPoint(M, points, si, feature, q);
+          V3<R> local = (F.sflags[si] & 2) ? V3<R>{F.spt[feature][0][si], F.spt[feature][1][si],
+                                                   F.spt[feature][2][si]}
+                                          : groundPoint(M, points, si, feature, q);
           const V3<R> world = x + rotate(q, local);
           R lam[3] = {0, 0, 0}, pen[3] = {1000, 1000, 1000};
           R anchor[2] = {world.x, world.y};

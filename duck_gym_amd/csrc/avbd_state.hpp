@@ -23,6 +23,9 @@ namespace duckhip {
 
 constexpr int kMaxModelBodies = 32, kMaxModelJoints = 32, kMaxModelShapes = 32,
               kMaxModelPairs = 32;
+// Point-set shapes with at most this many points are staged in LDS and keep
+// their candidate heights in registers during ground-contact selection.
+constexpr int kCachedPoints = 8;
 
 // Read-only model in global memory (one copy per batch).
 template <class R> struct DeviceModel {
@@ -50,6 +53,10 @@ template <class R> struct DeviceModel {
       soffset[kMaxModelShapes], scount[kMaxModelShapes];
   R center[3][kMaxModelShapes], size[3][kMaxModelShapes], sq[4][kMaxModelShapes],
       sfriction[kMaxModelShapes], radius[kMaxModelShapes], interior[3][kMaxModelShapes];
+  // ground detection: bit 0 ground contact enabled (model and shape), bit 1
+  // point set of at most kCachedPoints points, whose points are spts
+  int sflags[kMaxModelShapes];
+  R spts[kCachedPoints][3][kMaxModelShapes];
   // body-contact pairs (shape indices)
   int pa[kMaxModelPairs], pb[kMaxModelPairs];
   R pfriction[kMaxModelPairs];
@@ -66,6 +73,10 @@ template <class R, int B, int J> struct Frames {
   // Colour schedule without body-body contacts (model colours, bodies of
   // non-zero model mass in index order within each colour).
   int order[B], colorStart[3];
+  // Ground-detection data per shape (shapes <= B) and model masses.
+  int sbody[B], sflags[B], scount[B];
+  R sradius[B], mass[B];
+  R spt[kCachedPoints][3][B];
 };
 
 // Ground contact (normal = +z, anchor on the plane).  id packs

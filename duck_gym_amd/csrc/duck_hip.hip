@@ -143,6 +143,11 @@ template <class R> DeviceModel<R> pack(const HostModel &h, double dt, int iterat
       m.sq[k][s] = R(sh.q[k]);
     m.sfriction[s] = R(sh.friction);
     m.radius[s] = R(sh.radius);
+    const bool pointSet = (sh.type == 1 || sh.type == 3) && sh.count >= 1 && sh.count <= kCachedPoints;
+    m.sflags[s] = (h.ground && sh.ground ? 1 : 0) | (pointSet ? 2 : 0);
+    for (int k = 0; k < kCachedPoints; ++k)
+      for (int c = 0; c < 3; ++c)
+        m.spts[k][c][s] = pointSet && k < sh.count ? R(h.points[3 * (sh.offset + k) + c]) : R(0);
   }
   for (int p = 0; p < m.np; ++p) {
     m.pa[p] = h.pairs[p].a;
