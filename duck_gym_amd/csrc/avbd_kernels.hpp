@@ -1109,14 +1109,20 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
         const int ngc = E.s.ngc;
         R errC0 = 0;
         static_assert(L <= J && L <= CG, "a lane's first hinge and contact slots exist");
+        auto j0 = stp.jointDual(lane, lane < nj, error);
         const auto g0 = stp.groundDual(lane, lane < ngc, errC0);
-        const auto j0 = stp.jointDual(lane, lane < nj, error);
+        if (__any(j0.wide) && j0.wide)
+          error = stp.frictionDual(j0, wrapAngle(j0.angle));
         // unconditional: a lane past the last hinge or contact rewrites its
         // unused slot with the values it holds
         stp.storeGroundDual(lane, g0);
         stp.storeJointDual(lane, j0);
-        for (int ji = lane + L; ji < nj; ji += L)
-          stp.storeJointDual(ji, stp.jointDual(ji, true, error));
+        for (int ji = lane + L; ji < nj; ji += L) {
+          auto jd = stp.jointDual(ji, true, error);
+          if (jd.wide)
+            error = stp.frictionDual(jd, wrapAngle(jd.angle));
+          stp.storeJointDual(ji, jd);
+        }
         if (lane < ngc)
           error = mx(error, errC0);
         for (int i = lane + L; i < ngc; i += L)

@@ -402,7 +402,24 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
   // the error is left as it was.
   struct JointDual {
     R lambda[7], penalty[7], lambdaF, penaltyF;
+    // inputs of the dry-friction part, kept for frictionDual
+    R errRows, angle, fl, lambdaF0, penaltyF0;
+    bool rough, wide;
   };
+  // Dry-friction multiplier and penalty of a hinge for the wrapped angle
+  // change `delta`; returns the error after the hinge's terms.
+  __device__ R frictionDual(JointDual &o, R delta) const {
+    const R trial = fmad(o.penaltyF0, delta, o.lambdaF0);
+    const R ramped = mn(fmad(M.betaAngular, mabs(delta), o.penaltyF0), R(1e7));
+    o.lambdaF = o.rough ? clampv(trial, -o.fl, o.fl) : o.lambdaF0;
+    o.penaltyF = (o.rough & (mabs(trial) < o.fl)) ? ramped : o.penaltyF0;
+    const R residual = fmad(o.penaltyF, delta, o.lambdaF);
+    const R fErr = mx(o.errRows, mabs(o.lambdaF - clampv(residual, -o.fl, o.fl)) / o.penaltyF);
+    return o.rough ? fErr : o.errRows;
+  }
+  // The angle change is wrapped by wrapAngle's |a| < 3.14159 form (a + 0);
+  // `wide` marks a lane outside it, which the caller completes with
+  // frictionDual(o, wrapAngle(o.angle)) -- a branch kept out of this block.
   __device__ JointDual jointDual(int ji, bool valid, R &error) const {
     const int jg = valid ? ji : 0;
     const R alpha = M.alpha;
@@ -429,17 +446,14 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
       o.penalty[k] = (limited & (f < 0)) ? ramped : pen;
       err = limited ? mx(err, mx(R(0), -c)) : err;
     }
-    const R fl = E.s.frictionloss[jg], lamF = E.s.lambdaF[ji], penF = E.s.penaltyF[ji];
-    const R delta = wrapAngle(je.angle - E.angle0[jg]);
-    const R trial = fmad(penF, delta, lamF);
-    // every value formed, then selected: no branch splits the block
-    const bool rough = valid & (fl > 0);
-    const R ramped = mn(fmad(M.betaAngular, mabs(delta), penF), R(1e7));
-    o.lambdaF = rough ? clampv(trial, -fl, fl) : lamF;
-    o.penaltyF = (rough & (mabs(trial) < fl)) ? ramped : penF;
-    const R residual = fmad(o.penaltyF, delta, o.lambdaF);
-    const R fErr = mx(err, mabs(o.lambdaF - clampv(residual, -fl, fl)) / o.penaltyF);
-    err = rough ? fErr : err;
+    o.errRows = err;
+    o.angle = je.angle - E.angle0[jg];
+    o.fl = E.s.frictionloss[jg];
+    o.lambdaF0 = E.s.lambdaF[ji];
+    o.penaltyF0 = E.s.penaltyF[ji];
+    o.rough = valid & (o.fl > 0);
+    o.wide = valid & !(mabs(o.angle) < R(3.14159));
+    err = frictionDual(o, o.angle + R(0));
     error = valid ? err : error;
     return o;
   }
@@ -470,9 +484,12 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
     const R lam[3] = {c.lambda[0], c.lambda[1], c.lambda[2]}, pen[3] = {c.penalty[0], c.penalty[1], c.penalty[2]};
     const V3<R> f = contactForce(C, lam, pen, mu);
     const R trial = fhypot(fmad(pen[0], C.x, lam[0]), fmad(pen[1], C.y, lam[1]));
-    const bool stick = trial <= -mu * f.z && double(fhypot(C.x, C.y)) < 1e-5;
+    const R slip = fhypot(C.x, C.y);
+    const bool stick = trial <= -mu * f.z && double(slip) < 1e-5;
     GroundDual o;
-    o.id = valid ? (id & 0x7fffffff) | (stick ? int(0x80000000u) : 0) : id;
+    const int idNew = (id & 0x7fffffff) | (stick ? int(0x80000000u) : 0);
+    const R errNew = mx(error, mx(R(0), -C.z));
+    o.id = valid ? idNew : id;
     const R fk[3] = {f.x, f.y, f.z}, Ck[3] = {C.x, C.y, C.z};
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
@@ -481,7 +498,7 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
       const R ramped = mn(fmad(M.betaLinear, mabs(Ck[k]), pen[k]), R(1e9));
       o.penalty[k] = ramp ? ramped : pen[k];
     }
-    error = valid ? mx(error, mx(R(0), -C.z)) : error;
+    error = valid ? errNew : error;
     return o;
   }
   __device__ void storeGroundDual(int i, const GroundDual &o) {
