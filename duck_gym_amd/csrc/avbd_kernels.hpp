@@ -398,7 +398,7 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
   const int e = blockIdx.x * G + g;
   const bool valid = e < args.count;
   Env &E = envs[g];
-  const int nb = M.nb, nj = M.nj, ns = M.ns, np = M.np;
+  const int nb = args.nb, nj = args.nj, ns = args.ns, np = args.np;
 
   // Controls and the model's per-joint defaults, loaded first so that their
   // latency overlaps the model staging and the blob copy.

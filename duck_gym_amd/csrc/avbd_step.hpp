@@ -30,6 +30,8 @@ struct StepArgs {
   int substeps;
   int motorMode;
   double kp, limit;
+  int nb, nj, ns, np; // model counts (also in the model), here so that the
+                      // first loads need only the kernel arguments
 };
 
 DUCK_HD constexpr int tri(int i, int j) { return i * (i + 1) / 2 + j; }

@@ -199,7 +199,9 @@ template <class R, int B, int J, int CG, int CS, int L> class Batch final : publ
   void advance(unsigned char *states, int n, const void *targets, const void *forces,
                const void *motor, int substeps, double kp, double limit, hipStream_t s) {
     StepArgs args{dModel, dPoints, states, blobBytes, n, targets, forces, motor,
-                  substeps, motor != nullptr, kp, limit};
+                  substeps, motor != nullptr, kp, limit,
+                  int(host.bodies.size()), int(host.joints.size()), int(host.shapes.size()),
+                  int(host.pairs.size())};
     advanceKernel<R, B, J, CG, CS, L><<<(n + G - 1) / G, 64, 0, s>>>(args);
     launched("advanceKernel");
   }
