@@ -1026,7 +1026,7 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
     // When each of the first two colours fits in one pass of the block-solve
     // slots, every lane's body for them is fixed for the whole step.
     bool twoColourSlots = false;
-    int mine[2] = {-1, -1}, partOf[2] = {part, part}, partsOf[2] = {P, P}, partner[2] = {0, 0};
+    int mine[2] = {-1, -1}, partOf[2] = {part, part}, partsOf[2] = {P, P};
     if (active) {
       const int c0 = E.colorStart[0], c1 = E.colorStart[1], c2 = E.colorStart[2];
       twoColourSlots = c1 - c0 <= L / P && c2 - c1 <= L / P;
@@ -1058,20 +1058,23 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
           }
           if (best < 0)
             continue;
-          // The busy body moves to slot 0 (order within a colour is free:
-          // same-colour bodies do not interact) and borrows slot 7, so the
-          // two slots' pair sums meet through fixed DPP row rotations.
+          // The busy body takes slots 0 and 4 (order within a colour is free:
+          // same-colour bodies do not interact), so that one DPP row
+          // rotation by 12 meets the two slots' pair sums in both; the bodies
+          // it displaces move to the slot it left and to the free slot 7.
+          const int busy = E.order[cs + best];
           if (slot == 0) {
-            mine[c] = E.order[cs + best];
+            mine[c] = busy;
             partsOf[c] = 4;
-            partner[c] = 1; // takes the sum of slot 7
-          } else if (slot == best) {
-            mine[c] = E.order[cs];
-          } else if (slot == 7) {
-            mine[c] = E.order[cs + best];
+          } else if (slot == 4) {
+            mine[c] = busy;
             partOf[c] = part + 2;
             partsOf[c] = 4;
-            partner[c] = 0; // takes the sum of slot 0
+          } else if (slot == best) {
+            mine[c] = E.order[cs]; // best is neither 0 nor 4 here
+          } else if (slot == 7) {
+            // displaced from slot 4 (or from slot 0 when the busy body was at 4)
+            mine[c] = best == 4 ? E.order[cs] : (n > 4 ? E.order[cs + 4] : -1);
           }
         }
       }
@@ -1091,8 +1094,7 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
             const int bi = c0 ? mine[0] : mine[1];
             if (bi >= 0)
               maxUpdate = mx(maxUpdate, stp.updateBody(bi, true, c0 ? partOf[0] : partOf[1],
-                                                       c0 ? partsOf[0] : partsOf[1],
-                                                       c0 ? partner[0] : partner[1], quadPass));
+                                                       c0 ? partsOf[0] : partsOf[1], quadPass));
           } else {
             for (int k = E.colorStart[c] + slot; k < E.colorStart[c + 1]; k += L / P)
               maxUpdate = mx(maxUpdate, stp.updateBody(E.order[k], true, part));

@@ -520,10 +520,6 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
   // (i + 1) mod P and (n + 1) mod P; the partial systems are summed on every
   // lane of the group (bitwise the same sum: the pairwise sums commute), all
   // factor, part 0 writes the pose.
-  // nParts (<= 4) is the size of this body's lane group when a colour pass
-  // gives one body two slots (slots 0 and 7, lane and lane ^ 8 in each);
-  // `partner` is 1 in slot 0 and 0 in slot 7, and `quad` tells every lane of
-  // the wave that such a group exists in this pass.
   // Inertia block (kernel.cuh:837-855), assigned into the zeroed H (the
   // first terms of every sum).  With P >= 2 the first two lanes share it:
   // both form theta, the log-Jacobian and rotJ; part 0 applies the world
@@ -848,11 +844,9 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
   // partial systems are summed on every lane of the group (bitwise the same
   // sum: the pairwise sums commute), all factor, part 0 writes the pose.
   // nParts (<= 4) is the size of this body's lane group when a colour pass
-  // gives one body two slots (slots 0 and 7, lane and lane ^ 8 in each);
-  // `partner` is 1 in slot 0 and 0 in slot 7, and `quad` tells every lane of
-  // the wave that such a group exists in this pass.
-  __device__ R updateBody(int bi, bool implicitDrive, int part, int nParts = P, int partner = 0,
-                          bool quad = false) {
+  // gives one body two slots (slots 0 and 4, lane and lane ^ 8 in each), and
+  // `quad` tells every lane of the wave that such a group exists in this pass.
+  __device__ R updateBody(int bi, bool implicitDrive, int part, int nParts = P, bool quad = false) {
     const V3<R> x = X(bi);
     const Q4<R> q = Q(bi);
     Hess<R> H;
@@ -884,20 +878,20 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
         H.g[k] += halfSwap(H.g[k]);
     } else if constexpr (P == 2) {
       if (quad) {
-        // A two-slot group (slots 0 and 7 of the row) adds the other slot's
-        // pair sum: lane i reads lane i - 9 (mod 16) in slot 0 and lane
-        // i - 7 in slot 7.  Both slots then hold (a + b) + (c + d) and
+        // A two-slot group (slots 0 and 4 of the row: lanes 0, 8 and 4, 12)
+        // adds the other slot's pair sum, which lane i finds in lane i - 12
+        // (mod 16) in both slots.  Both then hold (a + b) + (c + d) and
         // (c + d) + (a + b): bitwise equal.
-        const bool four = nParts == 4, fromSeven = partner == 1;
+        const bool four = nParts == 4;
 #pragma unroll
         for (int k = 0; k < 21; ++k) {
-          const R a = rowRotate<9>(H.h[k]), b = rowRotate<7>(H.h[k]);
-          H.h[k] = four ? H.h[k] + (fromSeven ? a : b) : H.h[k];
+          const R o = H.h[k] + rowRotate<12>(H.h[k]);
+          H.h[k] = four ? o : H.h[k];
         }
 #pragma unroll
         for (int k = 0; k < 6; ++k) {
-          const R a = rowRotate<9>(H.g[k]), b = rowRotate<7>(H.g[k]);
-          H.g[k] = four ? H.g[k] + (fromSeven ? a : b) : H.g[k];
+          const R o = H.g[k] + rowRotate<12>(H.g[k]);
+          H.g[k] = four ? o : H.g[k];
         }
       }
     }
