@@ -427,7 +427,13 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
   if (valid && lane < 3)
     fin = static_cast<const R *>(args.forces)[size_t(e) * 3 + lane];
 
-  // Stage the joint model (all 64 lanes).
+  // Stage the joint model (all 64 lanes); the slots of absent hinges hold
+  // zero frames (a lane without a hinge evaluates slot 0).
+  for (int j = t + nj; j < J; j += 64) {
+#pragma unroll
+    for (int k = 0; k < 3; ++k)
+      F.ra[k][j] = F.rb[k][j] = F.axisA[k][j] = F.axisB[k][j] = F.tangentA[k][j] = F.tangentB[k][j] = 0;
+  }
   for (int j = t; j < nj; j += 64) {
     F.a[j] = M.ja[j];
     F.b[j] = M.jb[j];

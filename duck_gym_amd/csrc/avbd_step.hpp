@@ -610,10 +610,12 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
 
   // Rows of one hinge adjacent to body bi (kernel.cuh:861-913); `cur` packs
   // (hinge, body a, body b).  With valid false the rows are stamped with zero
-  // Jacobian, force and stiffness (indices clamped in range), so the same
-  // straight-line code serves a lane without a hinge in this slot.
+  // force and stiffness on hinge 0's geometry between world bodies (finite:
+  // the staged frames of absent hinges are zero), so the same straight-line
+  // code serves a lane without a hinge in this slot.
   // Fast: both wrapped angles on wrapAngle's |a| < 3.14159 branch, `slow`
-  // set otherwise.
+  // set otherwise; the two limit rows and the axis rows, all along +-J5, are
+  // one stamp with the summed force and stiffness (float sums reordered).
   template <bool Fast>
   __device__ void hingeRows(Hess<R> &H, int bi, int cur, bool valid, bool implicitDrive,
                             bool &slow) const {
@@ -622,18 +624,9 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
               jb = valid ? (cur >> 16) & 255 : 0;
     const bool parent = bi == ja;
     const R s = parent ? R(1) : R(-1);
-    JointEval je = evalJoint(ji, ja, jb);
+    const JointEval je = evalJoint(ji, ja, jb);
     if (!Fast && !valid)
       return;
-    if (Fast) {
-      auto z = [&](V3<R> v) { return valid ? v : V3<R>{0, 0, 0}; };
-      je.ra = z(je.ra);
-      je.rb = z(je.rb);
-      je.axis = z(je.axis);
-      je.axisB = z(je.axisB);
-      je.t1 = z(je.t1);
-      je.t2 = z(je.t2);
-    }
     // Anchor rows (k = 0..2): J_k = [s e_k, r x e_k] with r = ra (parent)
     // or -rb (child); their geometric terms share r.  Anchor and axis rows
     // are always active; the limit rows on limited hinges with f < 0 (the
@@ -666,20 +659,25 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
       stampAngular(H, fcross(u, w), fr[k], pr[k]);
       geometricAdd(H, u, w * fr[k]);
     }
+    // Rows along the hinge axis (kernel.cuh:893-913): implicit torque-
+    // limited PD potential, damping/armature, dry friction -- one stamp
+    // with the summed force and stiffness, selected without branches.  The
+    // lower limit row's Jacobian is J5, the upper's -J5.
+    const V3<R> J5 = parent ? -je.axis : je.axis;
     const int lim = F.limited[ji];
     const bool limited = valid & (lim != 0);
+    R limF[2], limK[2];
 #pragma unroll
     for (int k = 5; k < 7; ++k) {
       const R c = fmad(-alpha, mn(E.c0[k][ji], R(0)), je.C[k]);
       const R pen = E.s.penalty[k][ji];
       const R f = mn(fmad(pen, c, E.s.lambda[k][ji]), R(0));
       const bool on = limited && f < 0;
-      stampAngular(H, (k == 5) == parent ? -je.axis : je.axis, on ? f : R(0), on ? pen : R(0));
+      limF[k - 5] = on ? f : R(0);
+      limK[k - 5] = on ? pen : R(0);
+      if constexpr (!Fast)
+        stampAngular(H, k == 5 ? J5 : -J5, limF[k - 5], limK[k - 5]);
     }
-    // Rows along the hinge axis (kernel.cuh:893-913): implicit torque-
-    // limited PD potential, damping/armature, dry friction -- one stamp
-    // with the summed force and stiffness, selected without branches.
-    const V3<R> J5 = parent ? -je.axis : je.axis;
     R wTarget, delta;
     const R a0 = je.angle - E.s.target[ji], a1 = je.angle - E.angle0[ji];
     if constexpr (Fast) {
@@ -705,6 +703,10 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
     const R trial = fmad(E.s.penaltyF[ji], delta, E.s.lambdaF[ji]);
     axisForce += fl > 0 ? clampv(trial, -fl, fl) : R(0);
     axisStiff += fl > 0 && mabs(trial) < fl ? E.s.penaltyF[ji] : R(0);
+    if constexpr (Fast) {
+      axisForce += limF[0] - limF[1];
+      axisStiff += limK[0] + limK[1];
+    }
     stampAngular(H, J5, valid ? axisForce : R(0), valid ? axisStiff : R(0));
   }
 
