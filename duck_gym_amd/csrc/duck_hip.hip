@@ -267,7 +267,9 @@ public:
   void reset(const unsigned char *mask, const void *q, const void *root, const void *ext,
              hipStream_t s) override {
     DeviceGuard guard(device);
-    require(mask && q && root, "reset: null buffer");
+    // joint-indexed buffers of a model without hinges are empty (may be null)
+    const bool noJoints = host.joints.empty();
+    require(mask && (q || noJoints) && root, "reset: null buffer");
     wait(s);
     resetKernel<R, B, J, CG, CS><<<blocks64(count), 64, 0, s>>>(
         dModel, dStates, blobBytes, count, mask, static_cast<const R *>(q),
@@ -278,7 +280,7 @@ public:
   void step(const void *target, const void *force, int substeps, double kp, double limit,
             hipStream_t s) override {
     DeviceGuard guard(device);
-    require(target && force, "step: null buffer");
+    require((target || host.joints.empty()) && force, "step: null buffer");
     // extension.cu:290-294: zero limit = uncapped; negative/non-finite invalid.
     require(substeps > 0 && kp >= 0 && std::isfinite(kp) && limit >= 0 && std::isfinite(limit),
             "Invalid controls");
@@ -288,14 +290,14 @@ public:
   }
   void stepMotor(const void *motor, const void *force, hipStream_t s) override {
     DeviceGuard guard(device);
-    require(motor && force, "step_motor: null buffer");
+    require((motor || host.joints.empty()) && force, "step_motor: null buffer");
     wait(s);
     advance(dStates, count, nullptr, force, motor, 1, 0, 0, s);
     record(s);
   }
   void state(void *bodies, void *joints, void *diag, hipStream_t s) override {
     DeviceGuard guard(device);
-    require(bodies && joints && diag, "state: null buffer");
+    require(bodies && (joints || host.joints.empty()) && diag, "state: null buffer");
     wait(s);
     snapshotKernel<R, B, J, CG, CS><<<blocks64(count), 64, 0, s>>>(
         dModel, dStates, blobBytes, count, static_cast<R *>(bodies), static_cast<R *>(joints),
@@ -332,7 +334,7 @@ public:
   }
   void generalizedLoads(const void *offset, void *out, hipStream_t s) override {
     DeviceGuard guard(device);
-    require(offset && out, "generalized_loads: null buffer");
+    require(offset && (out || host.joints.empty()), "generalized_loads: null buffer");
     wait(s);
     generalizedLoadsKernel<R, B, J, CG, CS><<<blocks64(count), 64, 0, s>>>(
         dModel, dStates, blobBytes, count, static_cast<const R *>(offset), static_cast<R *>(out));

@@ -81,7 +81,7 @@ def compare_env(gpu, ref, tol, what=""):
         worst[key] = float(np.max(np.abs(gpu[key] - ref[key])))
     for key in ("lambda", "penalty"):
         scale = np.maximum(1.0, np.abs(ref[key]))
-        worst[key] = float(np.max(np.abs(gpu[key] - ref[key]) / scale))
+        worst[key] = float(np.max(np.abs(gpu[key] - ref[key]) / scale, initial=0.0))
     for key in ("x", "q"):
         assert worst[key] <= tol, f"{what} {key} differs by {worst[key]:.3g} > {tol:.3g}"
     return worst
