@@ -1086,6 +1086,8 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
       }
     }
     // ---------------- AVBD iterations (kernel.cuh:979-1063) ---------------
+    bool dualRan = false;
+    R dJoint = 0, dAxis = 0, dDepth = 0;
     for (int it = 0; it < M.iterations; ++it) {
       const bool work = active && !E.done;
       if (!__any(work))
@@ -1113,9 +1115,21 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
       if (work) {
         // The lane's first hinge and first ground contact as one straight-
         // line block (stores at its end), then any further ones; the error
-        // is folded in the reference's order (hinges, then contacts).
+        // is folded in the reference's order (hinges, then contacts).  The
+        // constraint values of the last iteration's dual update are the
+        // step's diagnostics (the poses do not move after it).
         const int ngc = E.s.ngc;
         R errC0 = 0;
+        dualRan = true;
+        dJoint = dAxis = dDepth = 0;
+        auto foldJoint = [&](const typename Stepper<R, B, J, CG, CS, L>::JointDual &jd) {
+#pragma unroll
+          for (int k = 0; k < 3; ++k)
+            dJoint = mx(dJoint, mabs(jd.C[k]));
+#pragma unroll
+          for (int k = 3; k < 5; ++k)
+            dAxis = mx(dAxis, mabs(jd.C[k]));
+        };
         static_assert(L <= J && L <= CG, "a lane's first hinge and contact slots exist");
         auto j0 = stp.jointDual(lane, lane < nj, error);
         const auto g0 = stp.groundDual(lane, lane < ngc, errC0);
@@ -1125,20 +1139,29 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
         // unused slot with the values it holds
         stp.storeGroundDual(lane, g0);
         stp.storeJointDual(lane, j0);
+        if (lane < nj)
+          foldJoint(j0);
         for (int ji = lane + L; ji < nj; ji += L) {
           auto jd = stp.jointDual(ji, true, error);
           if (jd.wide)
             error = stp.frictionDual(jd, wrapAngle(jd.angle));
           stp.storeJointDual(ji, jd);
+          foldJoint(jd);
         }
-        if (lane < ngc)
+        if (lane < ngc) {
           error = mx(error, errC0);
-        for (int i = lane + L; i < ngc; i += L)
-          stp.storeGroundDual(i, stp.groundDual(i, true, error));
+          dDepth = mx(dDepth, g0.depth);
+        }
+        for (int i = lane + L; i < ngc; i += L) {
+          const auto gd = stp.groundDual(i, true, error);
+          stp.storeGroundDual(i, gd);
+          dDepth = mx(dDepth, gd.depth);
+        }
         for (int i = lane; i < E.s.nsc; i += L) {
           SelfContact<R> &c = E.s.sc[i];
           V3<R> ra, rb;
           V3<R> C = stp.selfC(c, ra, rb);
+          dDepth = mx(dDepth, mx(R(0), -(C.z + alpha * c.c0)));
           V3<R> f = contactForce(C, c.lambda, c.penalty, c.friction);
           R trial = fhypot(fmad(c.penalty[0], C.x, c.lambda[0]), fmad(c.penalty[1], C.y, c.lambda[1]));
           bool stick = trial <= -c.friction * f.z && double(fhypot(C.x, C.y)) < 1e-5;
@@ -1185,8 +1208,8 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
     if (active && E.s.failed)
       active = false;
     // ---------------- diagnostics and substep summary ---------------------
-    R jointErr = 0, axisErr = 0, pen = 0;
-    if (active) {
+    R jointErr = dJoint, axisErr = dAxis, pen = dDepth;
+    if (active && !dualRan) {
       for (int ji = lane; ji < nj; ji += L) {
         auto je = stp.evalJoint(ji);
 #pragma unroll

@@ -407,6 +407,7 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
     // inputs of the dry-friction part, kept for frictionDual
     R errRows, angle, fl, lambdaF0, penaltyF0;
     bool rough, wide;
+    R C[5]; // anchor and axis constraint values (the step's diagnostics)
   };
   // Dry-friction multiplier and penalty of a hinge for the wrapped angle
   // change `delta`; returns the error after the hinge's terms.
@@ -449,6 +450,9 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
       err = limited ? mx(err, mx(R(0), -c)) : err;
     }
     o.errRows = err;
+#pragma unroll
+    for (int k = 0; k < 5; ++k)
+      o.C[k] = je.C[k];
     o.angle = je.angle - E.angle0[jg];
     o.fl = E.s.frictionloss[jg];
     o.lambdaF0 = E.s.lambdaF[ji];
@@ -474,6 +478,7 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
   struct GroundDual {
     int id;
     R lambda[3], penalty[3];
+    R depth; // max(0, -z) of the contact point (the step's diagnostics)
   };
   __device__ GroundDual groundDual(int i, bool valid, R &error) const {
     const GroundContact<R> &c = E.s.gc[i];
@@ -489,6 +494,7 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
     const R slip = fhypot(C.x, C.y);
     const bool stick = trial <= -mu * f.z && double(slip) < 1e-5;
     GroundDual o;
+    o.depth = mx(R(0), -(C.z + M.alpha * c.c0));
     const int idNew = (id & 0x7fffffff) | (stick ? int(0x80000000u) : 0);
     const R errNew = mx(error, mx(R(0), -C.z));
     o.id = valid ? idNew : id;

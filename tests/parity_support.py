@@ -84,4 +84,10 @@ def compare_env(gpu, ref, tol, what=""):
         worst[key] = float(np.max(np.abs(gpu[key] - ref[key]) / scale, initial=0.0))
     for key in ("x", "q"):
         assert worst[key] <= tol, f"{what} {key} differs by {worst[key]:.3g} > {tol:.3g}"
+    # step diagnostics: max anchor error, penetration, contact count,
+    # converged flag, max axis error (the decoded blob's first five slots)
+    gd, rd = np.asarray(gpu["diag"])[:5], np.asarray(ref["diag"])[:5]
+    assert gd[2] == rd[2] and gd[3] == rd[3], f"{what} diag counts/flags {gd} vs {rd}"
+    worst["diag"] = float(np.max(np.abs(gd - rd)))
+    assert worst["diag"] <= tol, f"{what} diag differs by {worst['diag']:.3g} > {tol:.3g}"
     return worst
