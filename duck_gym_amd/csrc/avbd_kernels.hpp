@@ -924,7 +924,6 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
       if (lane == 0) {
         E.s.nsc = 0;
         E.s.colorCount = 2;
-        E.done = 0;
       }
     } else if (active && lane == 0) {
       int nsc = pairHits;
@@ -950,7 +949,6 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
         for (int b = 0; b < nb; ++b)
           if (E.s.mass[b] > 0 && E.s.colors[b] == c)
             E.order[pos++] = b;
-      E.done = 0;
       for (int k = 0; k < 8; ++k)
         E.stepDiag[k] = 0;
     }
@@ -1088,14 +1086,20 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
     // ---------------- AVBD iterations (kernel.cuh:979-1063) ---------------
     bool dualRan = false;
     R dJoint = 0, dAxis = 0, dDepth = 0;
+    // Convergence is decided from group maxima, identical in every lane of
+    // an environment, so each lane keeps the flag in a register.
+    bool converged = false;
+    // Whether a colour pass has a four-lane group anywhere in the wave (a
+    // lane that stops iterating keeps its group's combine an identity).
+    const bool quadPass0 = P == 2 && __any(active && twoColourSlots && partsOf[0] == 4);
+    const bool quadPass1 = P == 2 && __any(active && twoColourSlots && partsOf[1] == 4);
     for (int it = 0; it < M.iterations; ++it) {
-      const bool work = active && !E.done;
+      const bool work = active && !converged;
       if (!__any(work))
         break;
       R maxUpdate = 0;
       for (int c = 0; c < colours; ++c) {
-        const bool quadPass = P == 2 && c < 2 &&
-                              __any(work && twoColourSlots && (c == 0 ? partsOf[0] : partsOf[1]) == 4);
+        const bool quadPass = c == 0 ? quadPass0 : (c == 1 ? quadPass1 : false);
         if (work && c < E.s.colorCount) {
           if (c < 2 && twoColourSlots) {
             const bool c0 = c == 0;
@@ -1177,13 +1181,12 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
         }
       }
       error = groupMax<L>(error);
+      const bool conv = maxUpdate < M.tolerance && error < M.tolerance;
       if (work && lane == 0) {
         E.stepDiag[kIterations] = R(it + 1);
-        const bool conv = maxUpdate < M.tolerance && error < M.tolerance;
         E.stepDiag[kConverged] = conv ? R(1) : R(0);
-        if (conv)
-          E.done = 1;
       }
+      converged = converged || (work && conv);
       __syncthreads();
     }
     // ---------------- velocity recovery (kernel.cuh:1064-1073) ------------
