@@ -585,6 +585,9 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
 #pragma unroll
     for (int r = 0; r < SPL; ++r) {
       npick[r] = 0;
+#pragma unroll
+      for (int p = 0; p < 4; ++p)
+        picks[r][p] = 0;
       const int si = lane + r * L;
       if (!active || si >= ns)
         continue;
@@ -607,68 +610,79 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
       V3<R> chosen[4];
       int n = 0;
       if (count <= kCachedPoints) {
-        // Predicted heights and world xy of every point, evaluated once and
-        // scanned by the four passes (same expressions, same order of scan).
+        // Predicted heights and world xy of every point, evaluated once as
+        // one straight-line block; entries past `count` come from zero
+        // points and never enter the candidate mask.
         R wz[kCachedPoints], wx[kCachedPoints], wy[kCachedPoints];
+        // body-frame points: staged in LDS, or formed from the shape (a
+        // branch, so that staged shapes never evaluate the shape formula)
+        V3<R> pts[kCachedPoints];
+        if (staged) {
+#pragma unroll
+          for (int k = 0; k < kCachedPoints; ++k)
+            pts[k] = V3<R>{F.spt[k][0][si], F.spt[k][1][si], F.spt[k][2][si]};
+        } else {
+#pragma unroll
+          for (int k = 0; k < kCachedPoints; ++k)
+            pts[k] = k < count ? groundPoint(M, points, si, k, q) : V3<R>{0, 0, 0};
+        }
 #pragma unroll
         for (int k = 0; k < kCachedPoints; ++k) {
-          wz[k] = wx[k] = wy[k] = 0;
-          if (k < count) {
-            const V3<R> local = staged ? V3<R>{F.spt[k][0][si], F.spt[k][1][si], F.spt[k][2][si]}
-                                       : groundPoint(M, points, si, k, q);
-            V3<R> world = x + rotate(q, local);
-            V3<R> vel = v + cross(w, world - x);
-            wz[k] = mn(world.z, world.z + h * vel.z + h * h * gz);
-            wx[k] = world.x;
-            wy[k] = world.y;
-          }
+          V3<R> world = x + rotate(q, pts[k]);
+          V3<R> vel = v + cross(w, world - x);
+          wz[k] = mn(world.z, world.z + h * vel.z + h * h * gz);
+          wx[k] = world.x;
+          wy[k] = world.y;
         }
-        // Pass pk takes the lowest (height, index) among the points below
-        // 3 mm that are not within 5 mm (xy) of a chosen point -- the
-        // reference's scan with ties to the lowest index.  Here a candidate
-        // is tested against the chosen points only once it is the lowest: a
-        // duplicate is dropped for good (the chosen set only grows) and the
-        // search repeats, so a pass costs pk distance tests, not 8 pk.
+        // Pass pk of the reference takes the lowest (height, index) among the
+        // points below 3 mm that are not within 5 mm (xy) of a chosen point.
+        // Equivalently, candidates are visited in ascending (height, index)
+        // order and each is kept unless it lies within 5 mm of a kept one: a
+        // dropped candidate stays dropped (the kept set only grows), so each
+        // round consumes one candidate, found by a pairwise-tree minimum.
         unsigned avail = 0;
 #pragma unroll
         for (int k = 0; k < kCachedPoints; ++k)
           avail |= (k < count && double(wz[k]) < .003) ? 1u << k : 0u;
-#pragma unroll
-        for (int pk = 0; pk < 4; ++pk) {
-          if (n < pk)
+        R keptX[3] = {0, 0, 0}, keptY[3] = {0, 0, 0};
+        for (int t = 0; t < kCachedPoints; ++t) {
+          if (avail == 0 || n == 4)
             break;
-          int best = -1;
-          R lowest = R(INFINITY);
-          for (int tries = 0; tries < kCachedPoints; ++tries) {
-            best = -1;
-            lowest = R(INFINITY);
+          R tz[kCachedPoints], tx[kCachedPoints], ty[kCachedPoints];
+          int tk[kCachedPoints];
 #pragma unroll
-            for (int k = 0; k < kCachedPoints; ++k) {
-              const bool better = ((avail >> k) & 1u) && wz[k] < lowest;
-              best = better ? k : best;
-              lowest = better ? wz[k] : lowest;
-            }
-            if (best < 0)
-              break;
-            R cx = 0, cy = 0;
+          for (int k = 0; k < kCachedPoints; ++k) {
+            tz[k] = ((avail >> k) & 1u) ? wz[k] : R(INFINITY);
+            tx[k] = wx[k];
+            ty[k] = wy[k];
+            tk[k] = k;
+          }
+          // the left operand holds the lower indices: equal heights keep it
 #pragma unroll
-            for (int k = 0; k < kCachedPoints; ++k) {
-              cx = k == best ? wx[k] : cx;
-              cy = k == best ? wy[k] : cy;
-            }
-            bool dup = false;
+          for (int st = 1; st < kCachedPoints; st <<= 1)
 #pragma unroll
-            for (int cc = 0; cc < 3; ++cc)
-              if (cc < pk && double(mhypot(chosen[cc].x - cx, chosen[cc].y - cy)) < .005)
-                dup = true;
-            avail &= ~(1u << best);
-            if (!dup) {
-              picks[r][pk] = best;
-              chosen[pk] = V3<R>{cx, cy, lowest};
-              n = pk + 1;
-              break;
+            for (int k = 0; k < kCachedPoints; k += 2 * st) {
+              const bool right = tz[k + st] < tz[k];
+              tz[k] = right ? tz[k + st] : tz[k];
+              tx[k] = right ? tx[k + st] : tx[k];
+              ty[k] = right ? ty[k + st] : ty[k];
+              tk[k] = right ? tk[k + st] : tk[k];
             }
-            best = -1;
+          avail &= ~(1u << tk[0]);
+          bool dup = false;
+#pragma unroll
+          for (int cc = 0; cc < 3; ++cc)
+            dup = dup | ((cc < n) & withinFiveMm(keptX[cc] - tx[0], keptY[cc] - ty[0]));
+          if (!dup) {
+#pragma unroll
+            for (int cc = 0; cc < 4; ++cc) {
+              picks[r][cc] = cc == n ? tk[0] : picks[r][cc];
+              if (cc < 3) {
+                keptX[cc] = cc == n ? tx[0] : keptX[cc];
+                keptY[cc] = cc == n ? ty[0] : keptY[cc];
+              }
+            }
+            ++n;
           }
         }
       } else {
@@ -688,7 +702,7 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
             bool dup = false;
 #pragma unroll
             for (int cc = 0; cc < 4; ++cc)
-              if (cc < pk && double(mhypot(chosen[cc].x - world.x, chosen[cc].y - world.y)) < .005)
+              if (cc < pk && withinFiveMm(chosen[cc].x - world.x, chosen[cc].y - world.y))
                 dup = true;
             if (dup)
               continue;
@@ -706,21 +720,26 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
       npick[r] = n;
       E.shapeCount[si] = n;
       // Warm-start source in the previous list (still in LDS): the first
-      // entry with this shape and feature, by one pass over the list with
-      // four independent loads per round.
-      int src[4] = {0, 0, 0, 0};
+      // entry with this shape and feature.  One pass from the end of the
+      // list, four independent loads per round, the last match kept; ids
+      // are compared on their shape and feature fields (`key` is -1 for an
+      // absent pick, which no masked id equals).
+      int src[4] = {0, 0, 0, 0}, key[4];
+#pragma unroll
+      for (int p = 0; p < 4; ++p)
+        key[p] = p < n ? gcPack(si, 0, picks[r][p], false) : -1;
       const int ngc = E.s.ngc;
-      for (int i0 = 0; i0 < ngc; i0 += 4) {
+      for (int i0 = (ngc - 1) & ~3; i0 >= 0; i0 -= 4) {
         int ids[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j)
           ids[j] = E.s.gc[i0 + j < ngc ? i0 + j : 0].id;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const bool mine = i0 + j < ngc && gcShape(ids[j]) == si;
+        for (int j = 3; j >= 0; --j) {
+          const int masked = i0 + j < ngc ? ids[j] & kGcShapeFeature : -2;
 #pragma unroll
           for (int p = 0; p < 4; ++p)
-            src[p] = (mine && src[p] == 0 && p < n && gcFeature(ids[j]) == picks[r][p]) ? i0 + j + 1 : src[p];
+            src[p] = masked == key[p] ? i0 + j + 1 : src[p];
         }
       }
 #pragma unroll
@@ -832,9 +851,11 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
             break;
           GroundContact<R> c;
           const int feature = picks[r][p] & 0xFFFFF, src = (picks[r][p] >> 20) - 1;
-          V3<R> local = (F.sflags[si] & 2) ? V3<R>{F.spt[feature][0][si], F.spt[feature][1][si],
-                                                   F.spt[feature][2][si]}
-                                          : groundPoint(M, points, si, feature, q);
+          V3<R> local;
+          if (F.sflags[si] & 2)
+            local = V3<R>{F.spt[feature][0][si], F.spt[feature][1][si], F.spt[feature][2][si]};
+          else
+            local = groundPoint(M, points, si, feature, q);
           const V3<R> world = x + rotate(q, local);
           R lam[3] = {0, 0, 0}, pen[3] = {1000, 1000, 1000};
           R anchor[2] = {world.x, world.y};

@@ -25,6 +25,15 @@ DUCK_HD float matan2(float y, float x) { return atan2f(y, x); }
 DUCK_HD double matan2(double y, double x) { return atan2(y, x); }
 DUCK_HD float mhypot(float x, float y) { return hypotf(x, y); }
 DUCK_HD double mhypot(double x, double y) { return hypot(x, y); }
+// double(hypot(dx, dy)) < .005 as the host's float hypot decides it: that
+// hypot rounds the double square root of the double sum of squares to
+// float, and the float squares are exact in double, so the test is one
+// threshold on that sum -- the smallest sum whose rounded root is not below
+// .005, found by bisection over the doubles.
+DUCK_HD bool withinFiveMm(float dx, float dy) {
+  return double(dx) * double(dx) + double(dy) * double(dy) < 0x1.a36e30068db92p-16;
+}
+DUCK_HD bool withinFiveMm(double dx, double dy) { return hypot(dx, dy) < .005; }
 DUCK_HD float mabs(float x) { return fabsf(x); }
 DUCK_HD double mabs(double x) { return fabs(x); }
 DUCK_HD bool mfinite(float x) { return isfinite(x); }

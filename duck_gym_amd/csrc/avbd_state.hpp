@@ -104,6 +104,8 @@ DUCK_HD int gcShape(int id) { return id & 63; }
 DUCK_HD int gcBody(int id) { return (id >> 6) & 63; }
 DUCK_HD int gcFeature(int id) { return (id >> 12) & 0x7ffff; }
 DUCK_HD bool gcStick(int id) { return id < 0; }
+// the shape and feature fields of a ground-contact id
+constexpr int kGcShapeFeature = 63 | (0x7ffff << 12);
 DUCK_HD int gcPack(int shape, int body, int feature, bool stick) {
   return shape | (body << 6) | (feature << 12) | (stick ? int(0x80000000u) : 0);
 }

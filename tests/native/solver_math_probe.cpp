@@ -78,5 +78,28 @@ int main() {
     mismatches += !same(m1.w, m2.w) + !same(m1.x, m2.x) + !same(m1.y, m2.y) + !same(m1.z, m2.z);
   }
   std::printf("double_fused_mismatches %d\n", mismatches);
+
+  // The 5 mm duplicate test of the ground-point passes against the host's
+  // own float hypot (the library the oracle calls), on offsets spread over
+  // the square and packed within a few ulps of the 5 mm circle.
+  std::uniform_real_distribution<float> side(-0.006f, 0.006f), turn(0.0f, 6.2831853f), jitter(-2e-6f, 2e-6f);
+  long fiveMm = 0;
+  for (int n = 0; n < 4000000; ++n) {
+    float dx, dy;
+    if (n & 1) {
+      dx = side(rng);
+      dy = side(rng);
+    } else {
+      const float a = turn(rng), rr = 0.005f * (1.0f + jitter(rng));
+      dx = rr * std::cos(a);
+      dy = rr * std::sin(a);
+    }
+    fiveMm += withinFiveMm(dx, dy) != (double(std::hypot(dx, dy)) < .005);
+  }
+  const float axis[] = {0.0f, 0.005f, -0.005f, std::nextafter(0.005f, 0.0f), std::nextafter(0.005f, 1.0f)};
+  for (float a : axis)
+    for (float b : axis)
+      fiveMm += withinFiveMm(a, b) != (double(std::hypot(a, b)) < .005);
+  std::printf("five_mm_mismatches %ld\n", fiveMm);
   return 0;
 }

@@ -1,8 +1,10 @@
 """The float solver's own math forms (duck_gym_amd/csrc/avbd_math.hpp),
 built for the host and checked against closed forms: the fitted atan2, the
 small-rotation series of exp/log and of the SO(3) log-Jacobian coefficient
-(kernel.cuh:136-160, 841-850), and that the fused helpers reduce, in double,
-to the reference's operations in the same order (bitwise)."""
+(kernel.cuh:136-160, 841-850), that the fused helpers reduce, in double,
+to the reference's operations in the same order (bitwise), and that the
+ground passes' 5 mm duplicate test decides as the host's float hypot does
+(kernel.cuh:601-653)."""
 
 import shutil
 import subprocess
@@ -41,3 +43,7 @@ def test_small_rotation_series(probe):
 
 def test_fused_forms_are_the_reference_operations_in_double(probe):
     assert probe["double_fused_mismatches"] == 0
+
+
+def test_five_mm_duplicate_test_matches_host_hypot(probe):
+    assert probe["five_mm_mismatches"] == 0
