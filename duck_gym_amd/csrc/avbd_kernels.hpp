@@ -1104,6 +1104,14 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
         }
       }
     }
+    // The lane's assembly plans for its bodies of the first two colours.
+    typename Stepper<R, B, J, CG, CS, L>::SlotPlan plans[2] = {{0, 0}, {0, 0}};
+    if constexpr (sizeof(R) == sizeof(float)) {
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+        if (active && twoColourSlots && mine[c] >= 0)
+          plans[c] = stp.plan(mine[c], partOf[c], partsOf[c]);
+    }
     // ---------------- AVBD iterations (kernel.cuh:979-1063) ---------------
     bool dualRan = false;
     R dJoint = 0, dAxis = 0, dDepth = 0;
@@ -1127,10 +1135,13 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
             const int bi = c0 ? mine[0] : mine[1];
             if (bi >= 0)
               maxUpdate = mx(maxUpdate, stp.updateBody(bi, true, c0 ? partOf[0] : partOf[1],
-                                                       c0 ? partsOf[0] : partsOf[1], quadPass));
+                                                       c0 ? partsOf[0] : partsOf[1], quadPass,
+                                                       c0 ? plans[0] : plans[1]));
           } else {
-            for (int k = E.colorStart[c] + slot; k < E.colorStart[c + 1]; k += L / P)
-              maxUpdate = mx(maxUpdate, stp.updateBody(E.order[k], true, part));
+            for (int k = E.colorStart[c] + slot; k < E.colorStart[c + 1]; k += L / P) {
+              const int bi = E.order[k];
+              maxUpdate = mx(maxUpdate, stp.updateBody(bi, true, part, P, false, stp.plan(bi, part, P)));
+            }
           }
         }
         __syncthreads();

@@ -798,8 +798,42 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
   // and contacts by the generic loops.  Contacts are added before further
   // hinges (a reordering of the sums, float only).  Returns false when a
   // lane's rotation or angle left the fast forms' range.
+  // What the float assembly of body bi on one lane reads before its first
+  // hinge and contacts: the lane's first hinge (packed), its first two
+  // ground contacts (positions p0 and p0 + nParts among the body's) and the
+  // range of its further hinges.  Model adjacency and the step's contact
+  // masks only, so fixed for a whole step: a lane computes it once per step
+  // for its bodies of the first two colours and keeps the two words in
+  // registers, and the assembly starts on the hinge data without the
+  // dependent adjacency loads.
+  struct SlotPlan {
+    int w0; // first hinge (hinge | a << 8 | b << 16) | h0 << 24 | v0 << 25 | v1 << 26 | any contact << 27
+    int w1; // c0 | c1 << 8 | next hinge slot << 16 | end of the body's hinges << 24
+  };
+  __device__ SlotPlan plan(int bi, int part, int nParts) const {
+    const int p0 = (part + nParts - 1) % nParts;
+    const int adjEnd = F.adjStart[bi + 1], adj0 = F.adjStart[bi] + p0;
+    const bool h0 = adj0 < adjEnd;
+    const int packed0 = F.adj[h0 ? adj0 : 0];
+    const uint64_t all = E.gmask[bi];
+    uint64_t m = all;
+#pragma unroll
+    for (int k = 0; k < 3; ++k)
+      m = k < p0 ? m & (m - 1) : m;
+    const bool v0 = m != 0;
+    const int c0 = v0 ? __builtin_ctzll(m) : 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      m = k < nParts ? m & (m - 1) : m;
+    const bool v1 = m != 0;
+    const int c1 = v1 ? __builtin_ctzll(m) : 0;
+    return {packed0 | int(h0) << 24 | int(v0) << 25 | int(v1) << 26 | int(all != 0) << 27,
+            c0 | c1 << 8 | (adj0 + nParts) << 16 | adjEnd << 24};
+  }
+
   template <bool Ground>
-  __device__ bool assembleFast(Hess<R> &H, int bi, bool implicitDrive, int part, int nParts) const {
+  __device__ bool assembleFast(Hess<R> &H, int bi, bool implicitDrive, int part, int nParts,
+                               SlotPlan sp) const {
     bool slow = false;
 #pragma unroll
     for (int k = 0; k < 21; ++k)
@@ -808,32 +842,16 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
     for (int k = 0; k < 6; ++k)
       H.g[k] = 0;
     const int p0 = (part + nParts - 1) % nParts;
-    const int adjEnd = F.adjStart[bi + 1], adj0 = F.adjStart[bi] + p0;
-    const bool h0 = adj0 < adjEnd;
-    const int packed0 = F.adj[h0 ? adj0 : 0];
-    uint64_t m = E.gmask[bi];
-    int c0 = 0, c1 = 0;
-    bool v0 = false, v1 = false;
-    if constexpr (Ground) {
-      // positions p0 and p0 + nParts among the body's contacts
-#pragma unroll
-      for (int k = 0; k < 3; ++k)
-        m = k < p0 ? m & (m - 1) : m;
-      v0 = m != 0;
-      c0 = v0 ? __builtin_ctzll(m) : 0;
-#pragma unroll
-      for (int k = 0; k < 4; ++k)
-        m = k < nParts ? m & (m - 1) : m;
-      v1 = m != 0;
-      c1 = v1 ? __builtin_ctzll(m) : 0;
-    }
+    const int packed0 = sp.w0 & 0xffffff;
+    const bool h0 = (sp.w0 >> 24) & 1;
+    const int adjNext = (sp.w1 >> 16) & 255, adjEnd = (sp.w1 >> 24) & 255;
     inertiaBlock<true>(H, bi, part, slow);
     hingeRows<true>(H, bi, packed0, h0, implicitDrive, slow);
     if constexpr (Ground) {
-      groundRows(H, bi, c0, v0);
-      groundRows(H, bi, c1, v1);
+      groundRows(H, bi, sp.w1 & 255, (sp.w0 >> 25) & 1);
+      groundRows(H, bi, (sp.w1 >> 8) & 255, (sp.w0 >> 26) & 1);
     }
-    for (int adj = adj0 + nParts; adj < adjEnd; adj += nParts)
+    for (int adj = adjNext; adj < adjEnd; adj += nParts)
       hingeRows<true>(H, bi, F.adj[adj], true, implicitDrive, slow);
     int nth = 0;
     for (uint64_t g = E.gmask[bi]; g; g &= g - 1, ++nth)
@@ -854,7 +872,8 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
   // nParts (<= 4) is the size of this body's lane group when a colour pass
   // gives one body two slots (slots 0 and 4, lane and lane ^ 8 in each), and
   // `quad` tells every lane of the wave that such a group exists in this pass.
-  __device__ R updateBody(int bi, bool implicitDrive, int part, int nParts = P, bool quad = false) {
+  // `sp` is plan(bi, part, nParts) (float only).
+  __device__ R updateBody(int bi, bool implicitDrive, int part, int nParts, bool quad, SlotPlan sp) {
     const V3<R> x = X(bi);
     const Q4<R> q = Q(bi);
     Hess<R> H;
@@ -863,8 +882,8 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
       // Wave-uniform choices: with or without the straight-line contacts,
       // and the generic assembly for every lane when any lane fell outside
       // the fast forms.
-      const bool fast = __any(E.gmask[bi] != 0) ? assembleFast<true>(H, bi, implicitDrive, part, nParts)
-                                                 : assembleFast<false>(H, bi, implicitDrive, part, nParts);
+      const bool fast = __any((sp.w0 >> 27) & 1) ? assembleFast<true>(H, bi, implicitDrive, part, nParts, sp)
+                                                  : assembleFast<false>(H, bi, implicitDrive, part, nParts, sp);
       done = !__any(!fast);
     }
     if (!done)
