@@ -36,8 +36,8 @@ DUCK_HD bool withinFiveMm(float dx, float dy) {
 DUCK_HD bool withinFiveMm(double dx, double dy) { return hypot(dx, dy) < .005; }
 DUCK_HD float mabs(float x) { return fabsf(x); }
 DUCK_HD double mabs(double x) { return fabs(x); }
-DUCK_HD bool mfinite(float x) { return isfinite(x); }
-DUCK_HD bool mfinite(double x) { return isfinite(x); }
+DUCK_HD bool mfinite(float x) { return __builtin_isfinite(x); }
+DUCK_HD bool mfinite(double x) { return __builtin_isfinite(x); }
 
 // Solver arithmetic.  The float solver uses the gfx950 reciprocal, square
 // root and reciprocal square root instructions (about 1 ulp) instead of the

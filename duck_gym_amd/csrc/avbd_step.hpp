@@ -139,7 +139,49 @@ template <class R> DUCK_HD void geometricAdd(Hess<R> &H, V3<R> r, V3<R> f) {
 // The float path multiplies by reciprocal pivots (fdivInv).  The factor runs
 // to the end without branching; a non-positive or non-finite pivot anywhere
 // replaces the whole solution by NaN, as the reference's early return does.
+// The float path factors H = L D L^T instead (the same pivots d = l^2, so the
+// same failure test, without the square roots on the pivot chain).
 template <class R> DUCK_HD void solve6(const Hess<R> &H, R x[6]) {
+  if constexpr (sizeof(R) == sizeof(float)) {
+    R W[21], U[21], invD[6]; // W = L D (below the diagonal), U = L
+    bool ok = true;
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+#pragma unroll
+      for (int j = 0; j <= i; ++j) {
+        R v = H.h[tri(i, j)];
+#pragma unroll
+        for (int k = 0; k < j; ++k)
+          v = fmad(-W[tri(i, k)], U[tri(j, k)], v);
+        if (i == j) {
+          ok = ok && v > 0 && mfinite(v);
+          invD[i] = frcp(v);
+        } else {
+          W[tri(i, j)] = v;
+          U[tri(i, j)] = v * invD[j];
+        }
+      }
+    }
+    R y[6];
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+      y[i] = -H.g[i];
+#pragma unroll
+      for (int k = 0; k < i; ++k)
+        y[i] = fmad(-U[tri(i, k)], y[k], y[i]);
+    }
+#pragma unroll
+    for (int i = 5; i >= 0; --i) {
+      x[i] = y[i] * invD[i];
+#pragma unroll
+      for (int k = i + 1; k < 6; ++k)
+        x[i] = fmad(-U[tri(k, i)], x[k], x[i]);
+    }
+#pragma unroll
+    for (int k = 0; k < 6; ++k)
+      x[k] = ok ? x[k] : R(NAN);
+    return;
+  }
   R L[21], inv[6];
   bool ok = true;
 #pragma unroll
@@ -202,6 +244,18 @@ template <class R> DUCK_HD R logJacobianCoef(R a) {
 
 template <class R> DUCK_HD V3<R> unitAxis(int k) {
   return V3<R>{k == 0 ? R(1) : R(0), k == 1 ? R(1) : R(0), k == 2 ? R(1) : R(0)};
+}
+
+// The rotational Jacobian columns e_k - (theta x e_k) / 2 + coef theta x
+// (theta x e_k) (kernel.cuh:851-858) with the unit axes' zeros dropped:
+// theta x (theta x e_k) = theta theta_k - e_k |theta|^2.  The float solver's
+// form (a reordering of the reference's sums).
+template <class R> DUCK_HD void rotationJacobianSparse(V3<R> t, R coef, V3<R> rotJ[3]) {
+  const R xy = coef * (t.x * t.y), xz = coef * (t.x * t.z), yz = coef * (t.y * t.z);
+  const R xx = t.x * t.x, yy = t.y * t.y, zz = t.z * t.z;
+  rotJ[0] = {fmad(-coef, yy + zz, R(1)), fmad(R(-0.5), t.z, xy), fmad(R(0.5), t.y, xz)};
+  rotJ[1] = {fmad(R(0.5), t.z, xy), fmad(-coef, xx + zz, R(1)), fmad(R(-0.5), t.x, yz)};
+  rotJ[2] = {fmad(R(-0.5), t.y, xz), fmad(R(0.5), t.x, yz), fmad(-coef, xx + yy, R(1))};
 }
 
 // Coulomb-projected contact force (kernel.cuh:304-315).
@@ -569,10 +623,14 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
       coef = logJacobianCoef(fnorm(theta));
     }
     V3<R> rotJ[3];
+    if constexpr (Fast) {
+      rotationJacobianSparse(theta, coef, rotJ);
+    } else {
 #pragma unroll
-    for (int k = 0; k < 3; ++k) {
-      V3<R> e = unitAxis<R>(k);
-      rotJ[k] = faxpy(coef, fcross(theta, fcross(theta, e)), faxpy(R(-0.5), fcross(theta, e), e));
+      for (int k = 0; k < 3; ++k) {
+        V3<R> e = unitAxis<R>(k);
+        rotJ[k] = faxpy(coef, fcross(theta, fcross(theta, e)), faxpy(R(-0.5), fcross(theta, e), e));
+      }
     }
     // World inertia at q0, formed once per step by the predictor.
     const R Iw[6] = {E.Iw[0][bi], E.Iw[1][bi], E.Iw[2][bi], E.Iw[3][bi], E.Iw[4][bi], E.Iw[5][bi]};

@@ -79,6 +79,70 @@ int main() {
   }
   std::printf("double_fused_mismatches %d\n", mismatches);
 
+  // The float block solve (L D L^T) against the double Cholesky solve on
+  // random SPD systems (condition up to ~1e3), and both return NaN on an
+  // indefinite one.
+  double solveErr = 0;
+  int solveNan = 0;
+  for (int n = 0; n < 20000; ++n) {
+    double A[6][6];
+    for (int i = 0; i < 6; ++i)
+      for (int j = 0; j < 6; ++j)
+        A[i][j] = u(rng);
+    Hess<double> hd;
+    Hess<float> hf;
+    const double ridge = 0.01 + 2.0 * double(n % 100) / 100;
+    for (int i = 0; i < 6; ++i) {
+      for (int j = 0; j <= i; ++j) {
+        double v = i == j ? ridge : 0.0;
+        for (int k = 0; k < 6; ++k)
+          v += A[i][k] * A[j][k];
+        hf.h[tri(i, j)] = float(v);
+        hd.h[tri(i, j)] = double(hf.h[tri(i, j)]);
+      }
+      hf.g[i] = float(u(rng));
+      hd.g[i] = double(hf.g[i]);
+    }
+    float xf[6];
+    double xd[6], scale = 0;
+    solve6(hf, xf);
+    solve6(hd, xd);
+    for (int i = 0; i < 6; ++i)
+      scale = std::fmax(scale, std::fabs(xd[i]));
+    for (int i = 0; i < 6; ++i)
+      solveErr = std::fmax(solveErr, std::fabs(double(xf[i]) - xd[i]) / scale);
+  }
+  {
+    Hess<float> hf{};
+    Hess<double> hd{};
+    for (int i = 0; i < 6; ++i)
+      hf.h[tri(i, i)] = hd.h[tri(i, i)] = i == 3 ? -1.0f : 1.0f;
+    float xf[6];
+    double xd[6];
+    solve6(hf, xf);
+    solve6(hd, xd);
+    for (int i = 0; i < 6; ++i)
+      solveNan += std::isnan(xf[i]) && std::isnan(xd[i]);
+  }
+  std::printf("solve6_float_rel_error %.9e\n", solveErr);
+  std::printf("solve6_indefinite_nan %d\n", solveNan);
+
+  // The sparse rotational Jacobian columns against e - (t x e) / 2 + c t x (t x e).
+  double jacErr = 0;
+  for (int n = 0; n < 100000; ++n) {
+    const V3<double> t{0.5 * u(rng), 0.5 * u(rng), 0.5 * u(rng)};
+    const double c = 1.0 / 12 + 0.01 * u(rng);
+    V3<double> sparse[3];
+    rotationJacobianSparse(t, c, sparse);
+    for (int k = 0; k < 3; ++k) {
+      const V3<double> e = unitAxis<double>(k);
+      const V3<double> full = (e - cross(t, e) * 0.5) + cross(t, cross(t, e)) * c;
+      jacErr = std::fmax(jacErr, std::fmax(std::fabs(full.x - sparse[k].x),
+                                           std::fmax(std::fabs(full.y - sparse[k].y), std::fabs(full.z - sparse[k].z))));
+    }
+  }
+  std::printf("rotation_jacobian_max_error %.9e\n", jacErr);
+
   // The 5 mm duplicate test of the ground-point passes against the host's
   // own float hypot (the library the oracle calls), on offsets spread over
   // the square and packed within a few ulps of the 5 mm circle.

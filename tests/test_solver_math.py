@@ -4,7 +4,9 @@ small-rotation series of exp/log and of the SO(3) log-Jacobian coefficient
 (kernel.cuh:136-160, 841-850), that the fused helpers reduce, in double,
 to the reference's operations in the same order (bitwise), and that the
 ground passes' 5 mm duplicate test decides as the host's float hypot does
-(kernel.cuh:601-653)."""
+(kernel.cuh:601-653), and that the float block solve's own forms -- the
+L D L^T factorisation and the sparse rotational Jacobian -- agree with the
+reference's Cholesky solve and general form (kernel.cuh:177-228, 851-857)."""
 
 import shutil
 import subprocess
@@ -47,3 +49,13 @@ def test_fused_forms_are_the_reference_operations_in_double(probe):
 
 def test_five_mm_duplicate_test_matches_host_hypot(probe):
     assert probe["five_mm_mismatches"] == 0
+
+
+def test_float_block_solve_matches_cholesky(probe):
+    # float rounding of systems with condition numbers up to ~1e3
+    assert probe["solve6_float_rel_error"] < 2e-3
+    assert probe["solve6_indefinite_nan"] == 6
+
+
+def test_sparse_rotation_jacobian(probe):
+    assert probe["rotation_jacobian_max_error"] < 1e-15
