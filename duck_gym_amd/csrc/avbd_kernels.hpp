@@ -1112,6 +1112,14 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
         if (active && twoColourSlots && mine[c] >= 0)
           plans[c] = stp.plan(mine[c], partOf[c], partsOf[c]);
     }
+    // The ends of the lane's first hinge and the owner of its first ground
+    // contact (the list is fixed until the next detection).
+    const int ends0 = lane < nj ? F.a[lane] | F.b[lane] << 8 : F.a[0] | F.b[0] << 8;
+    int owner0 = 0;
+    if (active && lane < E.s.ngc) {
+      const int id = E.s.gc[lane].id;
+      owner0 = gcBody(id) | gcShape(id) << 8;
+    }
     // ---------------- AVBD iterations (kernel.cuh:979-1063) ---------------
     bool dualRan = false;
     R dJoint = 0, dAxis = 0, dDepth = 0;
@@ -1167,8 +1175,8 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
             dAxis = mx(dAxis, mabs(jd.C[k]));
         };
         static_assert(L <= J && L <= CG, "a lane's first hinge and contact slots exist");
-        auto j0 = stp.jointDual(lane, lane < nj, error);
-        const auto g0 = stp.groundDual(lane, lane < ngc, errC0);
+        auto j0 = stp.jointDual(lane, lane < nj, error, ends0);
+        const auto g0 = stp.groundDual(lane, lane < ngc, errC0, owner0);
         if (__any(j0.wide) && j0.wide)
           error = stp.frictionDual(j0, wrapAngle(j0.angle));
         // unconditional: a lane past the last hinge or contact rewrites its
@@ -1178,7 +1186,7 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
         if (lane < nj)
           foldJoint(j0);
         for (int ji = lane + L; ji < nj; ji += L) {
-          auto jd = stp.jointDual(ji, true, error);
+          auto jd = stp.jointDual(ji, true, error, F.a[ji] | F.b[ji] << 8);
           if (jd.wide)
             error = stp.frictionDual(jd, wrapAngle(jd.angle));
           stp.storeJointDual(ji, jd);
@@ -1189,7 +1197,8 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
           dDepth = mx(dDepth, g0.depth);
         }
         for (int i = lane + L; i < ngc; i += L) {
-          const auto gd = stp.groundDual(i, true, error);
+          const int id = E.s.gc[i].id;
+          const auto gd = stp.groundDual(i, true, error, gcBody(id) | gcShape(id) << 8);
           stp.storeGroundDual(i, gd);
           dDepth = mx(dDepth, gd.depth);
         }

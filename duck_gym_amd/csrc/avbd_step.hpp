@@ -471,16 +471,18 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
     o.lambdaF = o.rough ? clampv(trial, -o.fl, o.fl) : o.lambdaF0;
     o.penaltyF = (o.rough & (mabs(trial) < o.fl)) ? ramped : o.penaltyF0;
     const R residual = fmad(o.penaltyF, delta, o.lambdaF);
-    const R fErr = mx(o.errRows, mabs(o.lambdaF - clampv(residual, -o.fl, o.fl)) / o.penaltyF);
+    const R fErr = mx(o.errRows, fdiv(mabs(o.lambdaF - clampv(residual, -o.fl, o.fl)), o.penaltyF));
     return o.rough ? fErr : o.errRows;
   }
   // The angle change is wrapped by wrapAngle's |a| < 3.14159 form (a + 0);
   // `wide` marks a lane outside it, which the caller completes with
   // frictionDual(o, wrapAngle(o.angle)) -- a branch kept out of this block.
-  __device__ JointDual jointDual(int ji, bool valid, R &error) const {
+  // `ends` is F.a[jg] | F.b[jg] << 8 (jg = valid ? ji : 0), which a lane may
+  // hold in a register for its first hinge.
+  __device__ JointDual jointDual(int ji, bool valid, R &error, int ends) const {
     const int jg = valid ? ji : 0;
     const R alpha = M.alpha;
-    const JointEval je = evalJoint(jg);
+    const JointEval je = evalJoint(jg, ends & 255, ends >> 8);
     JointDual o;
     R err = error;
 #pragma unroll
@@ -534,10 +536,12 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
     R lambda[3], penalty[3];
     R depth; // max(0, -z) of the contact point (the step's diagnostics)
   };
-  __device__ GroundDual groundDual(int i, bool valid, R &error) const {
+  // `owner` is the contact's body | shape << 8 (0 when not valid), which a
+  // lane may hold in a register for its first contact (fixed within a step).
+  __device__ GroundDual groundDual(int i, bool valid, R &error, int owner) const {
     const GroundContact<R> &c = E.s.gc[i];
     const int id = c.id;
-    const int b = valid ? gcBody(id) : 0, shape = valid ? gcShape(id) : 0;
+    const int b = owner & 255, shape = owner >> 8;
     const V3<R> ra = frotate(Q(b), V3<R>{c.local[0], c.local[1], c.local[2]});
     V3<R> C = (X(b) + ra) - V3<R>{c.anchor[0], c.anchor[1], R(0)};
     C.z = fmad(-M.alpha, c.c0, C.z);
