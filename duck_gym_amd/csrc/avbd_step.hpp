@@ -722,10 +722,16 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
 #pragma unroll
     for (int k = 3; k < 5; ++k) {
       const V3<R> t = k == 3 ? je.t1 : je.t2;
-      // operands selected before the product (one straight-line cross)
-      const V3<R> u = parent ? t : je.axisB, w = parent ? je.axisB : t;
-      stampAngular(H, fcross(u, w), fr[k], pr[k]);
-      geometricAdd(H, u, w * fr[k]);
+      if constexpr (Fast) {
+        // The child's row is the parent's negated, (t x axisB) with -f, and
+        // the geometric term is symmetric in its two vectors: no selects.
+        stampAngular(H, fcross(t, je.axisB), s * fr[k], pr[k]);
+        geometricAdd(H, t, je.axisB * fr[k]);
+      } else {
+        const V3<R> u = parent ? t : je.axisB, w = parent ? je.axisB : t;
+        stampAngular(H, fcross(u, w), fr[k], pr[k]);
+        geometricAdd(H, u, w * fr[k]);
+      }
     }
     // Rows along the hinge axis (kernel.cuh:893-913): implicit torque-
     // limited PD potential, damping/armature, dry friction -- one stamp
@@ -775,7 +781,10 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
       axisForce += limF[0] - limF[1];
       axisStiff += limK[0] + limK[1];
     }
-    stampAngular(H, J5, valid ? axisForce : R(0), valid ? axisStiff : R(0));
+    if constexpr (Fast) // J5 = -s axis: the stamp along axis with the force's sign flipped
+      stampAngular(H, je.axis, valid ? -s * axisForce : R(0), valid ? axisStiff : R(0));
+    else
+      stampAngular(H, J5, valid ? axisForce : R(0), valid ? axisStiff : R(0));
   }
 
   // Rows of ground contact `index` of body bi (kernel.cuh:915-931).  A
