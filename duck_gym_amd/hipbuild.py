@@ -6,6 +6,12 @@ Flags:
                      --fmad=false, scripts/build_cuda.py:37)
   -Xclang -target-feature -Xclang -packed-fp32-ops
                      no packed FP32 instructions
+  -mllvm -amdgpu-sched-strategy=iterative-ilp
+                     the machine scheduler's ILP strategy: the step kernel
+                     runs one wave per SIMD (its LDS fixes that), so latency
+                     hiding comes only from independent instructions within
+                     the wave; measured 6 % faster per step than the default
+                     occupancy-driven strategy on the 4096-env workload
 """
 
 from __future__ import annotations
@@ -24,6 +30,7 @@ FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
     "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-sched-strategy=iterative-ilp",
     "-Wall", "-Wno-unused-function", "-Wno-unused-variable",
 ]
 
