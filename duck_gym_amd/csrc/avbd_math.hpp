@@ -70,10 +70,12 @@ DUCK_HD float frsqrt(float x) {
 #endif
 }
 DUCK_HD double frsqrt(double x) { return 1.0 / sqrt(x); }
-// a * b + c.  The float solver fuses it (one rounding, v_fma_f32 -- nvcc
-// contracts the reference's kernel the same way by default); in double it is
-// the separately rounded a * b + c, so every solver expression written with
-// fmad keeps the float64 oracle's operation order and rounding exactly.
+// a * b + c.  The float solver fuses it (one rounding, v_fma_f32; the
+// reference's own CUDA build keeps the two roundings, --fmad=false in
+// scripts/build_cuda.py:37, so the float results differ from it by rounding);
+// in double it is the separately rounded a * b + c, so every solver expression
+// written with fmad keeps the float64 oracle's operation order and rounding
+// exactly.
 DUCK_HD float fmad(float a, float b, float c) { return __builtin_fmaf(a, b, c); }
 DUCK_HD double fmad(double a, double b, double c) { return a * b + c; }
 // |(x, y)|: the hardware square root of x^2 + y^2 in float (solver
