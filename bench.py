@@ -129,7 +129,7 @@ def other_workload(args):
     config = {}
     if args.workload in ("sweep", "drop"):
         sweep = args.workload == "sweep"
-        E = 4096 if sweep else 16384
+        E = args.envs or (4096 if sweep else 16384)
         iterations = 10 if sweep else 15
         model = write_model(Path(tmp.name) / "m", self_contact=sweep)
         batch = CudaBatch(model, E, DT, iterations, 0, False)
@@ -166,7 +166,7 @@ def other_workload(args):
         from duck_gym_amd.tensor_env import TensorEnv
 
         write_model(Path(tmp.name))
-        E, substeps = 32768, 4
+        E, substeps = args.envs or 32768, 4
         env = TensorEnv(Path(tmp.name), E, ITERATIONS, DT, substeps, seed=seed, task="rollout",
                         episode_seconds=10.0)
         torch.manual_seed(seed)
@@ -201,7 +201,8 @@ def main():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=1000)
     p.add_argument("--warmup", type=int, default=100)
-    p.add_argument("--envs", type=int, default=ENVS)
+    p.add_argument("--envs", type=int, default=None,
+                   help="environments (default: 4096; the other workloads' own sizes)")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--substeps", type=int, default=1,
                    help="physics steps per kernel launch (default 1, the tensor-env contract; "
@@ -246,7 +247,7 @@ def main():
     home = np.array([HOME[n] for n in JOINT_NAMES])
     tmp = tempfile.TemporaryDirectory()
     model = write_model(Path(tmp.name) / "standing")
-    E = args.envs
+    E = args.envs or ENVS
     dev = torch.device("cuda:0")
     batch = CudaBatch(model, E, DT, ITERATIONS, 0, False)
     target = torch.tensor(np.tile(home, (E, 1)), dtype=torch.float32, device=dev)
