@@ -1112,9 +1112,24 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
         if (active && twoColourSlots && mine[c] >= 0)
           plans[c] = stp.plan(mine[c], partOf[c], partsOf[c]);
     }
-    // The ends of the lane's first hinge and the owner of its first ground
+    // Which hinge's dual update a lane makes first.  A hinge's dual update
+    // and the next iteration's first-colour block solve of its colour-0 body
+    // evaluate it at the same poses (nothing moves in between), so when every
+    // environment of the wave has fixed first-colour slots, each lane updates
+    // the hinge its first-colour slot stamps first and that slot reuses the
+    // evaluation.  Hinges no such slot stamps (`leftover`) go round-robin.
+    const bool shareEval = sizeof(R) == sizeof(float) && P == 2 && __all(!active || twoColourSlots);
+    const uint32_t allJoints = nj >= 32 ? ~0u : (1u << nj) - 1;
+    int dualJoint = lane < nj ? lane : -1;
+    uint32_t leftover = L >= 32 ? 0u : allJoints & ~((1u << (L & 31)) - 1);
+    if (shareEval) {
+      dualJoint = active && mine[0] >= 0 && ((plans[0].w0 >> 24) & 1) ? plans[0].w0 & 255 : -1;
+      leftover = allJoints & ~uint32_t(groupOr<L>(dualJoint >= 0 ? int(1u << dualJoint) : 0));
+    }
+    // The ends of that hinge and the owner of the lane's first ground
     // contact (the list is fixed until the next detection).
-    const int ends0 = lane < nj ? F.a[lane] | F.b[lane] << 8 : F.a[0] | F.b[0] << 8;
+    const int ends0 = dualJoint >= 0 ? F.a[dualJoint] | F.b[dualJoint] << 8 : F.a[0] | F.b[0] << 8;
+    typename Stepper<R, B, J, CG, CS, L>::JointEval lastEval{};
     int owner0 = 0;
     if (active && lane < E.s.ngc) {
       const int id = E.s.gc[lane].id;
@@ -1141,7 +1156,11 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
           if (c < 2 && twoColourSlots) {
             const bool c0 = c == 0;
             const int bi = c0 ? mine[0] : mine[1];
-            if (bi >= 0)
+            const bool reuse = c0 && shareEval && dualRan;
+            if (bi >= 0 && reuse)
+              maxUpdate = mx(maxUpdate, stp.template updateBody<true>(bi, true, partOf[0], partsOf[0],
+                                                                      quadPass, plans[0], &lastEval));
+            else if (bi >= 0)
               maxUpdate = mx(maxUpdate, stp.updateBody(bi, true, c0 ? partOf[0] : partOf[1],
                                                        c0 ? partsOf[0] : partsOf[1], quadPass,
                                                        c0 ? plans[0] : plans[1]));
@@ -1175,17 +1194,24 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
             dAxis = mx(dAxis, mabs(jd.C[k]));
         };
         static_assert(L <= J && L <= CG, "a lane's first hinge and contact slots exist");
-        auto j0 = stp.jointDual(lane, lane < nj, error, ends0);
+        const bool hasJoint = dualJoint >= 0;
+        auto j0 = stp.jointDual(hasJoint ? dualJoint : lane, hasJoint, error, ends0);
         const auto g0 = stp.groundDual(lane, lane < ngc, errC0, owner0);
         if (__any(j0.wide) && j0.wide)
           error = stp.frictionDual(j0, wrapAngle(j0.angle));
-        // unconditional: a lane past the last hinge or contact rewrites its
-        // unused slot with the values it holds
+        lastEval = j0.je;
+        // unconditional: a lane past the last contact rewrites its unused
+        // slot with the values it holds
         stp.storeGroundDual(lane, g0);
-        stp.storeJointDual(lane, j0);
-        if (lane < nj)
+        if (hasJoint) {
+          stp.storeJointDual(dualJoint, j0);
           foldJoint(j0);
-        for (int ji = lane + L; ji < nj; ji += L) {
+        }
+        int nth = 0;
+        for (uint32_t m = leftover; m; m &= m - 1, ++nth) {
+          if (nth % L != lane)
+            continue;
+          const int ji = __builtin_ctz(m);
           auto jd = stp.jointDual(ji, true, error, F.a[ji] | F.b[ji] << 8);
           if (jd.wide)
             error = stp.frictionDual(jd, wrapAngle(jd.angle));

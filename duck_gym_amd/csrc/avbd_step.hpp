@@ -462,6 +462,7 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
     R errRows, angle, fl, lambdaF0, penaltyF0;
     bool rough, wide;
     R C[5]; // anchor and axis constraint values (the step's diagnostics)
+    JointEval je; // the evaluation (the next first pass may reuse it)
   };
   // Dry-friction multiplier and penalty of a hinge for the wrapped angle
   // change `delta`; returns the error after the hinge's terms.
@@ -484,6 +485,7 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
     const R alpha = M.alpha;
     const JointEval je = evalJoint(jg, ends & 255, ends >> 8);
     JointDual o;
+    o.je = je;
     R err = error;
 #pragma unroll
     for (int k = 0; k < 5; ++k) {
@@ -684,15 +686,21 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
   // Fast: both wrapped angles on wrapAngle's |a| < 3.14159 branch, `slow`
   // set otherwise; the two limit rows and the axis rows, all along +-J5, are
   // one stamp with the summed force and stiffness (float sums reordered).
-  template <bool Fast>
+  // Given: `given` is this hinge's evaluation at the current poses, made by
+  // the dual update (evalJoint is not repeated).
+  template <bool Fast, bool Given = false>
   __device__ void hingeRows(Hess<R> &H, int bi, int cur, bool valid, bool implicitDrive,
-                            bool &slow) const {
+                            bool &slow, const JointEval *given = nullptr) const {
     const R h = M.dt, h2 = h * h, ih2 = frcp(h2), ih = frcp(h), alpha = M.alpha;
     const int ji = valid ? cur & 255 : 0, ja = valid ? (cur >> 8) & 255 : 0,
               jb = valid ? (cur >> 16) & 255 : 0;
     const bool parent = bi == ja;
     const R s = parent ? R(1) : R(-1);
-    const JointEval je = evalJoint(ji, ja, jb);
+    JointEval je;
+    if constexpr (Given)
+      je = *given;
+    else
+      je = evalJoint(ji, ja, jb);
     if (!Fast && !valid)
       return;
     // Anchor rows (k = 0..2): J_k = [s e_k, r x e_k] with r = ra (parent)
@@ -902,9 +910,9 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
             c0 | c1 << 8 | (adj0 + nParts) << 16 | adjEnd << 24};
   }
 
-  template <bool Ground>
+  template <bool Ground, bool Given>
   __device__ bool assembleFast(Hess<R> &H, int bi, bool implicitDrive, int part, int nParts,
-                               SlotPlan sp) const {
+                               SlotPlan sp, const JointEval *given) const {
     bool slow = false;
 #pragma unroll
     for (int k = 0; k < 21; ++k)
@@ -917,7 +925,7 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
     const bool h0 = (sp.w0 >> 24) & 1;
     const int adjNext = (sp.w1 >> 16) & 255, adjEnd = (sp.w1 >> 24) & 255;
     inertiaBlock<true>(H, bi, part, slow);
-    hingeRows<true>(H, bi, packed0, h0, implicitDrive, slow);
+    hingeRows<true, Given>(H, bi, packed0, h0, implicitDrive, slow, given);
     if constexpr (Ground) {
       groundRows(H, bi, sp.w1 & 255, (sp.w0 >> 25) & 1);
       groundRows(H, bi, (sp.w1 >> 8) & 255, (sp.w0 >> 26) & 1);
@@ -943,8 +951,11 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
   // nParts (<= 4) is the size of this body's lane group when a colour pass
   // gives one body two slots (slots 0 and 4, lane and lane ^ 8 in each), and
   // `quad` tells every lane of the wave that such a group exists in this pass.
-  // `sp` is plan(bi, part, nParts) (float only).
-  __device__ R updateBody(int bi, bool implicitDrive, int part, int nParts, bool quad, SlotPlan sp) {
+  // `sp` is plan(bi, part, nParts) (float only).  Given: `given` is the
+  // evaluation of the lane's first hinge at the current poses (float only).
+  template <bool Given = false>
+  __device__ R updateBody(int bi, bool implicitDrive, int part, int nParts, bool quad, SlotPlan sp,
+                          const JointEval *given = nullptr) {
     const V3<R> x = X(bi);
     const Q4<R> q = Q(bi);
     Hess<R> H;
@@ -953,8 +964,9 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
       // Wave-uniform choices: with or without the straight-line contacts,
       // and the generic assembly for every lane when any lane fell outside
       // the fast forms.
-      const bool fast = __any((sp.w0 >> 27) & 1) ? assembleFast<true>(H, bi, implicitDrive, part, nParts, sp)
-                                                  : assembleFast<false>(H, bi, implicitDrive, part, nParts, sp);
+      const bool fast = __any((sp.w0 >> 27) & 1)
+                            ? assembleFast<true, Given>(H, bi, implicitDrive, part, nParts, sp, given)
+                            : assembleFast<false, Given>(H, bi, implicitDrive, part, nParts, sp, given);
       done = !__any(!fast);
     }
     if (!done)
