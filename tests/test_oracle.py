@@ -317,3 +317,27 @@ def _descends(i, root, parent):
         if i not in parent:
             return False
         i = parent[i]
+
+
+def test_exact_operation_count(tmp_path):
+    """oracle/op_count: the oracle instantiated with an operation-counting
+    number type gives the exact FLOP per env-step of the reference algorithm
+    (SURVEY's estimate for the MicroDuck HOME step was ~0.84 MFLOP)."""
+    import shutil
+    import subprocess
+
+    from duck_gym_amd.microduck import HOME, JOINT_NAMES, write_model
+
+    if shutil.which("g++") is None:
+        pytest.skip("g++ absent")
+    root = Path(__file__).resolve().parents[1] / "oracle"
+    subprocess.run(["make", "-s", "-C", str(root), "op_count"], check=True, capture_output=True)
+    model = write_model(tmp_path / "m")
+    q = [str(HOME[n]) for n in JOINT_NAMES]
+    out = subprocess.run([str(root / "op_count"), str(model), "40", "10", "0.005", "8", *q],
+                         check=True, capture_output=True, text=True).stdout
+    counts = {k: float(v) for k, v in (line.split() for line in out.splitlines())}
+    assert counts["failed"] == 0
+    total = counts["add_sub"] + counts["mul"] + counts["div"] + counts["sqrt"]
+    assert counts["flop_per_step"] == pytest.approx(total)
+    assert 5e5 < counts["flop_per_step"] < 1.5e6
