@@ -251,94 +251,97 @@ template <class R> DUCK_HD V3<R> closestToOrigin(V3<R> a, V3<R> b, V3<R> c) {
   return best;
 }
 
+// The portal is four named points (p0 the interior point) whose updates are
+// selected, never addressed: an indexed array here became scratch memory.
 template <class R> DUCK_HD MprHit<R> mprContact(const MprQuery<R> &Qy, R tolerance) {
   using SP = typename MprQuery<R>::SP;
+  auto pick = [](bool c, const SP &x, const SP &y) {
+    return SP{c ? x.v : y.v, c ? x.a : y.a, c ? x.b : y.b};
+  };
   MprHit<R> hit{0, {0, 0, 0}, {0, 0, 0}, 0};
-  SP p[4];
+  SP p0, p1, p2, p3;
   const auto &M = Qy.M;
   V3<R> ia{M.interior[0][Qy.sa], M.interior[1][Qy.sa], M.interior[2][Qy.sa]};
   V3<R> ib{M.interior[0][Qy.sb], M.interior[1][Qy.sb], M.interior[2][Qy.sb]};
-  p[0].a = Qy.xa + rotate(Qy.qa, ia);
-  p[0].b = Qy.xb + rotate(Qy.qb, ib);
-  p[0].v = p[0].a - p[0].b;
+  p0.a = Qy.xa + rotate(Qy.qa, ia);
+  p0.b = Qy.xb + rotate(Qy.qb, ib);
+  p0.v = p0.a - p0.b;
   R size = mx(R(0.001), M.radius[Qy.sa] + M.radius[Qy.sb]);
   R eps = tolerance * R(0.01);
-  if (norm(p[0].v) < eps)
-    p[0].v.x += eps * R(10);
-  V3<R> dir = unitOrNan(-p[0].v);
-  p[1] = Qy.support(dir);
-  if (dot(p[1].v, dir) <= 0)
+  if (norm(p0.v) < eps)
+    p0.v.x += eps * R(10);
+  V3<R> dir = unitOrNan(-p0.v);
+  p1 = Qy.support(dir);
+  if (dot(p1.v, dir) <= 0)
     return hit;
-  dir = cross(p[0].v, p[1].v);
+  dir = cross(p0.v, p1.v);
   if (norm(dir) <= eps * size) {
     hit.status = 1;
-    hit.depth = norm(p[1].v);
-    hit.normal = hit.depth > eps ? -unitOrNan(p[1].v) : unitOrNan(p[0].v);
-    hit.position = divide(p[1].a + p[1].b, R(2));
+    hit.depth = norm(p1.v);
+    hit.normal = hit.depth > eps ? -unitOrNan(p1.v) : unitOrNan(p0.v);
+    hit.position = divide(p1.a + p1.b, R(2));
     return hit;
   }
   dir = unitOrNan(dir);
-  p[2] = Qy.support(dir);
-  if (dot(p[2].v, dir) <= 0)
+  p2 = Qy.support(dir);
+  if (dot(p2.v, dir) <= 0)
     return hit;
-  dir = unitOrNan(cross(p[1].v - p[0].v, p[2].v - p[0].v));
-  if (dot(dir, p[0].v) > 0) {
-    SP t = p[1];
-    p[1] = p[2];
-    p[2] = t;
+  dir = unitOrNan(cross(p1.v - p0.v, p2.v - p0.v));
+  if (dot(dir, p0.v) > 0) {
+    const SP t = p1;
+    p1 = p2;
+    p2 = t;
     dir = -dir;
   }
   bool discovered = false;
   for (int it = 0; it < 128; ++it) {
     if (!mfinite(dir.x))
       break;
-    p[3] = Qy.support(dir);
-    if (dot(p[3].v, dir) <= 0)
+    p3 = Qy.support(dir);
+    if (dot(p3.v, dir) <= 0)
       return hit;
-    if (dot(cross(p[1].v, p[3].v), p[0].v) < -eps * size * size) {
-      p[2] = p[3];
-    } else if (dot(cross(p[3].v, p[2].v), p[0].v) < -eps * size * size) {
-      p[1] = p[3];
-    } else {
+    const bool into2 = dot(cross(p1.v, p3.v), p0.v) < -eps * size * size;
+    const bool into1 = !into2 && dot(cross(p3.v, p2.v), p0.v) < -eps * size * size;
+    if (!into2 && !into1) {
       discovered = true;
       break;
     }
-    dir = unitOrNan(cross(p[1].v - p[0].v, p[2].v - p[0].v));
+    p2 = pick(into2, p3, p2);
+    p1 = pick(into1, p3, p1);
+    dir = unitOrNan(cross(p1.v - p0.v, p2.v - p0.v));
   }
   if (!discovered) {
     hit.status = -1;
     return hit;
   }
-  auto portalDir = [&]() { return unitOrNan(cross(p[2].v - p[1].v, p[3].v - p[1].v)); };
-  auto advanceOf = [&](const SP &s, V3<R> d) {
-    return dot(s.v, d) - mx(dot(p[1].v, d), mx(dot(p[2].v, d), dot(p[3].v, d)));
+  auto portalDir = [&]() { return unitOrNan(cross(p2.v - p1.v, p3.v - p1.v)); };
+  auto advanceOf = [&](const SP &v, V3<R> d) {
+    return dot(v.v, d) - mx(dot(p1.v, d), mx(dot(p2.v, d), dot(p3.v, d)));
   };
+  // The new support point replaces p1 (both sides positive, or both
+  // negative), p3 (p1's side positive, p2's not) or p2 (p1's side negative,
+  // p3's positive) -- the reference's choice of the portal face to keep.
   auto expand = [&](const SP &v) {
-    V3<R> c = cross(v.v, p[0].v);
-    if (dot(p[1].v, c) > 0) {
-      if (dot(p[2].v, c) > 0)
-        p[1] = v;
-      else
-        p[3] = v;
-    } else if (dot(p[3].v, c) > 0) {
-      p[2] = v;
-    } else {
-      p[1] = v;
-    }
+    const V3<R> c = cross(v.v, p0.v);
+    const bool s1 = dot(p1.v, c) > 0, s2 = dot(p2.v, c) > 0, s3 = dot(p3.v, c) > 0;
+    const bool to1 = s1 ? s2 : !s3, to3 = s1 && !s2, to2 = !s1 && s3;
+    p1 = pick(to1, v, p1);
+    p2 = pick(to2, v, p2);
+    p3 = pick(to3, v, p3);
   };
   bool inside = false;
   for (int it = 0; it < 128; ++it) {
     dir = portalDir();
     if (!mfinite(dir.x))
       break;
-    if (dot(dir, p[1].v) >= -eps) {
+    if (dot(dir, p1.v) >= -eps) {
       inside = true;
       break;
     }
-    SP s = Qy.support(dir);
-    if (dot(s.v, dir) < 0 || advanceOf(s, dir) <= tolerance)
+    const SP sp = Qy.support(dir);
+    if (dot(sp.v, dir) < 0 || advanceOf(sp, dir) <= tolerance)
       return hit;
-    expand(s);
+    expand(sp);
   }
   if (!inside) {
     hit.status = -1;
@@ -348,34 +351,36 @@ template <class R> DUCK_HD MprHit<R> mprContact(const MprQuery<R> &Qy, R toleran
     dir = portalDir();
     if (!mfinite(dir.x))
       break;
-    SP s = Qy.support(dir);
-    if (advanceOf(s, dir) <= tolerance) {
-      V3<R> closest = closestToOrigin(p[1].v, p[2].v, p[3].v);
+    const SP sp = Qy.support(dir);
+    if (advanceOf(sp, dir) <= tolerance) {
+      V3<R> closest = closestToOrigin(p1.v, p2.v, p3.v);
       hit.depth = norm(closest);
       hit.normal = hit.depth > eps ? -divide(closest, hit.depth) : -dir;
       // Barycentric position on the portal (convex.cuh:105-123).
-      R w[4] = {dot(cross(p[1].v, p[2].v), p[3].v), dot(cross(p[3].v, p[2].v), p[0].v),
-                dot(cross(p[0].v, p[1].v), p[3].v), dot(cross(p[2].v, p[1].v), p[0].v)};
-      R sum = w[0] + w[1] + w[2] + w[3];
+      R w0 = dot(cross(p1.v, p2.v), p3.v), w1 = dot(cross(p3.v, p2.v), p0.v),
+        w2 = dot(cross(p0.v, p1.v), p3.v), w3 = dot(cross(p2.v, p1.v), p0.v);
+      R sum = ((w0 + w1) + w2) + w3;
       if (!(sum > 0)) {
-        w[0] = 0;
-        w[1] = dot(cross(p[2].v, p[3].v), dir);
-        w[2] = dot(cross(p[3].v, p[1].v), dir);
-        w[3] = dot(cross(p[1].v, p[2].v), dir);
-        sum = w[1] + w[2] + w[3];
+        w0 = 0;
+        w1 = dot(cross(p2.v, p3.v), dir);
+        w2 = dot(cross(p3.v, p1.v), dir);
+        w3 = dot(cross(p1.v, p2.v), dir);
+        sum = (w1 + w2) + w3;
       }
       if (!(sum > 0)) {
         hit.position = {R(NAN), R(NAN), R(NAN)};
       } else {
         V3<R> pos{0, 0, 0};
-        for (int i = 0; i < 4; ++i)
-          pos = pos + (p[i].a + p[i].b) * (w[i] / (R(2) * sum));
+        pos = pos + (p0.a + p0.b) * (w0 / (R(2) * sum));
+        pos = pos + (p1.a + p1.b) * (w1 / (R(2) * sum));
+        pos = pos + (p2.a + p2.b) * (w2 / (R(2) * sum));
+        pos = pos + (p3.a + p3.b) * (w3 / (R(2) * sum));
         hit.position = pos;
       }
       hit.status = mfinite(hit.position.x) ? 1 : -1;
       return hit;
     }
-    expand(s);
+    expand(sp);
   }
   hit.status = -1;
   return hit;
@@ -573,6 +578,73 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
   for (int sub = 0; sub < args.substeps; ++sub) {
     if (!__any(active))
       break;
+    // ---------------- detection: body-body pairs (kernel.cuh:656-722) ----
+    // (before the ground manifolds, so that the narrow phase does not hold
+    // the ground passes' warm-start registers)
+    struct PairGeom {
+      V3<R> n, t1, t2, local, localB;
+      R c0, lambda[3], penalty[3];
+      int src;
+    };
+    PairGeom pg[PPL];
+#pragma unroll
+    for (int r = 0; r < PPL; ++r) {
+      const int pi = lane + r * L;
+      if (!active || pi >= np)
+        continue;
+      E.pairHit[pi] = 0;
+      const int sa = M.pa[pi], sb = M.pb[pi], A = M.sbody[sa], Bb = M.sbody[sb];
+      if (E.s.mass[A] == 0 && E.s.mass[Bb] == 0)
+        continue;
+      V3<R> xa = stp.X(A), xb = stp.X(Bb);
+      Q4<R> qa = stp.Q(A), qb = stp.Q(Bb);
+      R skin = R(.003) + h * (norm(stp.Vel(A) - stp.Vel(Bb)) + norm(stp.Omega(A)) * M.radius[sa] +
+                              norm(stp.Omega(Bb)) * M.radius[sb]);
+      if (norm(xa - xb) > M.radius[sa] + M.radius[sb] + skin)
+        continue;
+      MprQuery<R> qy{M, points, sa, sb, xa, xb, qa, qb, skin};
+      MprHit<R> hit = mprContact(qy, mx(R(1e-8), M.tolerance * R(.1)));
+      if (hit.status < 0) {
+        E.s.failed = 1;
+        continue;
+      }
+      if (hit.status == 0)
+        continue;
+      PairGeom &o = pg[r];
+      o.n = hit.normal;
+      o.t1 = unitOrNan(cross(mabs(o.n.x) < R(.8) ? V3<R>{1, 0, 0} : V3<R>{0, 1, 0}, o.n));
+      o.t2 = cross(o.n, o.t1);
+      R gap = skin - hit.depth;
+      o.local = rotate(conj(qa), (hit.position + o.n * (gap / R(2))) - xa);
+      o.localB = rotate(conj(qb), (hit.position - o.n * (gap / R(2))) - xb);
+      o.c0 = mn(gap, R(0));
+      o.src = -1;
+      for (int i = 0; i < E.s.nsc; ++i) {
+        const SelfContact<R> &old = E.s.sc[i];
+        V3<R> on{old.n[0], old.n[1], old.n[2]};
+        V3<R> ol{old.local[0], old.local[1], old.local[2]},
+            olb{old.localB[0], old.localB[1], old.localB[2]};
+        if (scShape(old.id) == sa && scOtherShape(old.id) == sb && dot(on, o.n) > R(.95) &&
+            norm(rotate(qa, ol - o.local)) < R(.005) && norm(rotate(qb, olb - o.localB)) < R(.005)) {
+          o.src = i;
+          break;
+        }
+      }
+      if (o.src >= 0) {
+        // the source's force in the new basis, read while the previous list
+        // is still in LDS
+        const SelfContact<R> &old = E.s.sc[o.src];
+        V3<R> f = ((V3<R>{old.t1[0], old.t1[1], old.t1[2]} * old.lambda[0]) +
+                   (V3<R>{old.t2[0], old.t2[1], old.t2[2]} * old.lambda[1])) +
+                  (V3<R>{old.n[0], old.n[1], old.n[2]} * old.lambda[2]);
+        o.lambda[0] = dot(f, o.t1);
+        o.lambda[1] = dot(f, o.t2);
+        o.lambda[2] = dot(f, o.n);
+        for (int d = 0; d < 3; ++d)
+          o.penalty[d] = old.penalty[d];
+      }
+      E.pairHit[pi] = 1;
+    }
     // ---------------- detection: ground manifolds (kernel.cuh:601-653) ----
     // Per pick: point index | (warm-start source + 1) << 20, so that only
     // four registers per shape live across the barrier into compaction.
@@ -760,71 +832,6 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
         wm.anchor[1] = old.anchor[1];
         wm.stick = gcStick(old.id);
       }
-    }
-    // ---------------- detection: body-body pairs (kernel.cuh:656-722) ----
-    struct PairGeom {
-      V3<R> n, t1, t2, local, localB;
-      R c0, lambda[3], penalty[3];
-      int src;
-    };
-    PairGeom pg[PPL];
-#pragma unroll
-    for (int r = 0; r < PPL; ++r) {
-      const int pi = lane + r * L;
-      if (!active || pi >= np)
-        continue;
-      E.pairHit[pi] = 0;
-      const int sa = M.pa[pi], sb = M.pb[pi], A = M.sbody[sa], Bb = M.sbody[sb];
-      if (E.s.mass[A] == 0 && E.s.mass[Bb] == 0)
-        continue;
-      V3<R> xa = stp.X(A), xb = stp.X(Bb);
-      Q4<R> qa = stp.Q(A), qb = stp.Q(Bb);
-      R skin = R(.003) + h * (norm(stp.Vel(A) - stp.Vel(Bb)) + norm(stp.Omega(A)) * M.radius[sa] +
-                              norm(stp.Omega(Bb)) * M.radius[sb]);
-      if (norm(xa - xb) > M.radius[sa] + M.radius[sb] + skin)
-        continue;
-      MprQuery<R> qy{M, points, sa, sb, xa, xb, qa, qb, skin};
-      MprHit<R> hit = mprContact(qy, mx(R(1e-8), M.tolerance * R(.1)));
-      if (hit.status < 0) {
-        E.s.failed = 1;
-        continue;
-      }
-      if (hit.status == 0)
-        continue;
-      PairGeom &o = pg[r];
-      o.n = hit.normal;
-      o.t1 = unitOrNan(cross(mabs(o.n.x) < R(.8) ? V3<R>{1, 0, 0} : V3<R>{0, 1, 0}, o.n));
-      o.t2 = cross(o.n, o.t1);
-      R gap = skin - hit.depth;
-      o.local = rotate(conj(qa), (hit.position + o.n * (gap / R(2))) - xa);
-      o.localB = rotate(conj(qb), (hit.position - o.n * (gap / R(2))) - xb);
-      o.c0 = mn(gap, R(0));
-      o.src = -1;
-      for (int i = 0; i < E.s.nsc; ++i) {
-        const SelfContact<R> &old = E.s.sc[i];
-        V3<R> on{old.n[0], old.n[1], old.n[2]};
-        V3<R> ol{old.local[0], old.local[1], old.local[2]},
-            olb{old.localB[0], old.localB[1], old.localB[2]};
-        if (scShape(old.id) == sa && scOtherShape(old.id) == sb && dot(on, o.n) > R(.95) &&
-            norm(rotate(qa, ol - o.local)) < R(.005) && norm(rotate(qb, olb - o.localB)) < R(.005)) {
-          o.src = i;
-          break;
-        }
-      }
-      if (o.src >= 0) {
-        // the source's force in the new basis, read while the previous list
-        // is still in LDS
-        const SelfContact<R> &old = E.s.sc[o.src];
-        V3<R> f = ((V3<R>{old.t1[0], old.t1[1], old.t1[2]} * old.lambda[0]) +
-                   (V3<R>{old.t2[0], old.t2[1], old.t2[2]} * old.lambda[1])) +
-                  (V3<R>{old.n[0], old.n[1], old.n[2]} * old.lambda[2]);
-        o.lambda[0] = dot(f, o.t1);
-        o.lambda[1] = dot(f, o.t2);
-        o.lambda[2] = dot(f, o.n);
-        for (int d = 0; d < 3; ++d)
-          o.penalty[d] = old.penalty[d];
-      }
-      E.pairHit[pi] = 1;
     }
     __syncthreads();
     // ---------------- compaction + warm start ----------------------------
