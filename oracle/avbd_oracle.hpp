@@ -1,7 +1,7 @@
 // CPU oracle for the batched AVBD environment step: TEST INFRASTRUCTURE.
 //
 // A clean-room restatement of the reference's two solver semantics, used only
-// as the checker in tests/, the bench's cpu_baseline leg and smoke():
+// for the expected values in tests/, the bench's cpu_baseline leg and smoke():
 //   mode 0  implicit-coloured  = src/cuda/kernel.cuh + convex.cuh + model.hpp
 //                                 (what the reference's CudaBatch computes)
 //   mode 1  explicit-sequential = src/solver.cpp (explicit PD predictor,

@@ -322,7 +322,8 @@ def _descends(i, root, parent):
 def test_exact_operation_count(tmp_path):
     """oracle/op_count: the oracle instantiated with an operation-counting
     number type gives the exact FLOP per env-step of the reference algorithm
-    (SURVEY's estimate for the MicroDuck HOME step was ~0.84 MFLOP)."""
+    (about 0.84 MFLOP for the MicroDuck HOME step by a count of the code's
+    structure)."""
     import shutil
     import subprocess
 
