@@ -1,0 +1,151 @@
+"""Every collision-shape kind against the oracle: a three-hinge body imported
+from MJCF (duck_gym_amd/duck_format.py) whose box, two capsules (one on the
+base, one on the leg), sphere and 12-vertex hull all reach the ground, and a
+v2 variant whose leg capsule and hull collide.  This covers the kernel paths
+the MicroDuck models do not: a sphere's and a capsule's ground points
+(kernel.cuh:576-583), a hull of more points than the staged point sets (the
+uncached ground scan), a body of two shapes, and the MPR support of capsules,
+spheres and large hulls (convex.cuh:18-41).
+
+Gates as in test_gpu_parity.py: float64 trajectories equal to the oracle's to
+1e-9 over 40 steps (1e-7 to step 120) with identical contact sets and colours; seeded float32 single steps
+within 1e-5 with identical contact sets."""
+
+
+import numpy as np
+import pytest
+import torch
+
+from duck_gym_amd import CudaBatch
+from duck_gym_amd import duck_format as D
+from parity_support import compare_env, oracle_envs, oracle_state, seed_batch
+
+pytestmark = pytest.mark.gpu
+DT, ITER, KP = 0.005, 10, 8.0
+DEV = "cuda:0"
+
+_PHI = (1 + 5 ** 0.5) / 2
+_ICOSAHEDRON = " ".join(f"{0.02 * x:.6f} {0.02 * y:.6f} {0.02 * z:.6f}"
+                        for a in (-1, 1) for b in (-_PHI, _PHI)
+                        for x, y, z in ((0, a, b), (a, b, 0), (b, 0, a)))
+
+
+def mixed_mjcf(tail_pos):
+    return f"""
+<mujoco>
+  <compiler angle="radian"/>
+  <default><geom friction="0.9" contype="1" conaffinity="2"/></default>
+  <worldbody>
+    <geom type="plane" size="1 1 0.1" contype="2" conaffinity="1"/>
+    <body name="base" pos="0 0 0.14" euler="1.2 -0.3 0.3">
+      <freejoint/>
+      <geom type="box" size="0.06 0.04 0.02" mass="0.5"/>
+      <geom type="capsule" fromto="-0.05 -0.04 -0.02 0.05 -0.04 -0.02" size="0.01" mass="0.05"/>
+      <body name="leg" pos="0.04 0 -0.02">
+        <joint name="hip" axis="0 1 0" range="-0.8 0.8" damping="0.05" armature="0.002"/>
+        <geom type="capsule" fromto="0 0 0 0.02 0 -0.08" size="0.012" mass="0.1"/>
+        <body name="foot" pos="0.02 0 -0.09">
+          <joint name="ankle" axis="1 0 0" range="-0.5 0.5" damping="0.02" armature="0.001"/>
+          <geom type="sphere" size="0.015" mass="0.05"/>
+        </body>
+      </body>
+      <body name="tail" pos="{tail_pos}">
+        <joint name="tail" axis="0 1 0" damping="0.05" armature="0.002"/>
+        <geom type="mesh" mesh="ico" mass="0.08" pos="-0.03 0 -0.04"/>
+      </body>
+    </body>
+  </worldbody>
+  <asset><mesh name="ico" vertex="{_ICOSAHEDRON}"/></asset>
+</mujoco>"""
+
+
+CASES = {
+    # v1: shapes 0 box, 1 base capsule, 2 leg capsule, 3 sphere, 4 hull; all
+    # touch the ground (the leg capsule in the first env only)
+    "ground": ("-0.06 0 0", False, [0.4, -0.3, 0.9]),
+    # v2: the leg capsule and the hull collide; the base capsule, sphere and
+    # hull on the ground
+    "pairs": ("0.02 0.0 -0.04", True, [0.8, 0.4, -2.0]),
+}
+
+
+@pytest.fixture(scope="module")
+def mixed_models(tmp_path_factory):
+    out = {}
+    for name, (tail, pairs, _) in CASES.items():
+        model = D.from_mjcf(mixed_mjcf(tail))
+        if pairs:
+            model = D.with_body_pairs(model)
+        path = tmp_path_factory.mktemp("shapes") / f"{name}.duck"
+        D.write_duck(model, path)
+        out[name] = path
+    return out
+
+
+def targets_for(name, E):
+    base = np.array(CASES[name][2])
+    # per-env variations of the held pose, seeded
+    rng = np.random.default_rng(20260927)
+    return base + rng.uniform(-0.01, 0.01, (E, 3))
+
+
+@pytest.mark.parametrize("split", [False, True], ids=["one-lane", "split"])
+@pytest.mark.parametrize("name", list(CASES))
+def test_fp64_every_shape_kind_matches_oracle(mixed_models, name, split):
+    model, E = mixed_models[name], 4
+    targets = targets_for(name, E)
+    batch = CudaBatch(model, E, DT, ITER, 0, True, split_solve=split)
+    oracles = oracle_envs(model, E, DT, ITER, True)
+    for o, q in zip(oracles, targets):
+        o.reset(q, np.zeros(6))
+    seed_batch(batch, oracles)
+    tg = torch.tensor(targets, dtype=torch.float64, device=DEV)
+    fg = torch.zeros(E, 3, dtype=torch.float64, device=DEV)
+    codec = batch.codec()
+    shapes, pairs = set(), 0
+    for step in range(120):
+        batch.step(tg, fg, 1, KP, 0.0)
+        for o, t in zip(oracles, targets):
+            o.step(t, None, 1, KP, 0.0)
+        raw = batch.export_state().cpu().numpy()
+        for e, o in enumerate(oracles):
+            ref = oracle_state(o)
+            # rounding differences (the device's float64 sin/cos/atan2 are
+            # not the host's) grow through the contacts: 1e-9 over the first
+            # 40 steps, 1e-7 after that; contact sets stay identical
+            tol = 1e-9 if step < 40 else 1e-7
+            compare_env(codec.decode(raw[e]), ref, tol, f"{name} step {step + 1} env {e}")
+            shapes |= {c["shape"] for c in ref["gc"]}
+            pairs += len(ref["sc"])
+    expected = {0, 1, 2, 3, 4} if name == "ground" else {1, 3, 4}
+    assert expected <= shapes, f"ground contacts seen on shapes {sorted(shapes)}"
+    assert (pairs > 0) == (name == "pairs")
+
+
+@pytest.mark.parametrize("name", list(CASES))
+def test_fp32_seeded_steps_every_shape_kind(mixed_models, name):
+    model, E = mixed_models[name], 4
+    targets = targets_for(name, E)
+    batch = CudaBatch(model, E, DT, ITER, 0, False)
+    oracles = oracle_envs(model, E, DT, ITER, False)
+    for o, q in zip(oracles, targets):
+        o.reset(q, np.zeros(6))
+    tg = torch.tensor(targets, dtype=torch.float32, device=DEV)
+    fg = torch.zeros(E, 3, device=DEV)
+    codec = batch.codec()
+    checked = 0
+    for step in range(90):
+        seeded = step % 6 == 5
+        if seeded:
+            seed_batch(batch, oracles)
+            batch.step(tg, fg, 1, KP, 0.0)
+        for o, t in zip(oracles, targets):
+            o.step(t, None, 1, KP, 0.0)
+        if seeded:
+            raw = batch.export_state().cpu().numpy()
+            for e, o in enumerate(oracles):
+                compare_env(codec.decode(raw[e]), oracle_state(o), 1e-5, f"fp32 {name} step {step} env {e}")
+                checked += 1
+    assert checked == 15 * E
+    b, _, d = batch.state()
+    assert bool(torch.isfinite(b).all()) and int((d[:, 5] != 0).sum()) == 0
