@@ -162,7 +162,7 @@ def other_workload(args):
                        "velocity N(0, 0.5), masses x U(0.9, 1.1)",
                   "envs": E, "iterations": iterations, "dt_s": DT, "failed_envs": failed}
         ms = wall / args.steps * 1e3
-    else:
+    elif args.workload == "rollout":
         from duck_gym_amd.tensor_env import TensorEnv
 
         write_model(Path(tmp.name))
@@ -190,6 +190,33 @@ def other_workload(args):
                   "envs": E, "iterations": ITERATIONS, "dt_s": DT,
                   "physics_steps_per_control_step": substeps,
                   "control_steps_per_s": E * args.steps / wall}
+    elif args.workload == "train":
+        from duck_gym_amd.on_policy import STANDING, OnPolicyRunner
+        from duck_gym_amd.tensor_env import TensorEnv
+
+        write_model(Path(tmp.name))
+        E, substeps = args.envs or 4096, 4
+        env = TensorEnv(Path(tmp.name), E, ITERATIONS, DT, substeps, seed=seed, task="standing")
+        torch.manual_seed(seed)
+        runner = OnPolicyRunner(env, STANDING, device="cuda:0")
+        runner.learn(args.warmup, init_at_random_ep_len=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        runner.learn(args.steps)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        T = STANDING["num_steps_per_env"]
+        value = E * T * args.steps * substeps / wall
+        ms = wall / args.steps * 1e3
+        timed = runner.history[-args.steps:]
+        config = {"workload": "PPO training iterations (configs/standing.json: 24 control steps "
+                              "per env, 4 epochs x 4 mini-batches, 64-64 ELU actor and critic, "
+                              "empirical normalisation) on the standing tensor env",
+                  "envs": E, "iterations": ITERATIONS, "dt_s": DT,
+                  "physics_steps_per_control_step": substeps,
+                  "control_steps_per_s": E * T * args.steps / wall,
+                  "collection_s_per_iteration": sum(h["collection_s"] for h in timed) / len(timed),
+                  "update_s_per_iteration": sum(h["learning_s"] for h in timed) / len(timed)}
     return {"metric": f"physics env-steps/s ({args.workload} workload)", "value": value,
             "unit": "env-steps/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
             "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
@@ -207,11 +234,14 @@ def main():
     p.add_argument("--substeps", type=int, default=1,
                    help="physics steps per kernel launch (default 1, the tensor-env contract; "
                         "K > 1 runs K steps inside one launch, the reference's chunked form)")
-    p.add_argument("--workload", choices=("home", "sweep", "drop", "rollout"), default="home",
+    p.add_argument("--workload", choices=("home", "sweep", "drop", "rollout", "train"),
+                   default="home",
                    help="home: fixed HOME, 4096 envs (default, the headline line); sweep: "
                         "servo-target sweep with body contacts and per-env friction; drop: "
                         "drop/jump stress, 16384 envs, 15 iterations; rollout: tensor-env "
-                        "rollout with a random MLP policy, 32768 envs")
+                        "rollout with a random MLP policy, 32768 envs; train: PPO iterations "
+                        "of configs/standing.json on the standing tensor env, 4096 envs "
+                        "(--steps and --warmup count learning iterations)")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                    help="only run a plain device copy of MIB MiB (three times): the "
                         "reference dispatch for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE")
