@@ -231,7 +231,16 @@ class PPO:
             raise ValueError(f"Unknown schedule {schedule}")
         self.device = device
         self.policy = policy.to(device)
-        self.optimizer = torch.optim.Adam(self.policy.parameters(), lr=learning_rate)
+        # On the GPU the learning rate lives in device memory (Adam with
+        # capturable=True takes a tensor rate): the KL-adaptive schedule then
+        # makes no host round trip per mini-batch.
+        self._device_lr = torch.device(device).type == "cuda"
+        if self._device_lr:
+            self.optimizer = torch.optim.Adam(
+                self.policy.parameters(), capturable=True,
+                lr=torch.tensor(float(learning_rate), dtype=torch.float32, device=device))
+        else:
+            self.optimizer = torch.optim.Adam(self.policy.parameters(), lr=learning_rate)
         self.learning_rate = learning_rate
         self.num_learning_epochs, self.num_mini_batches = num_learning_epochs, num_mini_batches
         self.clip_param, self.gamma, self.lam = clip_param, gamma, lam
@@ -278,9 +287,38 @@ class PPO:
                          + (old_sigma.square() + (old_mu - mu).square()) / (2 * sigma.square())
                          - 0.5, dim=-1)
 
+    @property
+    def learning_rate(self):
+        return float(self.optimizer.param_groups[0]["lr"])
+
+    @learning_rate.setter
+    def learning_rate(self, value):
+        for group in self.optimizer.param_groups:
+            if torch.is_tensor(group["lr"]):
+                group["lr"].fill_(float(value))
+            else:
+                group["lr"] = float(value)
+
+    def _adapt_learning_rate(self, kl_mean):
+        """lr / 1.5 (not below 1e-5) when the mean KL exceeds twice the target,
+        lr * 1.5 (not above 1e-2) when it is positive and below half of it."""
+        high, low = self.desired_kl * 2.0, self.desired_kl / 2.0
+        if self._device_lr:
+            lr = self.optimizer.param_groups[0]["lr"]
+            lr.copy_(torch.where(kl_mean > high, (lr / 1.5).clamp(min=1e-5),
+                                 torch.where((kl_mean > 0.0) & (kl_mean < low),
+                                             (lr * 1.5).clamp(max=1e-2), lr)))
+            return
+        lr = self.learning_rate
+        if kl_mean > high:
+            self.learning_rate = max(1e-5, lr / 1.5)
+        elif 0.0 < kl_mean < low:
+            self.learning_rate = min(1e-2, lr * 1.5)
+
     def update(self):
         p = self.policy
-        value_sum = surrogate_sum = entropy_sum = 0.0
+        # loss sums stay on the device until the update ends
+        sums = torch.zeros(3, device=self.device)
         n = 0
         for (obs, critic_obs, actions, target_values, advantages, returns, old_log_prob,
              old_mu, old_sigma) in self.storage.mini_batches(self.num_mini_batches,
@@ -293,14 +331,8 @@ class PPO:
             values = p.evaluate(critic_obs)
             mu, sigma, entropy = p.action_mean, p.action_std, p.entropy
             if self.desired_kl is not None and self.schedule == "adaptive":
-                with torch.inference_mode():
-                    kl_mean = self.kl(old_mu, old_sigma, mu, sigma).mean()
-                    if kl_mean > self.desired_kl * 2.0:
-                        self.learning_rate = max(1e-5, self.learning_rate / 1.5)
-                    elif 0.0 < kl_mean < self.desired_kl / 2.0:
-                        self.learning_rate = min(1e-2, self.learning_rate * 1.5)
-                for group in self.optimizer.param_groups:
-                    group["lr"] = self.learning_rate
+                with torch.no_grad():
+                    self._adapt_learning_rate(self.kl(old_mu, old_sigma, mu, sigma).mean())
             ratio = torch.exp(log_prob - old_log_prob.squeeze(-1))
             adv = advantages.squeeze(-1)
             surrogate = torch.max(-adv * ratio, -adv * ratio.clamp(1.0 - self.clip_param,
@@ -317,13 +349,12 @@ class PPO:
             loss.backward()
             nn.utils.clip_grad_norm_(p.parameters(), self.max_grad_norm)
             self.optimizer.step()
-            value_sum += value_loss.item()
-            surrogate_sum += surrogate.item()
-            entropy_sum += entropy.mean().item()
+            sums += torch.stack((value_loss.detach(), surrogate.detach(),
+                                 entropy.mean().detach()))
             n += 1
         self.storage.clear()
-        return {"value_function": value_sum / n, "surrogate": surrogate_sum / n,
-                "entropy": entropy_sum / n}
+        value, surrogate, entropy = (sums / n).tolist()
+        return {"value_function": value, "surrogate": surrogate, "entropy": entropy}
 
 
 class OnPolicyRunner:
@@ -386,7 +417,8 @@ class OnPolicyRunner:
         start = self.current_learning_iteration
         for it in range(start, start + num_learning_iterations):
             t0 = time.perf_counter()
-            finished_return = finished_length = finished = 0.0
+            # episode statistics stay on the device until the iteration ends
+            ended = torch.zeros(3, device=self.device)
             with torch.inference_mode():
                 for _ in range(self.num_steps_per_env):
                     actions = alg.act(obs, critic_obs)
@@ -401,14 +433,16 @@ class OnPolicyRunner:
                     episode_return += rewards
                     episode_length += 1
                     d = dones.bool()
-                    finished_return += float(episode_return[d].sum())
-                    finished_length += float(episode_length[d].sum())
-                    finished += float(d.sum())
-                    episode_return[d] = 0
-                    episode_length[d] = 0
+                    ended += torch.stack((torch.where(d, episode_return, 0).sum(),
+                                          torch.where(d, episode_length, 0).sum(), d.sum()))
+                    episode_return.masked_fill_(d, 0)
+                    episode_length.masked_fill_(d, 0)
+                if torch.device(self.device).type == "cuda":
+                    torch.cuda.synchronize(self.device)  # time the phases, once per iteration
                 collected = time.perf_counter() - t0
                 alg.compute_returns(critic_obs)
             losses = alg.update()
+            finished_return, finished_length, finished = ended.tolist()
             learned = time.perf_counter() - t0 - collected
             self.current_learning_iteration = it
             record = dict(iteration=it, collection_s=collected, learning_s=learned,

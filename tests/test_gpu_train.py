@@ -6,12 +6,14 @@ losses, a policy that moved, the observation normaliser fed every control
 step, and a checkpoint that restores the same deterministic policy."""
 
 import math
+import sys
+from pathlib import Path
 
 import pytest
 import torch
 
 from duck_gym_amd.microduck import write_model
-from duck_gym_amd.on_policy import STANDING, OnPolicyRunner
+from duck_gym_amd.on_policy import PPO, STANDING, ActorCritic, OnPolicyRunner
 from duck_gym_amd.tensor_env import TensorEnv
 
 pytestmark = pytest.mark.gpu
@@ -56,3 +58,19 @@ def test_ppo_iterations_on_the_standing_env(model_dir, tmp_path):
     obs, _ = env.get_observations()
     with torch.no_grad():
         assert torch.equal(again.get_inference_policy()(obs), runner.get_inference_policy()(obs))
+
+
+def test_device_learning_rate_follows_the_host_schedule():
+    """On the GPU the KL-adaptive rate is updated in device memory; it takes
+    the host schedule's decisions, to float32 rounding."""
+    sys.path.insert(0, str(Path(__file__).parent))
+    from test_on_policy import KL_SEQUENCE, expected_rates
+
+    ppo = PPO(ActorCritic(3, 3, 2, [8], [8]), learning_rate=3e-4, schedule="adaptive",
+              device=DEV)
+    assert torch.is_tensor(ppo.optimizer.param_groups[0]["lr"])
+    got = []
+    for kl in KL_SEQUENCE:
+        ppo._adapt_learning_rate(torch.tensor(kl, device=DEV))
+        got.append(ppo.learning_rate)
+    assert got == pytest.approx(expected_rates(3e-4, KL_SEQUENCE), rel=1e-5)

@@ -111,6 +111,34 @@ def test_kl_matches_torch_distributions():
     assert torch.all(ppo.kl(mu0, s0, mu0, s0).abs() < 1e-4)
 
 
+KL_SEQUENCE = [0.05, 0.001, 0.0, 0.01, 0.02, 0.0051, 0.0049] + [1.0] * 12 + [1e-4] * 20
+
+
+def expected_rates(lr, kls, target=0.01):
+    out = []
+    for kl in kls:
+        if kl > 2 * target:
+            lr = lr / 1.5 if lr / 1.5 > 1e-5 else 1e-5
+        elif 0 < kl < target / 2:
+            lr = lr * 1.5 if lr * 1.5 < 1e-2 else 1e-2
+        out.append(lr)
+    return out
+
+
+def test_adaptive_learning_rate_schedule():
+    """Divide by 1.5 above twice the target KL, multiply by 1.5 for a positive
+    KL below half of it, hold otherwise, within [1e-5, 1e-2]."""
+    ppo = PPO(ActorCritic(3, 3, 2, [8], [8]), learning_rate=3e-4, schedule="adaptive")
+    got = []
+    for kl in KL_SEQUENCE:
+        ppo._adapt_learning_rate(torch.tensor(kl))
+        got.append(ppo.learning_rate)
+    want = expected_rates(3e-4, KL_SEQUENCE)
+    assert got[:7] == pytest.approx([2e-4, 3e-4, 3e-4, 3e-4, 3e-4, 3e-4, 4.5e-4], rel=1e-12)
+    assert got == pytest.approx(want, rel=1e-12)
+    assert min(got) == 1e-5 and max(got) == 1e-2
+
+
 def test_timeouts_bootstrap_the_value_into_the_reward():
     torch.manual_seed(0)
     ppo = PPO(ActorCritic(3, 3, 2, [8], [8]), gamma=0.9)
