@@ -259,9 +259,9 @@ def main():
         return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print("bench.py measures one MI355X: environments shard across GPUs with no "
-              "exchange, and this build runs on a single-GPU box (use --gpus 1).",
-              file=sys.stderr)
+        print("bench.py measures one MI355X (use --gpus 1): environments shard across "
+              "GPUs with no exchange, so an N-GPU run is N independent runs of E/N envs "
+              "each (bench.py --envs E/N).", file=sys.stderr)
         sys.exit(2)
 
     if args.workload != "home":
