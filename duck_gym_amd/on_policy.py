@@ -315,42 +315,48 @@ class PPO:
         elif 0.0 < kl_mean < low:
             self.learning_rate = min(1e-2, lr * 1.5)
 
-    def update(self):
+    def _mini_batch(self, batch, sums):
+        """One mini-batch: losses, KL-adaptive rate, backward, clipped Adam
+        step; adds (value loss, surrogate, entropy) to `sums`."""
         p = self.policy
+        (obs, critic_obs, actions, target_values, advantages, returns, old_log_prob, old_mu,
+         old_sigma) = batch
+        if self.normalize_advantage_per_mini_batch:
+            with torch.no_grad():
+                advantages = (advantages - advantages.mean()) / (advantages.std() + 1e-8)
+        p.update_distribution(obs)
+        log_prob = p.get_actions_log_prob(actions)
+        values = p.evaluate(critic_obs)
+        mu, sigma, entropy = p.action_mean, p.action_std, p.entropy
+        if self.desired_kl is not None and self.schedule == "adaptive":
+            with torch.no_grad():
+                self._adapt_learning_rate(self.kl(old_mu, old_sigma, mu, sigma).mean())
+        ratio = torch.exp(log_prob - old_log_prob.squeeze(-1))
+        adv = advantages.squeeze(-1)
+        surrogate = torch.max(-adv * ratio, -adv * ratio.clamp(1.0 - self.clip_param,
+                                                               1.0 + self.clip_param)).mean()
+        if self.use_clipped_value_loss:
+            clipped = target_values + (values - target_values).clamp(-self.clip_param,
+                                                                     self.clip_param)
+            value_loss = torch.max((values - returns).square(),
+                                   (clipped - returns).square()).mean()
+        else:
+            value_loss = (returns - values).square().mean()
+        loss = surrogate + self.value_loss_coef * value_loss - self.entropy_coef * entropy.mean()
+        self.optimizer.zero_grad()
+        loss.backward()
+        nn.utils.clip_grad_norm_(p.parameters(), self.max_grad_norm)
+        self.optimizer.step()
+        with torch.no_grad():
+            sums += torch.stack((value_loss.detach(), surrogate.detach(),
+                                 entropy.mean().detach()))
+
+    def update(self):
         # loss sums stay on the device until the update ends
         sums = torch.zeros(3, device=self.device)
         n = 0
-        for (obs, critic_obs, actions, target_values, advantages, returns, old_log_prob,
-             old_mu, old_sigma) in self.storage.mini_batches(self.num_mini_batches,
-                                                             self.num_learning_epochs):
-            if self.normalize_advantage_per_mini_batch:
-                with torch.no_grad():
-                    advantages = (advantages - advantages.mean()) / (advantages.std() + 1e-8)
-            p.act(obs)
-            log_prob = p.get_actions_log_prob(actions)
-            values = p.evaluate(critic_obs)
-            mu, sigma, entropy = p.action_mean, p.action_std, p.entropy
-            if self.desired_kl is not None and self.schedule == "adaptive":
-                with torch.no_grad():
-                    self._adapt_learning_rate(self.kl(old_mu, old_sigma, mu, sigma).mean())
-            ratio = torch.exp(log_prob - old_log_prob.squeeze(-1))
-            adv = advantages.squeeze(-1)
-            surrogate = torch.max(-adv * ratio, -adv * ratio.clamp(1.0 - self.clip_param,
-                                                                   1.0 + self.clip_param)).mean()
-            if self.use_clipped_value_loss:
-                clipped = target_values + (values - target_values).clamp(-self.clip_param,
-                                                                         self.clip_param)
-                value_loss = torch.max((values - returns).square(),
-                                       (clipped - returns).square()).mean()
-            else:
-                value_loss = (returns - values).square().mean()
-            loss = surrogate + self.value_loss_coef * value_loss - self.entropy_coef * entropy.mean()
-            self.optimizer.zero_grad()
-            loss.backward()
-            nn.utils.clip_grad_norm_(p.parameters(), self.max_grad_norm)
-            self.optimizer.step()
-            sums += torch.stack((value_loss.detach(), surrogate.detach(),
-                                 entropy.mean().detach()))
+        for batch in self.storage.mini_batches(self.num_mini_batches, self.num_learning_epochs):
+            self._mini_batch(batch, sums)
             n += 1
         self.storage.clear()
         value, surrogate, entropy = (sums / n).tolist()
