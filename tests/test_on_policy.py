@@ -264,3 +264,40 @@ def test_runner_rejects_unknown_configuration():
     with pytest.raises(ValueError):
         OnPolicyRunner(env, {**STANDING, "algorithm": {**STANDING["algorithm"], "lr": 1.0}},
                        device="cpu")
+
+
+class _WithCritic(_LinearTarget):
+    """The same problem with a 6-wide privileged critic observation."""
+
+    def _critic(self):
+        return torch.cat((self.obs, self.obs[:, :2] * 2), -1)
+
+    def get_observations(self):
+        return self.obs.clone(), {"observations": {"critic": self._critic()}}
+
+    def step(self, actions):
+        obs, reward, timeout, info = super().step(actions)
+        info["observations"]["critic"] = self._critic()
+        return obs, reward, timeout, info
+
+
+def test_runner_critic_observations_and_random_episode_start():
+    torch.manual_seed(1)
+    env = _WithCritic(32)
+    runner = OnPolicyRunner(env, {**STANDING, "num_steps_per_env": 8}, device="cpu")
+    assert runner.alg.policy.critic[0].in_features == 6
+    assert runner.alg.policy.actor[0].in_features == 4
+    assert runner.alg.storage.critic_observations.shape == (8, 32, 6)
+    runner.learn(2, init_at_random_ep_len=True)
+    # both normalisers saw every control step: the critic's its own 6 columns
+    assert int(runner.obs_normalizer.count) == 32 * 8 * 2
+    assert int(runner.critic_obs_normalizer.count) == 32 * 8 * 2
+    assert runner.critic_obs_normalizer._mean.shape == (1, 6)
+    assert runner.current_learning_iteration == 1
+    starts = OnPolicyRunner(_WithCritic(256), {**STANDING, "num_steps_per_env": 1},
+                            device="cpu")
+    starts.env.episode_length_buf.zero_()
+    starts.learn(1, init_at_random_ep_len=True)
+    lengths = starts.env.episode_length_buf
+    assert int(lengths.min()) >= 0 and int(lengths.max()) < 8
+    assert len(set(lengths.tolist())) > 4
