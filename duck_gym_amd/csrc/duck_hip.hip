@@ -30,6 +30,13 @@ void require(bool ok, const std::string &message) {
     throw DuckError(DUCK_ERR_ARGUMENT, message);
 }
 
+// Clears `words` 32-bit words (a fill kernel rather than hipMemset, so that
+// the sequence stays capturable).
+__global__ void zeroWordsKernel(unsigned *p, long long words) {
+  for (long long i = blockIdx.x * 64ll + threadIdx.x; i < words; i += 64ll * gridDim.x)
+    p[i] = 0;
+}
+
 // Makes `device` current for the lifetime of the guard.
 struct DeviceGuard {
   int previous = -1;
@@ -341,33 +348,48 @@ public:
     launched("generalizedLoadsKernel");
     record(s);
   }
+  // Reals of duck_reference's device inputs and outputs: target, force,
+  // bodies, joints, diag.
+  size_t referenceIoCount() const {
+    const int nb = host.bodies.size(), nj = host.joints.size();
+    return size_t(nj) + 3 + size_t(nb) * 13 + size_t(nj) * 2 + 6;
+  }
+  // One environment from the model file's state (extension.cu:385-415) in
+  // `state` (blobBytes of device memory) with its inputs and outputs in `io`
+  // (referenceIoCount() device reals); synchronous, on the null stream.
+  void referenceIn(unsigned char *state, R *io, const void *target, const void *force,
+                   int substeps, double kp, double limit, void *bodies, void *joints, void *diag) {
+    require(target && force && bodies && joints && diag && substeps > 0,
+            "Invalid CPU reference inputs");
+    const int nb = host.bodies.size(), nj = host.joints.size();
+    R *dTarget = io, *dForce = io + nj, *dB = dForce + 3, *dJ = dB + nb * 13, *dD = dJ + nj * 2;
+    hipCheck(hipMemcpy(dTarget, target, nj * sizeof(R), hipMemcpyHostToDevice), "upload");
+    hipCheck(hipMemcpy(dForce, force, 3 * sizeof(R), hipMemcpyHostToDevice), "upload");
+    zeroWordsKernel<<<(blobBytes / 4 + 63) / 64, 64, 0, 0>>>(reinterpret_cast<unsigned *>(state),
+                                                             blobBytes / 4);
+    launched("zeroWordsKernel");
+    initializeKernel<R, B, J, CG, CS><<<1, 64, 0, 0>>>(dModel, state, blobBytes, 1);
+    launched("initializeKernel");
+    // extension.cu:403-410 sets force, kp, limit and target only; the
+    // model's torque/friction/damping are already in place.
+    advance(state, 1, dTarget, dForce, nullptr, substeps, kp, limit, 0);
+    snapshotKernel<R, B, J, CG, CS><<<1, 64, 0, 0>>>(dModel, state, blobBytes, 1, dB, dJ, dD);
+    launched("snapshotKernel");
+    hipCheck(hipMemcpy(bodies, dB, nb * 13 * sizeof(R), hipMemcpyDeviceToHost), "download");
+    hipCheck(hipMemcpy(joints, dJ, nj * 2 * sizeof(R), hipMemcpyDeviceToHost), "download");
+    hipCheck(hipMemcpy(diag, dD, 6 * sizeof(R), hipMemcpyDeviceToHost), "download");
+  }
   void reference(const void *target, const void *force, int substeps, double kp, double limit,
                  void *bodies, void *joints, void *diag) override {
     DeviceGuard guard(device);
     require(target && force && bodies && joints && diag && substeps > 0,
             "Invalid CPU reference inputs");
-    const int nb = host.bodies.size(), nj = host.joints.size();
     unsigned char *state = nullptr;
     R *buf = nullptr;
-    const size_t nbuf = nj + 3 + nb * 13 + nj * 2 + 6;
     try {
       hipCheck(hipMalloc(&state, blobBytes), "hipMalloc(reference state)");
-      hipCheck(hipMalloc(&buf, nbuf * sizeof(R)), "hipMalloc(reference io)");
-      R *dTarget = buf, *dForce = buf + nj, *dB = dForce + 3, *dJ = dB + nb * 13,
-        *dD = dJ + nj * 2;
-      hipCheck(hipMemcpy(dTarget, target, nj * sizeof(R), hipMemcpyHostToDevice), "upload");
-      hipCheck(hipMemcpy(dForce, force, 3 * sizeof(R), hipMemcpyHostToDevice), "upload");
-      hipCheck(hipMemset(state, 0, blobBytes), "hipMemset");
-      initializeKernel<R, B, J, CG, CS><<<1, 64, 0, 0>>>(dModel, state, blobBytes, 1);
-      launched("initializeKernel");
-      // extension.cu:403-410 sets force, kp, limit and target only; the
-      // model's torque/friction/damping are already in place.
-      advance(state, 1, dTarget, dForce, nullptr, substeps, kp, limit, 0);
-      snapshotKernel<R, B, J, CG, CS><<<1, 64, 0, 0>>>(dModel, state, blobBytes, 1, dB, dJ, dD);
-      launched("snapshotKernel");
-      hipCheck(hipMemcpy(bodies, dB, nb * 13 * sizeof(R), hipMemcpyDeviceToHost), "download");
-      hipCheck(hipMemcpy(joints, dJ, nj * 2 * sizeof(R), hipMemcpyDeviceToHost), "download");
-      hipCheck(hipMemcpy(diag, dD, 6 * sizeof(R), hipMemcpyDeviceToHost), "download");
+      hipCheck(hipMalloc(&buf, referenceIoCount() * sizeof(R)), "hipMalloc(reference io)");
+      referenceIn(state, buf, target, force, substeps, kp, limit, bodies, joints, diag);
     } catch (...) {
       if (state)
         (void)hipFree(state);
@@ -477,6 +499,30 @@ BatchBase *makeBatch(HostModel &&m, int n, double dt, int iterations, int device
   return new Batch<R, 32, 32, 64, 32, 32>(std::move(m), n, dt, iterations, device);
 }
 
+// The model checks of the selected backend after loadModel's flattening
+// checks: the specialized state's capacities (model.hpp:30-40 with
+// MicroDuckState<16, 14, 64>, kernel.cuh:1098; std::invalid_argument, a
+// ValueError in Python), then its exact layout (extension.cu:225-236;
+// TORCH_CHECK, a RuntimeError).  The generic state's capacities (32 bodies
+// and joints, pairs + 4 per ground shape <= 160) follow from loadModel's
+// 32-body/joint/shape/pair limit.
+void checkBackend(const HostModel &m, unsigned flags) {
+  if (!(flags & DUCK_FLAG_SPECIALIZED))
+    return;
+  if (m.bodies.size() > 16 || m.joints.size() > 14)
+    throw std::invalid_argument("Model exceeds selected state body/joint capacity");
+  if (m.groundCapacity + m.selfCapacity > 64)
+    throw std::invalid_argument("Model exceeds selected state contact capacity");
+  require(m.bodies.size() == 16 && m.joints.size() == 14,
+          "MicroDuck specialized backend requires 16 bodies and 14 hinges");
+  for (int i = 0; i < 14; ++i) {
+    std::string label = m.joints[i].name;
+    if (label.rfind("robot/", 0) == 0)
+      label = label.substr(6);
+    require(label == kMicroDuckJoints[i], "Unsupported MicroDuck joint layout");
+  }
+}
+
 template <class F> int guarded(F &&f) {
   try {
     f();
@@ -510,11 +556,28 @@ extern "C" {
 
 const char *duck_last_error(void) { return g_lastError.c_str(); }
 
+int duck_model_info(const char *model_path, unsigned flags, int *out) {
+  return guarded([&] {
+    require(model_path != nullptr && out != nullptr, "null argument");
+    require(!(flags & DUCK_FLAG_SHARED_MEMORY) || (flags & DUCK_FLAG_SPECIALIZED),
+            "Shared memory requires the compact MicroDuck backend");
+    HostModel m = loadModel(model_path);
+    checkBackend(m, flags);
+    const int v[] = {int(m.bodies.size()), int(m.joints.size()), int(m.shapes.size()),
+                     int(m.pairs.size()), m.groundCapacity, m.selfCapacity};
+    for (int i = 0; i < 6; ++i)
+      out[i] = v[i];
+  });
+}
+
 int duck_create(const char *model_path, int num_envs, double dt, int iterations, int device,
                 int fp_bits, unsigned flags, void **out_handle) {
   return guarded([&] {
     require(out_handle != nullptr && model_path != nullptr, "null argument");
     *out_handle = nullptr;
+    // extension.cu:424 checks the shared-memory option before anything else
+    require(!(flags & DUCK_FLAG_SHARED_MEMORY) || (flags & DUCK_FLAG_SPECIALIZED),
+            "Shared memory requires the compact MicroDuck backend");
     require(num_envs > 0 && num_envs <= 65536 && dt > 0 && std::isfinite(dt) && iterations > 0,
             "Invalid batch parameters");
     require(fp_bits == 32 || fp_bits == 64, "fp_bits must be 32 or 64");
@@ -522,16 +585,7 @@ int duck_create(const char *model_path, int num_envs, double dt, int iterations,
     hipCheck(hipGetDeviceCount(&devices), "hipGetDeviceCount");
     require(device >= 0 && device < devices, "Invalid device index");
     HostModel m = loadModel(model_path);
-    if (flags & DUCK_FLAG_SPECIALIZED) {
-      require(m.bodies.size() == 16 && m.joints.size() == 14,
-              "MicroDuck specialized backend requires 16 bodies and 14 hinges");
-      for (int i = 0; i < 14; ++i) {
-        std::string label = m.joints[i].name;
-        if (label.rfind("robot/", 0) == 0)
-          label = label.substr(6);
-        require(label == kMicroDuckJoints[i], "Unsupported MicroDuck joint layout");
-      }
-    }
+    checkBackend(m, flags);
     const bool split = flags & DUCK_FLAG_SPLIT;
     BatchBase *b =
         fp_bits == 64 ? makeBatch<double>(std::move(m), num_envs, dt, iterations, device, split)

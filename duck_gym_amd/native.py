@@ -34,6 +34,7 @@ def library():
         sig = {
             "duck_create": (ip, [cp, ip, dbl, ip, ip, ip, ctypes.c_uint, ctypes.POINTER(vp)]),
             "duck_destroy": (None, [vp]),
+            "duck_model_info": (ip, [cp, ctypes.c_uint, ctypes.POINTER(ip)]),
             "duck_dims": (ip, [vp, ctypes.POINTER(ip), ctypes.POINTER(ip), ctypes.POINTER(ip)]),
             "duck_num_envs": (ip, [vp]),
             "duck_fp_bits": (ip, [vp]),
@@ -67,10 +68,11 @@ def library():
 
 
 EXPORTED = (
-    "duck_create", "duck_destroy", "duck_dims", "duck_num_envs", "duck_fp_bits",
+    "duck_create", "duck_destroy", "duck_model_info", "duck_dims", "duck_num_envs", "duck_fp_bits",
     "duck_state_bytes", "duck_joint_name", "duck_reset", "duck_step", "duck_step_motor",
     "duck_state", "duck_contact_forces", "duck_self_contact_stats", "duck_contact_counts",
-    "duck_generalized_loads", "duck_reference", "duck_state_layout", "duck_export_state",
+    "duck_generalized_loads", "duck_reference", "duck_state_layout",
+    "duck_export_state",
     "duck_import_state", "duck_last_error", "duck_task_obs_dim", "duck_task_targets",
     "duck_task_step", "duck_task_observe", "duck_servo",
 )
@@ -118,12 +120,32 @@ def _raise(code, what):
     raise RuntimeError(f"{what}: {msg}")
 
 
+def _flags(specialized, shared_memory, split_solve=False):
+    return (1 if specialized else 0) | (2 if split_solve else 0) | (4 if shared_memory else 0)
+
+
+def check_model(model, specialized=False, shared_memory=False):
+    """Parse and validate a `.duck` model as CudaBatch(model, ...) does,
+    without a device (duck_model_info): returns the counts, or raises the
+    exception the constructor would (RuntimeError for an unreadable or
+    malformed file and for the specialized layout checks, ValueError for a
+    flattening or capacity violation)."""
+    out = (ctypes.c_int * 6)()
+    code = library().duck_model_info(str(model).encode(),
+                                     _flags(specialized, shared_memory), out)
+    if code:
+        _raise(code, "CudaBatch")
+    keys = ("bodies", "joints", "shapes", "pairs", "ground_capacity", "self_capacity")
+    return dict(zip(keys, list(out)))
+
+
 class CudaBatch:
     """Batched AVBD environments on one MI355X (gfx950) device."""
 
     def __init__(self, model, num_envs, dt=0.001, iterations=200, device=0, fp64=False,
                  specialized=False, shared_memory=False, split_solve=False):
-        # `shared_memory` is accepted for signature compatibility: the gfx950
+        # `shared_memory` (with `specialized` only, as extension.cu:424
+        # requires) is accepted for signature compatibility: the gfx950
         # kernel always stages environment state in LDS.  `split_solve` (an
         # extension) runs float64 batches in the float layout: two lanes per
         # body block solve, whose partial systems are summed in another order.
@@ -132,7 +154,7 @@ class CudaBatch:
         handle = ctypes.c_void_p()
         code = lib.duck_create(str(model).encode(), int(num_envs), float(dt), int(iterations),
                                int(device), 64 if fp64 else 32,
-                               (1 if specialized else 0) | (2 if split_solve else 0),
+                               _flags(specialized, shared_memory, split_solve),
                                ctypes.byref(handle))
         if code:
             _raise(code, "CudaBatch")

@@ -33,12 +33,25 @@ enum {
 #define DUCK_FLAG_SPECIALIZED 1u /* require the MicroDuck 16-body/14-hinge layout */
 #define DUCK_FLAG_SPLIT 2u       /* float64: use the float layout (two lanes per body
                                     block solve) instead of one lane per solve */
+#define DUCK_FLAG_SHARED_MEMORY 4u /* CudaBatch(shared_memory=True): accepted with
+                                      DUCK_FLAG_SPECIALIZED only (extension.cu:424); the
+                                      state is always staged in LDS */
 
 /* CudaBatch(model, num_envs, dt, iterations, device, fp64, specialized)
  * (extension.cu:216-265, 423-441).  num_envs in [1, 65536]. */
 int duck_create(const char *model_path, int num_envs, double dt, int iterations, int device,
                 int fp_bits, unsigned flags, void **out_handle);
 void duck_destroy(void *handle);
+
+/* Parse and validate a `.duck` model file without a device: the checks of
+ * duck_create (Solver::load, solver.cpp:67-174; the flattening checks of
+ * convert, model.hpp:20-91; the backend checks of makeBatch and the Batch
+ * constructor, extension.cu:216-236, 423-435, for `flags`).  out[6] = bodies,
+ * joints, shapes, body-contact pairs, ground-contact capacity, body-contact
+ * capacity.  Errors as duck_create: DUCK_ERR_RUNTIME for an unreadable or
+ * malformed file, DUCK_ERR_MODEL for a flattening or capacity violation,
+ * DUCK_ERR_ARGUMENT for the backend's layout checks. */
+int duck_model_info(const char *model_path, unsigned flags, int *out);
 
 /* Bodies (including the static world body 0), hinges and contact capacity. */
 int duck_dims(void *handle, int *bodies, int *joints, int *contact_capacity);

@@ -46,7 +46,33 @@ def test_invalid_inputs_raise(models, home):
         CudaBatch(models["standing"], 0, DT, ITER)
     with pytest.raises(RuntimeError):
         CudaBatch(str(models["standing"]) + ".missing", 4, DT, ITER)
+    # extension.cu:424
+    with pytest.raises(RuntimeError, match="Shared memory requires the compact MicroDuck backend"):
+        CudaBatch(models["standing"], 4, DT, ITER, 0, False, False, True)
+    CudaBatch(models["standing"], 4, DT, ITER, 0, False, True, True)
     assert b.joint_names[0] == "left_hip_yaw" and len(b.joint_names) == 14
+
+
+def test_model_file_errors_raise_as_the_reference(tmp_path, models):
+    """Every malformed file (RuntimeError) and model-contract violation
+    (ValueError) of tests/test_model_errors.py, through the constructor on
+    the device, and the specialized backend's checks."""
+    from model_text import chain
+    from test_model_errors import RUNTIME, VALUE
+
+    path = tmp_path / "m.duck"
+    for cases, error in ((RUNTIME, RuntimeError), ([c for c in VALUE if c[1]], ValueError)):
+        for name, text, message in cases:
+            path.write_text(text)
+            with pytest.raises(error) as caught:
+                CudaBatch(path, 4, DT, ITER)
+            assert message in str(caught.value), name
+    path.write_text(chain(bodies=17))
+    with pytest.raises(ValueError, match="body/joint capacity"):
+        CudaBatch(path, 4, DT, ITER, 0, False, True)
+    path.write_text(chain(bodies=10))
+    with pytest.raises(RuntimeError, match="requires 16 bodies and 14 hinges"):
+        CudaBatch(path, 4, DT, ITER, 0, True, True)
 
 
 def test_nan_isolation_and_reset_recovery(models, home):
