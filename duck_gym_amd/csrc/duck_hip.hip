@@ -7,9 +7,18 @@
 
 #include <cstring>
 #include <memory>
+#include <mutex>
 #include <stdexcept>
 #include <string>
 #include <vector>
+
+// Device scratch of duck_reference_noalloc: one environment's state blob
+// followed by its inputs and outputs.  Every device that runs this library
+// holds its own copy for the life of the process; host code uses the address
+// hipGetSymbolAddress returns for the current device (referenceScratch), never
+// this name, which on the host is a stand-in and no device address.
+constexpr size_t kReferenceScratchBytes = 64 * 1024;
+static __device__ __align__(256) unsigned char scratch[kReferenceScratchBytes];
 
 namespace duckhip {
 namespace {
@@ -28,6 +37,22 @@ void hipCheck(hipError_t err, const char *what) {
 void require(bool ok, const std::string &message) {
   if (!ok)
     throw DuckError(DUCK_ERR_ARGUMENT, message);
+}
+
+// The device address of `scratch` on the current device `device`, looked up
+// once per device (at the first batch created there) and kept.
+void *referenceScratch(int device) {
+  static std::mutex guard;
+  static std::vector<void *> address;
+  std::lock_guard<std::mutex> lock(guard);
+  if (device >= int(address.size()))
+    address.resize(device + 1, nullptr);
+  if (!address[device]) {
+    void *p = nullptr;
+    hipCheck(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+    address[device] = p;
+  }
+  return address[device];
 }
 
 // Clears `words` 32-bit words (a fill kernel rather than hipMemset, so that
@@ -181,6 +206,8 @@ struct BatchBase {
   virtual void generalizedLoads(const void *, void *, hipStream_t) = 0;
   virtual void reference(const void *, const void *, int, double, double, void *, void *,
                          void *) = 0;
+  virtual void referenceNoAlloc(const void *, const void *, int, double, double, void *, void *,
+                                void *) = 0;
   virtual void layout(long long *out) const = 0;
   virtual void exportState(void *, hipStream_t) = 0;
   virtual void importState(const void *, hipStream_t) = 0;
@@ -197,6 +224,7 @@ template <class R, int B, int J, int CG, int CS, int L> class Batch final : publ
   V3<R> *dPoints = nullptr;
   unsigned char *dStates = nullptr;
   hipEvent_t ready = nullptr;
+  void *dScratch = nullptr; // this device's `scratch`
 
   void wait(hipStream_t s) { hipCheck(hipStreamWaitEvent(s, ready, 0), "hipStreamWaitEvent"); }
   void record(hipStream_t s) { hipCheck(hipEventRecord(ready, s), "hipEventRecord"); }
@@ -241,6 +269,7 @@ public:
       launched("initializeKernel");
       hipCheck(hipDeviceSynchronize(), "initialize");
       hipCheck(hipEventCreateWithFlags(&ready, hipEventDisableTiming), "hipEventCreate");
+      dScratch = referenceScratch(device);
       record(0);
     } catch (...) {
       release();
@@ -399,6 +428,21 @@ public:
     }
     hipCheck(hipFree(state), "hipFree");
     hipCheck(hipFree(buf), "hipFree");
+  }
+  // duck_reference with the blob and the inputs/outputs in this device's
+  // `scratch` (blob first, 256-byte aligned, then the reals): no allocation.
+  void referenceNoAlloc(const void *target, const void *force, int substeps, double kp,
+                        double limit, void *bodies, void *joints, void *diag) override {
+    DeviceGuard guard(device);
+    const size_t need = size_t(blobBytes) + referenceIoCount() * sizeof(R);
+    if (need > kReferenceScratchBytes)
+      throw DuckError(DUCK_ERR_ARGUMENT,
+                      "reference scratch: this model needs " + std::to_string(need) +
+                          " bytes of the library's " + std::to_string(kReferenceScratchBytes));
+    require(dScratch != nullptr, "reference scratch: no device address");
+    unsigned char *base = static_cast<unsigned char *>(dScratch);
+    referenceIn(base, reinterpret_cast<R *>(base + blobBytes), target, force, substeps, kp, limit,
+                bodies, joints, diag);
   }
   void taskTargets(const DuckTask &t, const void *actions, const void *reference, void *clamped,
                    void *target, hipStream_t s) override {
@@ -744,5 +788,11 @@ int duck_reference(void *handle, const void *target, const void *force, int subs
                    double limit, void *bodies, void *joints, void *diag) {
   return guarded(
       [&] { as(handle)->reference(target, force, substeps, kp, limit, bodies, joints, diag); });
+}
+int duck_reference_noalloc(void *handle, const void *target, const void *force, int substeps,
+                           double kp, double limit, void *bodies, void *joints, void *diag) {
+  return guarded([&] {
+    as(handle)->referenceNoAlloc(target, force, substeps, kp, limit, bodies, joints, diag);
+  });
 }
 }

@@ -49,6 +49,7 @@ def library():
             "duck_contact_counts": (ip, [vp, vp, vp]),
             "duck_generalized_loads": (ip, [vp, vp, vp, vp]),
             "duck_reference": (ip, [vp, vp, vp, ip, dbl, dbl, vp, vp, vp]),
+            "duck_reference_noalloc": (ip, [vp, vp, vp, ip, dbl, dbl, vp, vp, vp]),
             "duck_state_layout": (ip, [vp, ctypes.POINTER(ctypes.c_longlong)]),
             "duck_export_state": (ip, [vp, vp, vp]),
             "duck_import_state": (ip, [vp, vp, vp]),
@@ -71,7 +72,7 @@ EXPORTED = (
     "duck_create", "duck_destroy", "duck_model_info", "duck_dims", "duck_num_envs", "duck_fp_bits",
     "duck_state_bytes", "duck_joint_name", "duck_reset", "duck_step", "duck_step_motor",
     "duck_state", "duck_contact_forces", "duck_self_contact_stats", "duck_contact_counts",
-    "duck_generalized_loads", "duck_reference", "duck_state_layout",
+    "duck_generalized_loads", "duck_reference", "duck_reference_noalloc", "duck_state_layout",
     "duck_export_state",
     "duck_import_state", "duck_last_error", "duck_task_obs_dim", "duck_task_targets",
     "duck_task_step", "duck_task_observe", "duck_servo",

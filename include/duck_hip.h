@@ -99,6 +99,18 @@ int duck_generalized_loads(void *handle, const void *offset, void *out, void *hi
 int duck_reference(void *handle, const void *target, const void *force, int substeps, double kp,
                    double limit, void *bodies, void *joints, void *diag);
 
+/* duck_reference without any allocation.  No counterpart in the reference:
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, serving loops, harnesses that forbid hipMalloc).  The state blob
+ * and the device copies of the inputs and outputs live in the library's
+ * static device scratch, 64 KiB per device (held until the process ends);
+ * a model whose blob plus 6 + 3 J + 13 B reals exceeds it is rejected with
+ * DUCK_ERR_ARGUMENT.  Results are those of duck_reference.  The scratch is
+ * shared by every call on a device and keeps the last call's contents:
+ * calls that overlap on one device (from several host threads) race. */
+int duck_reference_noalloc(void *handle, const void *target, const void *force, int substeps,
+                           double kp, double limit, void *bodies, void *joints, void *diag);
+
 /* Size in bytes of one environment's HBM state blob. */
 long long duck_state_bytes(void *handle);
 
