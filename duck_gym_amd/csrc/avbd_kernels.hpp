@@ -387,7 +387,7 @@ template <class R> DUCK_HD MprHit<R> mprContact(const MprQuery<R> &Qy, R toleran
 }
 
 // Per-launch kernel: controls, `substeps` physics steps, write-back.
-template <class R, int B, int J, int CG, int CS, int L>
+template <class R, int B, int J, int CG, int CS, int L, int PL = defaultSolveLanes(L)>
 __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
   constexpr int G = 64 / L;
   constexpr int PPL = (CS + L - 1) / L; // pairs per lane (pairs <= CS)
@@ -566,10 +566,10 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
   }
   __syncthreads();
 
-  Stepper<R, B, J, CG, CS, L> stp{M, points, F, E, lane};
+  Stepper<R, B, J, CG, CS, L, PL> stp{M, points, F, E, lane};
   // Block-solve lanes: with P == 2, lanes l and l ^ 8 (same 16-lane DPP row)
   // share a body; `slot` numbers the bodies a colour pass runs at once.
-  constexpr int P = Stepper<R, B, J, CG, CS, L>::P;
+  constexpr int P = Stepper<R, B, J, CG, CS, L, PL>::P;
   static_assert(P == 1 || L % (8 * P) == 0, "split block solves need 8 P-lane groups");
   const int part = (lane >> 3) & (P - 1);
   const int slot = P == 1 ? lane : (lane & 7) + 8 * (lane / (8 * P));
@@ -1021,17 +1021,20 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
           for (int k = 0; k < 6; ++k)
             E.Iw[k][b] = iw[k];
         }
-        uint64_t gm = 0;
+        constexpr int GW = (CG + 63) / 64;
+        uint64_t gm[GW] = {};
         for (int i = 0; i < E.s.ngc; ++i)
           if (gcBody(E.s.gc[i].id) == b)
-            gm |= uint64_t(1) << i;
+            gm[i >> 6] |= uint64_t(1) << (i & 63);
         uint32_t sm = 0;
         for (int i = 0; i < E.s.nsc; ++i) {
           int id = E.s.sc[i].id;
           if (scBody(id) == b || scOther(id) == b)
             sm |= 1u << i;
         }
-        E.gmask[b] = gm;
+#pragma unroll
+        for (int k = 0; k < GW; ++k)
+          E.gmask[k][b] = gm[k];
         E.smask[b] = sm;
         const R mass = E.s.mass[b];
         if (mass == 0)
@@ -1081,7 +1084,7 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
           for (int k = 0; k < n; ++k) {
             const int b = E.order[cs + k];
             const int hinges = F.adjStart[b + 1] - F.adjStart[b];
-            const int ground = __popcll(E.gmask[b]);
+            const int ground = stp.groundCount(b);
             const int units = hinges > ground ? hinges : ground;
             if (units > bestUnits) {
               bestUnits = units;
@@ -1112,7 +1115,7 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
       }
     }
     // The lane's assembly plans for its bodies of the first two colours.
-    typename Stepper<R, B, J, CG, CS, L>::SlotPlan plans[2] = {{0, 0}, {0, 0}};
+    typename Stepper<R, B, J, CG, CS, L, PL>::SlotPlan plans[2] = {{0, 0}, {0, 0}};
     if constexpr (sizeof(R) == sizeof(float)) {
 #pragma unroll
       for (int c = 0; c < 2; ++c)
@@ -1136,12 +1139,16 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
     // The ends of that hinge and the owner of the lane's first ground
     // contact (the list is fixed until the next detection).
     const int ends0 = dualJoint >= 0 ? F.a[dualJoint] | F.b[dualJoint] << 8 : F.a[0] | F.b[0] << 8;
-    typename Stepper<R, B, J, CG, CS, L>::JointEval lastEval{};
+    typename Stepper<R, B, J, CG, CS, L, PL>::JointEval lastEval{};
     int owner0 = 0;
     if (active && lane < E.s.ngc) {
       const int id = E.s.gc[lane].id;
       owner0 = gcBody(id) | gcShape(id) << 8;
     }
+    // Contact rounds of the dual update for the whole wave (scalars; the
+    // lists are fixed until the next detection).
+    const int groundRounds = __builtin_amdgcn_readfirstlane(waveMaxInt(active ? E.s.ngc : 0));
+    const int selfRounds = __builtin_amdgcn_readfirstlane(waveMaxInt(active ? E.s.nsc : 0));
     // ---------------- AVBD iterations (kernel.cuh:979-1063) ---------------
     bool dualRan = false;
     R dJoint = 0, dAxis = 0, dDepth = 0;
@@ -1192,7 +1199,7 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
         R errC0 = 0;
         dualRan = true;
         dJoint = dAxis = dDepth = 0;
-        auto foldJoint = [&](const typename Stepper<R, B, J, CG, CS, L>::JointDual &jd) {
+        auto foldJoint = [&](const typename Stepper<R, B, J, CG, CS, L, PL>::JointDual &jd) {
 #pragma unroll
           for (int k = 0; k < 3; ++k)
             dJoint = mx(dJoint, mabs(jd.C[k]));
@@ -1229,29 +1236,44 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
           error = mx(error, errC0);
           dDepth = mx(dDepth, g0.depth);
         }
-        for (int i = lane + L; i < ngc; i += L) {
-          const int id = E.s.gc[i].id;
-          const auto gd = stp.groundDual(i, true, error, gcBody(id) | gcShape(id) << 8);
-          stp.storeGroundDual(i, gd);
-          dDepth = mx(dDepth, gd.depth);
+        // Further ground contacts and the body contacts run in rounds counted
+        // for the whole wave (scalar trip counts, predicated bodies): a loop
+        // that lanes leave at different trips ends in a block entered with
+        // exec zero, and this compiler has placed the copy of a loop-carried
+        // maximum there, before exec is restored, losing it.  A lane with no
+        // contact in a round rewrites its own first slot with its values.
+        for (int i0 = L; i0 < groundRounds; i0 += L) {
+          const int i = i0 + lane;
+          const bool v = i < ngc;
+          const int k = v ? i : lane;
+          const int id = E.s.gc[k].id;
+          const auto gd = stp.groundDual(k, v, error, v ? gcBody(id) | gcShape(id) << 8 : owner0);
+          stp.storeGroundDual(k, gd);
+          dDepth = v ? mx(dDepth, gd.depth) : dDepth;
         }
-        for (int i = lane; i < E.s.nsc; i += L) {
-          SelfContact<R> &c = E.s.sc[i];
+        const int nsc = E.s.nsc;
+        for (int i0 = 0; i0 < selfRounds; i0 += L) {
+          const int i = i0 + lane;
+          const bool v = i < nsc;
+          SelfContact<R> &c = E.s.sc[v ? i : 0];
           V3<R> ra, rb;
           V3<R> C = stp.selfC(c, ra, rb);
-          dDepth = mx(dDepth, mx(R(0), -(C.z + alpha * c.c0)));
+          const R depth = mx(R(0), -(C.z + alpha * c.c0));
           V3<R> f = contactForce(C, c.lambda, c.penalty, c.friction);
           R trial = fhypot(fmad(c.penalty[0], C.x, c.lambda[0]), fmad(c.penalty[1], C.y, c.lambda[1]));
           bool stick = trial <= -c.friction * f.z && double(fhypot(C.x, C.y)) < 1e-5;
-          c.id = (c.id & 0x7fffffff) | (stick ? int(0x80000000u) : 0);
           R fk[3] = {f.x, f.y, f.z}, Ck[3] = {C.x, C.y, C.z};
+          if (v) {
+            c.id = (c.id & 0x7fffffff) | (stick ? int(0x80000000u) : 0);
 #pragma unroll
-          for (int k = 0; k < 3; ++k) {
-            c.lambda[k] = fk[k];
-            if (f.z < 0 && (k == 2 || trial <= -c.friction * f.z))
-              c.penalty[k] = mn(fmad(M.betaLinear, mabs(Ck[k]), c.penalty[k]), R(1e9));
+            for (int k = 0; k < 3; ++k) {
+              c.lambda[k] = fk[k];
+              if (f.z < 0 && (k == 2 || trial <= -c.friction * f.z))
+                c.penalty[k] = mn(fmad(M.betaLinear, mabs(Ck[k]), c.penalty[k]), R(1e9));
+            }
           }
-          error = mx(error, mx(R(0), -C.z));
+          dDepth = v ? mx(dDepth, depth) : dDepth;
+          error = v ? mx(error, mx(R(0), -C.z)) : error;
         }
       }
       error = groupMax<L>(error);

@@ -146,7 +146,9 @@ template <class R, int B, int J, int CG, int CS> struct alignas(16) EnvLds {
   R Iw[6][B]; // world inertia at q0 (xx yy zz xy xz yz)
   R c0[7][J], angle0[J], velocity0[J];
   R stepDiag[8];
-  uint64_t gmask[B];
+  // per body: bit i of word i / 64 = ground contact i belongs to the body;
+  // bit i = body-body contact i involves it
+  uint64_t gmask[(CG + 63) / 64][B];
   uint32_t smask[B];
   int order[B], colorStart[CS + 3];
   int done, pad0, pad1, pad2;

@@ -329,7 +329,12 @@ template <int N> __device__ __forceinline__ double rowRotate(double v) {
   return __longlong_as_double(static_cast<long long>((static_cast<unsigned long long>(hi) << 32) | lo));
 }
 
-template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
+// Lanes per block solve by default: one with up to 8 lanes per
+// environment, two with 16, four with 32.
+constexpr int defaultSolveLanes(int L) { return L >= 32 ? 4 : (L >= 16 ? 2 : 1); }
+
+template <class R, int B, int J, int CG, int CS, int L, int PL = defaultSolveLanes(L)>
+struct Stepper {
   using Env = EnvLds<R, B, J, CG, CS>;
   using Fr = Frames<R, B, J>;
   const DeviceModel<R> &M;
@@ -337,10 +342,39 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
   const Fr &F;
   Env &E;
   int lane; // 0..L-1 within the environment
-  // Lanes per block solve: with 16 lanes per environment two lanes (lane,
-  // lane ^ 8), with 32 lanes four (lane ^ 8, ^ 16, ^ 24) share each body's
-  // assembly and sum it by DPP row rotation / swizzle.
-  static constexpr int P = L >= 32 ? 4 : (L >= 16 ? 2 : 1);
+  // Lanes per block solve: one (the reference's accumulation order), or
+  // with 16 lanes per environment two lanes (lane, lane ^ 8), with 32 lanes
+  // four (lane ^ 8, ^ 16, ^ 24) that share each body's assembly and sum it by
+  // DPP row rotation / swizzle.
+  static constexpr int P = PL;
+  static_assert(P == 1 || (P == 2 && L == 16) || (P == 4 && L == 32),
+                "split block solves: two lanes with 16 per environment, four with 32");
+  // 64-bit words of a body's ground-contact mask
+  static constexpr int GW = (CG + 63) / 64;
+
+  // Ground contacts of body bi.
+  __device__ int groundCount(int bi) const {
+    int n = 0;
+#pragma unroll
+    for (int w = 0; w < GW; ++w)
+      n += __popcll(E.gmask[w][bi]);
+    return n;
+  }
+  // Index of body bi's n-th ground contact (from 0, list order), or -1.
+  __device__ int nthGround(int bi, int n) const {
+#pragma unroll
+    for (int w = 0; w < GW; ++w) {
+      uint64_t m = E.gmask[w][bi];
+      const int c = __popcll(m);
+      if (n < c) {
+        for (int k = 0; k < n; ++k)
+          m &= m - 1;
+        return 64 * w + __builtin_ctzll(m);
+      }
+      n -= c;
+    }
+    return -1;
+  }
 
   // ------------------------------------------------------------ access --
   DUCK_HD V3<R> X(int b) const { return {E.s.x[0][b], E.s.x[1][b], E.s.x[2][b]}; }
@@ -862,9 +896,11 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
       hingeRows<false>(H, bi, cur, true, implicitDrive, slow);
     }
     int nth = 0;
-    for (uint64_t m = E.gmask[bi]; m; m &= m - 1, ++nth)
-      if ((nth + 1) % nParts == part % nParts)
-        groundRows(H, bi, __builtin_ctzll(m), true);
+#pragma unroll
+    for (int w = 0; w < GW; ++w)
+      for (uint64_t m = E.gmask[w][bi]; m; m &= m - 1, ++nth)
+        if ((nth + 1) % nParts == part % nParts)
+          groundRows(H, bi, 64 * w + __builtin_ctzll(m), true);
     nth = 0;
     for (uint32_t m = E.smask[bi]; m; m &= m - 1, ++nth)
       if ((nth + 1) % nParts == part % nParts)
@@ -894,19 +930,32 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
     const int adjEnd = F.adjStart[bi + 1], adj0 = F.adjStart[bi] + p0;
     const bool h0 = adj0 < adjEnd;
     const int packed0 = F.adj[h0 ? adj0 : 0];
-    const uint64_t all = E.gmask[bi];
-    uint64_t m = all;
+    bool v0, v1, any;
+    int c0, c1;
+    if constexpr (GW == 1) {
+      const uint64_t all = E.gmask[0][bi];
+      uint64_t m = all;
 #pragma unroll
-    for (int k = 0; k < 3; ++k)
-      m = k < p0 ? m & (m - 1) : m;
-    const bool v0 = m != 0;
-    const int c0 = v0 ? __builtin_ctzll(m) : 0;
+      for (int k = 0; k < 3; ++k)
+        m = k < p0 ? m & (m - 1) : m;
+      v0 = m != 0;
+      c0 = v0 ? __builtin_ctzll(m) : 0;
 #pragma unroll
-    for (int k = 0; k < 4; ++k)
-      m = k < nParts ? m & (m - 1) : m;
-    const bool v1 = m != 0;
-    const int c1 = v1 ? __builtin_ctzll(m) : 0;
-    return {packed0 | int(h0) << 24 | int(v0) << 25 | int(v1) << 26 | int(all != 0) << 27,
+      for (int k = 0; k < 4; ++k)
+        m = k < nParts ? m & (m - 1) : m;
+      v1 = m != 0;
+      c1 = v1 ? __builtin_ctzll(m) : 0;
+      any = all != 0;
+    } else {
+      c0 = nthGround(bi, p0);
+      c1 = nthGround(bi, p0 + nParts);
+      v0 = c0 >= 0;
+      v1 = c1 >= 0;
+      c0 = v0 ? c0 : 0;
+      c1 = v1 ? c1 : 0;
+      any = groundCount(bi) != 0;
+    }
+    return {packed0 | int(h0) << 24 | int(v0) << 25 | int(v1) << 26 | int(any) << 27,
             c0 | c1 << 8 | (adj0 + nParts) << 16 | adjEnd << 24};
   }
 
@@ -933,9 +982,11 @@ template <class R, int B, int J, int CG, int CS, int L> struct Stepper {
     for (int adj = adjNext; adj < adjEnd; adj += nParts)
       hingeRows<true>(H, bi, F.adj[adj], true, implicitDrive, slow);
     int nth = 0;
-    for (uint64_t g = E.gmask[bi]; g; g &= g - 1, ++nth)
-      if ((!Ground || nth >= 2 * nParts) && nth % nParts == p0)
-        groundRows(H, bi, __builtin_ctzll(g), true);
+#pragma unroll
+    for (int w = 0; w < GW; ++w)
+      for (uint64_t g = E.gmask[w][bi]; g; g &= g - 1, ++nth)
+        if ((!Ground || nth >= 2 * nParts) && nth % nParts == p0)
+          groundRows(H, bi, 64 * w + __builtin_ctzll(g), true);
     nth = 0;
     for (uint32_t g = E.smask[bi]; g; g &= g - 1, ++nth)
       if (nth % nParts == p0)

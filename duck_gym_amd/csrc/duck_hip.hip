@@ -217,7 +217,8 @@ struct BatchBase {
   virtual void servo(const DuckServo &, const ServoBuffers &, hipStream_t) = 0;
 };
 
-template <class R, int B, int J, int CG, int CS, int L> class Batch final : public BatchBase {
+template <class R, int B, int J, int CG, int CS, int L, int PL = defaultSolveLanes(L)>
+class Batch final : public BatchBase {
   using State = EnvState<R, B, J, CG, CS>;
   static constexpr int G = 64 / L;
   DeviceModel<R> *dModel = nullptr;
@@ -237,7 +238,7 @@ template <class R, int B, int J, int CG, int CS, int L> class Batch final : publ
                   substeps, motor != nullptr, kp, limit,
                   int(host.bodies.size()), int(host.joints.size()), int(host.shapes.size()),
                   int(host.pairs.size())};
-    advanceKernel<R, B, J, CG, CS, L><<<(n + G - 1) / G, 64, 0, s>>>(args);
+    advanceKernel<R, B, J, CG, CS, L, PL><<<(n + G - 1) / G, 64, 0, s>>>(args);
     launched("advanceKernel");
   }
 
@@ -490,8 +491,8 @@ public:
 };
 
 #define DUCK_OFF(T, f) static_cast<long long>(offsetof(T, f))
-template <class R, int B, int J, int CG, int CS, int L>
-void Batch<R, B, J, CG, CS, L>::layout(long long *o) const {
+template <class R, int B, int J, int CG, int CS, int L, int PL>
+void Batch<R, B, J, CG, CS, L, PL>::layout(long long *o) const {
   using S = EnvState<R, B, J, CG, CS>;
   using GC = GroundContact<R>;
   using SC = SelfContact<R>;
@@ -533,14 +534,22 @@ BatchBase *makeBatch(HostModel &&m, int n, double dt, int iterations, int device
   const int nb = m.bodies.size(), nj = m.joints.size(), ns = m.shapes.size(),
             np = m.pairs.size();
   if (nb <= 16 && nj <= 16 && ns <= 16 && np <= 8 && m.groundCapacity <= 64) {
-    if (split || sizeof(R) == sizeof(float))
-      return new Batch<R, 16, 16, 64, 8, 16>(std::move(m), n, dt, iterations, device);
-    return new Batch<R, 16, 16, 64, 8, 8>(std::move(m), n, dt, iterations, device);
+    if constexpr (sizeof(R) == sizeof(double))
+      if (!split)
+        return new Batch<R, 16, 16, 64, 8, 8>(std::move(m), n, dt, iterations, device);
+    return new Batch<R, 16, 16, 64, 8, 16>(std::move(m), n, dt, iterations, device);
   }
-  // Per-body contact masks are 64-bit: at most 64 ground contacts per env.
-  if (m.groundCapacity > 64)
+  // The generic state: 32 bodies and hinges, 4 ground contacts for each of
+  // up to 32 shapes and one per body-contact pair (the reference's
+  // BasicState<32, 32, 160>, kernel.cuh:365, holds the sum of both).
+  // Float (and float64 with DUCK_FLAG_SPLIT): four lanes per block solve;
+  // float64: one lane per block solve, the reference's accumulation order.
+  if (m.groundCapacity > 128 || m.selfCapacity > 32)
     throw DuckError(DUCK_ERR_MODEL, "Model exceeds selected state contact capacity");
-  return new Batch<R, 32, 32, 64, 32, 32>(std::move(m), n, dt, iterations, device);
+  if constexpr (sizeof(R) == sizeof(double))
+    if (!split)
+      return new Batch<R, 32, 32, 128, 32, 32, 1>(std::move(m), n, dt, iterations, device);
+  return new Batch<R, 32, 32, 128, 32, 32>(std::move(m), n, dt, iterations, device);
 }
 
 // The model checks of the selected backend after loadModel's flattening

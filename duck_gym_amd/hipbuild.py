@@ -1,4 +1,5 @@
-"""Build libduck_hip.so (gfx950) in-tree with hipcc.
+"""Build libduck_hip.so (gfx950) in-tree with hipcc, then check its machine
+code (codecheck: no vector instruction placed where exec is zero).
 
 Flags:
   -ffp-contract=off  no FMA contraction, so float results track the reference
@@ -53,6 +54,9 @@ def build(force: bool = True, verbose: bool = False) -> Path:
     if verbose:
         print(" ".join(cmd), flush=True)
     subprocess.run(cmd, check=True)
+    from . import codecheck
+
+    codecheck.check(tmp, ARCH)  # no vector writes placed where exec is zero
     os.replace(tmp, LIBRARY)
     return LIBRARY
 

@@ -128,6 +128,21 @@ def _rel(a, b, floor):
     return float(np.max(np.abs(a - b) / np.maximum(floor, np.abs(b))))
 
 
+# One float32 rounding of a constraint value formed from coordinates of
+# order 0.1-1 (m or rad).
+CONSTRAINT_EPS = 1e-8
+
+
+def _rel_k(a, b, k):
+    """Multiplier difference beyond what one rounding of the constraint
+    moves it by (penalty k x CONSTRAINT_EPS), relative to max(1, |ref|)."""
+    a, b, k = (np.asarray(v, dtype=np.float64) for v in (a, b, k))
+    if a.size == 0:
+        return 0.0
+    excess = np.maximum(0.0, np.abs(a - b) - np.abs(k) * CONSTRAINT_EPS)
+    return float(np.max(excess / np.maximum(1.0, np.abs(b))))
+
+
 def _abs(a, b):
     a, b = np.asarray(a, dtype=np.float64), np.asarray(b, dtype=np.float64)
     return float(np.max(np.abs(a - b), initial=0.0))
@@ -150,6 +165,8 @@ def differences(gpu, ref):
     d["w"] = _abs(gpu["w"], ref["w"])
     d["joint_lambda"] = max(_rel(gpu["lambda"], ref["lambda"], 1.0),
                             _rel(gpu["lambdaF"], ref["lambdaF"], 1.0))
+    d["joint_lambda_k"] = max(_rel_k(gpu["lambda"], ref["lambda"], ref["penalty"]),
+                              _rel_k(gpu["lambdaF"], ref["lambdaF"], ref["penaltyF"]))
     d["joint_penalty"] = max(_rel(gpu["penalty"], ref["penalty"], 1.0),
                              _rel(gpu["penaltyF"], ref["penaltyF"], 1.0))
     same_g = [k[:5] for k in contact_keys(gpu["gc"])] == [k[:5] for k in contact_keys(ref["gc"])]
@@ -159,22 +176,25 @@ def differences(gpu, ref):
         p, f = stick_mismatches(gpu[key], ref[key])
         stick_pressing += p
         stick_free += f
-    geo, c0, lam, pen = 0.0, 0.0, 0.0, 0.0
+    geo, c0, lam, lamk, pen = 0.0, 0.0, 0.0, 0.0, 0.0
     if same_g:
         for a, b in zip(gpu["gc"], ref["gc"]):
             geo = max(geo, _abs(a["local"], b["local"]), _abs(a["anchor"], b["anchor"]))
             c0 = max(c0, _abs(a["c0"], b["c0"]))
             lam = max(lam, _rel(a["lambda"], b["lambda"], 1.0))
+            lamk = max(lamk, _rel_k(a["lambda"], b["lambda"], b["penalty"]))
             pen = max(pen, _rel(a["penalty"], b["penalty"], 1.0))
     if same_s:
         for a, b in zip(gpu["sc"], ref["sc"]):
             geo = max(geo, *(_abs(a[k], b[k]) for k in ("local", "localB", "t1", "t2", "n")))
             c0 = max(c0, _abs(a["c0"], b["c0"]))
             lam = max(lam, _rel(a["lambda"], b["lambda"], 1.0))
+            lamk = max(lamk, _rel_k(a["lambda"], b["lambda"], b["penalty"]))
             pen = max(pen, _rel(a["penalty"], b["penalty"], 1.0))
             assert abs(float(a["friction"][0]) - float(b["friction"][0])) <= 1e-7 * max(
                 1.0, abs(float(b["friction"][0]))), "pair friction"
-    d.update(contact_geometry=geo, contact_c0=c0, contact_lambda=lam, contact_penalty=pen)
+    d.update(contact_geometry=geo, contact_c0=c0, contact_lambda=lam, contact_lambda_k=lamk,
+             contact_penalty=pen)
     gd, rd = np.asarray(gpu["diag"])[:5], np.asarray(ref["diag"])[:5]
     d["diag"] = float(np.max(np.abs(gd - rd)))
     d["stick_free"] = stick_free
@@ -192,15 +212,20 @@ def differences(gpu, ref):
 # joint and contact multipliers, penalties, contact points -- is held to
 # `tol` as well (absolute, or relative to max(1, |ref|)).  float32 runs use
 # the hardware reciprocal/square root, fused multiply-adds and another
-# summation order.  After the ten augmented-Lagrangian iterations of one
-# step from an identical state the multipliers differ by up to ~2e-3
-# relative (a multiplier moves by penalty x constraint, penalties up to
-# 1e9): FLOAT_LAMBDA_RTOL.  A penalty ramps by beta |C| per iteration, so
+# summation order.  A multiplier moves by penalty x constraint (penalties up
+# to 1e9 on positions, 1e7 on angles), so one float rounding of a
+# constraint value (CONSTRAINT_EPS) moves it by k x CONSTRAINT_EPS; beyond
+# that, after the ten augmented-Lagrangian iterations of one step from an
+# identical state, multipliers agree within FLOAT_LAMBDA_RTOL of
+# max(1, |lambda|).  Measured: 2.2e-3 on the biped, 2.0e-2 on a curled
+# 24-segment chain with its hinge limits engaged -- where the reference's
+# own float32 build differs from its float64 build by as much (2.0e-2 after
+# 20 steps, poses within 7e-6).  A penalty ramps by beta |C| per iteration, so
 # float rounding of an angle (~1e-7 rad) moves an angular penalty at its
 # floor of 1 by beta_angular (1e5) x 1e-7 x 10 iterations = 0.1 relative:
 # FLOAT_PENALTY_RTOL.  Velocities are pose differences over one step
 # (v = (x - x0) / h), so a pose tolerance admits 2 tol / h.
-FLOAT_LAMBDA_RTOL = 1e-2
+FLOAT_LAMBDA_RTOL = 5e-2
 FLOAT_PENALTY_RTOL = 1e-1
 
 
@@ -210,8 +235,8 @@ def default_gates(tol, dt, fp64):
                     contact_geometry=tol, contact_c0=tol, contact_lambda=tol,
                     contact_penalty=tol, diag=tol)
     return dict(x=tol, rot=tol, q=tol, v=2 * tol / dt, w=2 * tol / dt,
-                joint_lambda=FLOAT_LAMBDA_RTOL, joint_penalty=FLOAT_PENALTY_RTOL,
-                contact_geometry=tol, contact_c0=tol, contact_lambda=FLOAT_LAMBDA_RTOL,
+                joint_lambda_k=FLOAT_LAMBDA_RTOL, joint_penalty=FLOAT_PENALTY_RTOL,
+                contact_geometry=tol, contact_c0=tol, contact_lambda_k=FLOAT_LAMBDA_RTOL,
                 contact_penalty=FLOAT_PENALTY_RTOL, diag=tol)
 
 

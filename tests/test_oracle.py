@@ -113,6 +113,35 @@ def test_oracle_matches_reference_build_live(fp64, models, home):
                 np.testing.assert_array_equal(a, b)
 
 
+@pytest.mark.skipif(not probe_available(), reason="reference build (oracle/_ref) absent")
+@pytest.mark.parametrize("fp64", [False, True])
+def test_oracle_matches_reference_build_on_generic_model(fp64, tmp_path):
+    """The generic state (kernel.cuh:365, BasicState<32, 32, 160>) on a
+    25-body caterpillar: 96 ground contacts plus body contacts between
+    segments i and i + 2 and up to 7 colours, bit-exact with kernel.cuh."""
+    from model_text import caterpillar
+
+    model = _model_file(caterpillar(), tmp_path)
+    rng = np.random.default_rng(5 if fp64 else 6)
+    o, p = Oracle(model, 0.005, 10, fp64), ReferenceProbe(model, 0.005, 10, fp64)
+    for x in (o, p):
+        x.reset(np.zeros(23))
+    target = 1.05 + rng.uniform(-0.1, 0.1, 23)
+    most = [0, 0, 0]
+    for _ in range(40):
+        for x in (o, p):
+            x.step(target, None, 1, 8.0, 0.0)
+        for a, b in zip(o.snapshot(), p.snapshot()):
+            np.testing.assert_array_equal(a, b)
+        np.testing.assert_array_equal(o.joint_state(), p.joint_state())
+        for a, b in zip(o.contacts(256), p.contacts(256)):
+            np.testing.assert_array_equal(a, b)
+        assert o.colors()[1] == p.colors()[1]
+        counts = o.contact_counts()
+        most = [max(most[0], counts[0]), max(most[1], counts[1]), max(most[2], o.colors()[1])]
+    assert most[0] == 96 and most[1] > 0 and most[2] > 2, most
+
+
 # --------------------------------------------------------------- closed forms
 FREE_BODY = """DUCK_MODEL 1 2 0 0
 0 0 -9.81 0
