@@ -17,7 +17,9 @@ The JSON line also carries
                 rocprofv3 FETCH_SIZE/WRITE_SIZE when recorded in profiles/
   cpu_baseline  the reference's own CPU build of the same solver core
                 (src/cuda/kernel.cuh via src/cuda/cpu_bindings.cpp, compiled
-                in place into oracle/_ref) on a bounded sample, all threads
+                in place into oracle/_ref) on a bounded sample of the
+                4096-env workload over the host's CPUs, plus the single-env
+                float64 figure and src/solver.cpp's own CLI on that env
 """
 
 from __future__ import annotations
@@ -61,55 +63,97 @@ def measured_traffic():
     return float(m.group(1)) if m else None
 
 
+def host_facts():
+    """The CPU the baseline ran on: logical CPUs, those this process may use,
+    the model name, and the reference build's compiler and flags."""
+    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    model = None
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    info = ROOT / "oracle" / "_ref" / "BUILD_INFO"
+    build = info.read_text().splitlines() if info.exists() else [None, None]
+    return {"nproc": os.cpu_count(), "available_cpus": threads, "cpu_model": model,
+            "compiler": build[0], "flags": build[1] if len(build) > 1 else None}
+
+
 def cpu_baseline(model, home, seconds_budget=12.0):
-    """Time the reference CPU core (oracle/_ref/_duck_reference.CpuBatch32)
-    on a bounded sample of the same workload; fall back to this repository's
-    oracle ("port") when the reference build is absent."""
+    """The reference's own CPU build of the solver core, timed on this host:
+
+    batch   kernel.cuh's CPU batch (CpuBatch32, src/cuda/cpu_bindings.cpp,
+            compiled in place into oracle/_ref) on the same 4096-env workload,
+            env-striped over every CPU this process may use (capped by
+            OMP_NUM_THREADS where set: a GPU box grants 16 per GPU), for about
+            `seconds_budget` seconds;
+    single  one env in float64 on one thread for 200 steps (CpuBatch64),
+            timed around step() only, as src/main.cpp:63-68 times its solver;
+    solver  src/solver.cpp's own CLI (duck_sim) on the same env: its steps/s
+            and where the root ends -- its explicit PD drive diverges at
+            kp = 8, dt = 5 ms.
+    The reference build is required: without oracle/_ref this raises."""
+    import json as _json
+    import subprocess
+
     import numpy as np
 
-    threads = max(1, min(16, os.cpu_count() or 1))
-    envs = 64 * threads
     sys.path.insert(0, str(ROOT / "oracle" / "_ref"))
     try:
-        import _duck_reference  # noqa: F401
+        import _duck_reference
+    except ImportError as e:
+        raise RuntimeError("the reference CPU build is missing (make -C oracle ref): "
+                           f"{e}") from e
+    facts = host_facts()
+    threads = facts["available_cpus"] or 1
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        threads = min(threads, int(os.environ["OMP_NUM_THREADS"]))
+    threads = max(1, min(64, threads))  # CpuBatch accepts 1-64 threads
+    envs = ENVS
+    batch = _duck_reference.CpuBatch32(str(model), envs, DT, ITERATIONS, threads)
+    q = np.tile(home, (envs, 1)).astype(np.float32)
+    batch.reset(np.ones(envs, bool), q, np.zeros((envs, 6), np.float32))
+    forces = np.zeros((envs, 3), np.float32)
+    batch.step(q, forces, 1, KP, 1e9)  # warm; limit 1e9 = uncapped PD torques
+    steps, start = 0, time.perf_counter()
+    while time.perf_counter() - start < seconds_budget:
+        batch.step(q, forces, 1, KP, 1e9)
+        steps += 1
+    elapsed = time.perf_counter() - start
 
-        batch = _duck_reference.CpuBatch32(str(model), envs, DT, ITERATIONS, threads)
-        q = np.tile(home, (envs, 1)).astype(np.float32)
-        batch.reset(np.ones(envs, bool), q, np.zeros((envs, 6), np.float32))
-        forces = np.zeros((envs, 3), np.float32)
-        batch.step(q, forces, 1, KP, 1e9)  # warm
-        steps, start = 0, time.perf_counter()
-        while time.perf_counter() - start < seconds_budget:
-            batch.step(q, forces, 1, KP, 1e9)  # limit 1e9 = uncapped for PD torques
-            steps += 1
-        elapsed = time.perf_counter() - start
-        kind, cores = "reference", threads
-        sample = (f"{envs} envs x {steps} steps of src/cuda/kernel.cuh's CPU build "
-                  f"(CpuBatch32, {threads} threads), same model/HOME/dt/iterations")
-    except ImportError:
-        from concurrent.futures import ThreadPoolExecutor
+    single = _duck_reference.CpuBatch64(str(model), 1, DT, ITERATIONS, 1)
+    q1 = home[None].astype(np.float64)
+    single.reset(np.ones(1, bool), q1, np.zeros((1, 6)))
+    f1 = np.zeros((1, 3))
+    spent = 0.0
+    for _ in range(200):
+        t0 = time.perf_counter()
+        single.step(q1, f1, 1, KP, 1e9)
+        spent += time.perf_counter() - t0
 
-        from oracle.oracle import Oracle
-
-        envs = 4 * threads
-        oracles = [Oracle(model, DT, ITERATIONS, False) for _ in range(envs)]
-        for o in oracles:
-            o.reset(home)
-
-        def run(o, n):
-            for _ in range(n):
-                o.step(home, None, 1, KP, 0.0)
-
-        steps, start = 0, time.perf_counter()
-        with ThreadPoolExecutor(threads) as pool:
-            while time.perf_counter() - start < seconds_budget:
-                list(pool.map(lambda o: run(o, 5), oracles))
-                steps += 5
-        elapsed = time.perf_counter() - start
-        kind, cores = "port", threads
-        sample = f"{envs} envs x {steps} steps of the CPU oracle, {threads} threads"
-    return {"value": envs * steps / elapsed, "unit": "env-steps/s", "cores": cores,
-            "kind": kind, "sample": sample}
+    run = subprocess.run([str(ROOT / "oracle" / "_ref" / "duck_sim"), str(model), "--steps", "200",
+                          "--dt", str(DT), "--iterations", str(ITERATIONS), "--output",
+                          "/dev/stdout"], capture_output=True, text=True, check=True).stdout
+    summary = _json.loads([line for line in run.splitlines() if line.startswith("{")][-1])
+    rows = [line.split(",") for line in run.splitlines() if line[:1].isdigit()]
+    roots = {int(r[0]): np.array([float(v) for v in r[3:6]]) for r in rows if r[2] == "1"}
+    return {
+        "value": envs * steps / elapsed, "unit": "env-steps/s", "cores": threads,
+        "kind": "reference",
+        "sample": (f"{envs} envs x {steps} steps of src/cuda/kernel.cuh's CPU build (CpuBatch32, "
+                   f"float32, {threads} threads), same model/HOME/dt/iterations"),
+        "host": facts,
+        "single_env_fp64": {
+            "value": 200 / spent, "unit": "steps/s", "steps": 200, "threads": 1,
+            "sample": "CpuBatch64 (kernel.cuh, float64), 1 env at HOME, timed around step()"},
+        "solver_cpp": {
+            "steps_per_second": summary["steps_per_second"], "steps": 200,
+            "root_displacement_m": float(np.linalg.norm(roots[200] - roots[0])),
+            "unconverged_steps": summary["unconverged_steps"],
+            "note": "src/solver.cpp (duck_sim): its explicit PD drive diverges at kp 8, dt 5 ms"},
+    }
 
 
 def other_workload(args):

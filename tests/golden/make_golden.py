@@ -13,6 +13,7 @@ text is stored in each fixture) and the reference's tests/fixtures/pendulum.duck
 
 Run in a container that has the reference tree:
     make -C oracle ref && python tests/golden/make_golden.py
+(`--solver-pd` writes only the explicit-PD duck_sim fixtures.)
 """
 
 from __future__ import annotations
@@ -90,20 +91,48 @@ def probe_record(model_path, fp64, targets, steps, limit=0.0, motor=None, root=N
     return {k: np.array(v) for k, v in rec.items()}
 
 
-def duck_sim_record(model_path, steps, iterations=ITER):
+def duck_sim_record(model_path, steps, iterations=ITER, dt=DT, summary=False):
     out = subprocess.run([str(REF_DIR / "duck_sim"), str(model_path), "--steps", str(steps),
-                          "--dt", str(DT), "--iterations", str(iterations), "--output",
+                          "--dt", str(dt), "--iterations", str(iterations), "--output",
                           "/dev/stdout"], capture_output=True, text=True, check=True).stdout
     rows = [r for r in csv.reader(io.StringIO(out)) if r and r[0].isdigit()]
     by_step = {}
     for r in rows:
         by_step.setdefault(int(r[0]), []).append([float(v) for v in r[3:]])
-    return np.array([by_step[s] for s in range(steps + 1)])
+    trajectory = np.array([by_step[s] for s in range(steps + 1)])
+    if summary:
+        return trajectory, [line for line in out.splitlines() if line.startswith("{")][-1]
+    return trajectory
+
+
+SOLVER_CHECKPOINTS = (0, 1, 2, 3, 10, 50, 100, 150, 200)
+
+
+def solver_pd_fixtures(tmp):
+    """src/solver.cpp (duck_sim) with the explicit PD drive of the standing
+    biped (kp = 8 from the file, HOME targets): 200 steps at the single-env
+    workload's dt = 5 ms, where it diverges, and at dt = 1 ms, where it stays
+    bounded; checkpoints of the trajectory and duck_sim's JSON summary."""
+    text, _ = model_text()
+    path = tmp / "standing_pd.duck"
+    path.write_text(text)
+    for dt, name in ((0.005, "solver_standing_kp8_dt5ms_fp64"),
+                     (0.001, "solver_standing_kp8_dt1ms_fp64")):
+        trajectory, summary = duck_sim_record(path, 200, dt=dt, summary=True)
+        np.savez_compressed(HERE / f"{name}.npz", model=np.array(text), dt=dt,
+                            step=np.array(SOLVER_CHECKPOINTS),
+                            trajectory=trajectory[list(SOLVER_CHECKPOINTS)],
+                            summary=np.array(summary))
+        print("wrote", name, flush=True)
 
 
 def main():
     if not (REF_DIR / "ref_probe.so").exists():
         raise SystemExit("oracle/_ref is not built: make -C oracle ref")
+    if sys.argv[1:] == ["--solver-pd"]:
+        with tempfile.TemporaryDirectory() as tmp:
+            solver_pd_fixtures(Path(tmp))
+        return
     rng = np.random.default_rng(20260927)
     with tempfile.TemporaryDirectory() as tmp:
         tmp = Path(tmp)

@@ -88,6 +88,40 @@ def test_oracle_explicit_mode_reproduces_duck_sim(name, steps, tmp_path):
         np.testing.assert_array_equal(o.snapshot()[0][1:], traj[s])
 
 
+@pytest.mark.parametrize("name", ["solver_standing_kp8_dt5ms_fp64", "solver_standing_kp8_dt1ms_fp64"])
+def test_oracle_explicit_pd_reproduces_duck_sim(name, tmp_path):
+    """The explicit PD drive of solver.cpp (solver.cpp:339-347, kp = 8 from
+    the model file, HOME targets) bit for bit at every checkpoint of
+    duck_sim's own 200-step trajectories."""
+    f = np.load(GOLDEN / f"{name}.npz")
+    o = Oracle(_model_file(f["model"], tmp_path), float(f["dt"]), 10, True, EXPLICIT_SEQUENTIAL)
+    steps = list(f["step"])
+    np.testing.assert_array_equal(o.snapshot()[0][1:], f["trajectory"][0])
+    for s in range(1, steps[-1] + 1):
+        o.advance(1)
+        if s in steps:
+            np.testing.assert_array_equal(o.snapshot()[0][1:], f["trajectory"][steps.index(s)])
+
+
+def test_solver_cpp_diverges_on_the_single_env_workload():
+    """The reference's own duck_sim on the single-env workload (the biped at
+    HOME, kp = 8 with its explicit PD drive, dt = 5 ms, 10 iterations): the
+    root leaves for tens of metres and no step converges; at dt = 1 ms the
+    same model stays within a few centimetres of its start.  This is why the
+    GPU path (the CudaBatch semantics: the PD drive stamped implicitly into
+    the Hessian) is checked against kernel.cuh, not against solver.cpp."""
+    import json
+
+    f = np.load(GOLDEN / "solver_standing_kp8_dt5ms_fp64.npz")
+    root = f["trajectory"][:, 0, :3]
+    summary = json.loads(str(f["summary"]))
+    assert np.linalg.norm(root[-1] - root[0]) > 10.0
+    assert summary["unconverged_steps"] == 200 and summary["max_contacts"] > 16
+    g = np.load(GOLDEN / "solver_standing_kp8_dt1ms_fp64.npz")
+    bounded = g["trajectory"][:, 0, :3]
+    assert np.linalg.norm(bounded[-1] - bounded[0]) < 0.2
+
+
 @pytest.mark.skipif(not probe_available(), reason="reference build (oracle/_ref) absent")
 @pytest.mark.parametrize("fp64", [False, True])
 def test_oracle_matches_reference_build_live(fp64, models, home):
