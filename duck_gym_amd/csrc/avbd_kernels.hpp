@@ -415,8 +415,8 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
     const bool in = valid && j < nj;
     const int jc = j < nj ? j : 0;
     ctl[r][0] = ctl[r][1] = ctl[r][2] = 0;
-    if (in) {
-      if (args.motorMode) {
+    if (in && args.motorMode != kHeldControls) {
+      if (args.motorMode == kMotorControls) {
         const R *motor = static_cast<const R *>(args.motor) + size_t(e) * nj * 3;
         ctl[r][0] = motor[3 * j];
         ctl[r][1] = motor[3 * j + 1];
@@ -429,7 +429,7 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
     defs[r][1] = M.frictionloss[jc];
     defs[r][2] = M.damping[jc];
   }
-  if (valid && lane < 3)
+  if (valid && lane < 3 && args.motorMode != kHeldControls)
     fin = static_cast<const R *>(args.forces)[size_t(e) * 3 + lane];
 
   // Stage the joint model (all 64 lanes); the slots of absent hinges hold
@@ -494,12 +494,12 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
 
   // ---- controls (extension.cu:87-110 / kernel.cuh:448-466) ----
   int bad = 0;
-  if (valid) {
+  if (valid && args.motorMode != kHeldControls) {
 #pragma unroll
     for (int r = 0; r < JPL; ++r) {
       if (lane + r * L >= nj)
         continue;
-      if (args.motorMode) {
+      if (args.motorMode == kMotorControls) {
         if (!mfinite(ctl[r][0]) || !mfinite(ctl[r][1]) || !mfinite(ctl[r][2]) || ctl[r][1] < 0 ||
             ctl[r][2] < 0)
           bad = 1;
@@ -514,7 +514,11 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
   __syncthreads();
   bool active = false;
   if (valid) {
-    if (args.motorMode) {
+    if (args.motorMode == kHeldControls) {
+      // State::advance (kernel.cuh:421-443): the controls in the state as
+      // they stand
+      active = !E.s.failed;
+    } else if (args.motorMode == kMotorControls) {
       // setMotor applies the channels even when they are invalid.
 #pragma unroll
       for (int r = 0; r < JPL; ++r) {

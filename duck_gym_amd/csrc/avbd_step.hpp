@@ -18,6 +18,11 @@
 
 namespace duckhip {
 
+// StepArgs::motorMode: the controls a launch applies before its steps --
+// targets with kp and limit (CudaBatch.step), explicit motor channels
+// (step_motor), or none: the state's own (duck_advance).
+enum { kTargetControls = 0, kMotorControls = 1, kHeldControls = 2 };
+
 struct StepArgs {
   const void *model;   // DeviceModel<R>
   const void *points;  // shape points, R[3] each
@@ -28,7 +33,7 @@ struct StepArgs {
   const void *forces;  // [E,3]
   const void *motor;   // [E,J,3] (motor mode)
   int substeps;
-  int motorMode;
+  int motorMode; // kTargetControls, kMotorControls or kHeldControls
   double kp, limit;
   int nb, nj, ns, np; // model counts (also in the model), here so that the
                       // first loads need only the kernel arguments

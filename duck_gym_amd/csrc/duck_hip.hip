@@ -199,6 +199,7 @@ struct BatchBase {
                      hipStream_t) = 0;
   virtual void step(const void *, const void *, int, double, double, hipStream_t) = 0;
   virtual void stepMotor(const void *, const void *, hipStream_t) = 0;
+  virtual void advanceHeld(int, hipStream_t) = 0;
   virtual void state(void *, void *, void *, hipStream_t) = 0;
   virtual void contactForces(int, void *, hipStream_t) = 0;
   virtual void selfContactStats(void *, hipStream_t) = 0;
@@ -233,9 +234,12 @@ class Batch final : public BatchBase {
   static int blocks64(int n) { return (n + 63) / 64; }
 
   void advance(unsigned char *states, int n, const void *targets, const void *forces,
-               const void *motor, int substeps, double kp, double limit, hipStream_t s) {
+               const void *motor, int substeps, double kp, double limit, hipStream_t s,
+               int mode = -1) {
+    if (mode < 0)
+      mode = motor != nullptr ? kMotorControls : kTargetControls;
     StepArgs args{dModel, dPoints, states, blobBytes, n, targets, forces, motor,
-                  substeps, motor != nullptr, kp, limit,
+                  substeps, mode, kp, limit,
                   int(host.bodies.size()), int(host.joints.size()), int(host.shapes.size()),
                   int(host.pairs.size())};
     advanceKernel<R, B, J, CG, CS, L, PL><<<(n + G - 1) / G, 64, 0, s>>>(args);
@@ -330,6 +334,13 @@ public:
     require((motor || host.joints.empty()) && force, "step_motor: null buffer");
     wait(s);
     advance(dStates, count, nullptr, force, motor, 1, 0, 0, s);
+    record(s);
+  }
+  void advanceHeld(int substeps, hipStream_t s) override {
+    DeviceGuard guard(device);
+    require(substeps > 0, "Invalid controls");
+    wait(s);
+    advance(dStates, count, nullptr, nullptr, nullptr, substeps, 0, 0, s, kHeldControls);
     record(s);
   }
   void state(void *bodies, void *joints, void *diag, hipStream_t s) override {
@@ -683,6 +694,9 @@ int duck_step(void *handle, const void *target, const void *force, int substeps,
 }
 int duck_step_motor(void *handle, const void *motor, const void *force, void *hip_stream) {
   return guarded([&] { as(handle)->stepMotor(motor, force, st(hip_stream)); });
+}
+int duck_advance(void *handle, int substeps, void *hip_stream) {
+  return guarded([&] { as(handle)->advanceHeld(substeps, st(hip_stream)); });
 }
 int duck_state(void *handle, void *bodies, void *joints, void *diag, void *hip_stream) {
   return guarded([&] { as(handle)->state(bodies, joints, diag, st(hip_stream)); });

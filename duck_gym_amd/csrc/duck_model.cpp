@@ -56,6 +56,12 @@ void readUnit(std::istream &in, double v[3]) {
 } // namespace
 
 HostModel loadModel(const std::string &path) {
+  HostModel m = parseModel(path);
+  flattenModel(m);
+  return m;
+}
+
+HostModel parseModel(const std::string &path) {
   std::ifstream in(path);
   if (!in)
     throw std::runtime_error("Cannot read model: " + path);
@@ -95,7 +101,6 @@ HostModel loadModel(const std::string &path) {
         j.armature < 0 || j.frictionloss < 0)
       throw std::runtime_error("Invalid joint");
   }
-  std::vector<std::vector<D3>> shapePoints(ns);
   for (int si = 0; si < ns; ++si) {
     auto &s = m.shapes[si];
     int n = -1;
@@ -107,30 +112,13 @@ HostModel loadModel(const std::string &path) {
     if (s.body < 0 || s.body >= nb || s.type < 0 || s.type > 3 || n < 0 || n > 1000000 ||
         s.friction < 0)
       throw std::runtime_error("Invalid collision shape");
-    std::vector<D3> vertices(n);
-    for (auto &v : vertices)
-      in >> v.x >> v.y >> v.z;
+    s.vertices.resize(3 * size_t(n));
+    for (auto &v : s.vertices)
+      in >> v;
     if (version == 2)
       in >> s.ground;
     if (s.type == 3 && n < 4)
       throw std::runtime_error("Convex mesh needs at least four vertices");
-    auto &pts = shapePoints[si];
-    if (s.type == 1) {
-      for (int i = 0; i < 8; ++i)
-        pts.push_back(add(get(s.center), rotate(s.q, D3{(i & 1 ? 1 : -1) * s.size[0],
-                                                        (i & 2 ? 1 : -1) * s.size[1],
-                                                        (i & 4 ? 1 : -1) * s.size[2]})));
-    } else if (s.type == 3) {
-      for (auto v : vertices)
-        pts.push_back(add(get(s.center), rotate(s.q, v)));
-    }
-    for (auto p : pts)
-      s.radius = std::max(s.radius, std::sqrt(dot(p, p)));
-    D3 c = get(s.center);
-    if (s.type == 0)
-      s.radius = std::sqrt(dot(c, c)) + s.size[0];
-    if (s.type == 2)
-      s.radius = std::sqrt(dot(c, c)) + s.size[0] + s.size[1];
   }
   if (version == 2) {
     int count = -1;
@@ -155,6 +143,41 @@ HostModel loadModel(const std::string &path) {
   std::string extra;
   if (in >> extra)
     throw std::runtime_error("Unexpected model data");
+  return m;
+}
+
+void flattenModel(HostModel &m) {
+  const int nb = m.bodies.size(), nj = m.joints.size(), ns = m.shapes.size();
+  // Body-frame points of boxes (8 corners) and hulls, and bounding radii
+  // (solver.cpp:130-148).
+  std::vector<std::vector<D3>> shapePoints(ns);
+  for (int si = 0; si < ns; ++si) {
+    auto &s = m.shapes[si];
+    auto &pts = shapePoints[si];
+    s.radius = 0;
+    if (s.type == 1) {
+      for (int i = 0; i < 8; ++i)
+        pts.push_back(add(get(s.center), rotate(s.q, D3{(i & 1 ? 1 : -1) * s.size[0],
+                                                        (i & 2 ? 1 : -1) * s.size[1],
+                                                        (i & 4 ? 1 : -1) * s.size[2]})));
+    } else if (s.type == 3) {
+      for (size_t v = 0; v + 2 < s.vertices.size(); v += 3)
+        pts.push_back(add(get(s.center),
+                          rotate(s.q, D3{s.vertices[v], s.vertices[v + 1], s.vertices[v + 2]})));
+    }
+    for (auto p : pts)
+      s.radius = std::max(s.radius, std::sqrt(dot(p, p)));
+    D3 c = get(s.center);
+    if (s.type == 0)
+      s.radius = std::sqrt(dot(c, c)) + s.size[0];
+    if (s.type == 2)
+      s.radius = std::sqrt(dot(c, c)) + s.size[0] + s.size[1];
+  }
+  m.points.clear();
+  m.colors.clear();
+  m.adjacencyStart.clear();
+  m.adjacency.clear();
+  m.groundCapacity = 0;
 
   // Flattening checks (model.hpp:26-91).
   require(nb <= 32 && nj <= 32 && ns <= 32 && int(m.pairs.size()) <= 32,
@@ -207,7 +230,6 @@ HostModel loadModel(const std::string &path) {
       m.points.push_back(p.z);
     }
   }
-  return m;
 }
 
 } // namespace duckhip

@@ -25,6 +25,7 @@ struct HostJoint {
 struct HostShape {
   int body = 0, type = 0, ground = 1, offset = 0, count = 0;
   double center[3]{}, size[3]{}, q[4]{1, 0, 0, 0}, friction = 0.8, radius = 0, interior[3]{};
+  std::vector<double> vertices; // the file's hull vertices (xyz), shape frame
 };
 struct HostPair {
   int a = 0, b = 0;
@@ -46,5 +47,11 @@ struct HostModel {
 // Throws std::invalid_argument / std::runtime_error with the reference's
 // messages on malformed input.
 HostModel loadModel(const std::string &path);
+// The two halves of loadModel: parse the text with the checks of
+// Solver::load (std::runtime_error), and flatten it with the checks of
+// convert (std::invalid_argument): capacities, tree order, colours,
+// adjacency, shape points, interiors and contact capacities.
+HostModel parseModel(const std::string &path);
+void flattenModel(HostModel &m);
 
 } // namespace duckhip

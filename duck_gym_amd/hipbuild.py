@@ -24,8 +24,10 @@ from pathlib import Path
 PACKAGE = Path(__file__).resolve().parent
 ROOT = PACKAGE.parent
 LIBRARY = PACKAGE / "libduck_hip.so"
-SOURCES = [PACKAGE / "csrc" / "duck_hip.hip", PACKAGE / "csrc" / "duck_model.cpp"]
-HEADERS = sorted((PACKAGE / "csrc").glob("*.hpp")) + [ROOT / "include" / "duck_hip.h"]
+SOURCES = [PACKAGE / "csrc" / "duck_hip.hip", PACKAGE / "csrc" / "duck_model.cpp",
+           PACKAGE / "csrc" / "duck_solver.cpp"]
+HEADERS = sorted((PACKAGE / "csrc").glob("*.hpp")) + [ROOT / "include" / "duck_hip.h"] + sorted(
+    (ROOT / "include" / "duck").glob("*.hpp"))
 ARCH = os.environ.get("DUCK_HIP_ARCH", "gfx950")
 FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
@@ -59,6 +61,20 @@ def build(force: bool = True, verbose: bool = False) -> Path:
     codecheck.check(tmp, ARCH)  # no vector writes placed where exec is zero
     os.replace(tmp, LIBRARY)
     return LIBRARY
+
+
+CPP_TEST = ROOT / "tests" / "native" / "solver_api_test"
+
+
+def build_cpp_test() -> Path:
+    """The C++ interface's test program (tests/native/solver_api_test.cpp),
+    linked against the built library."""
+    source = CPP_TEST.with_suffix(".cpp")
+    cmd = ["g++", "-std=c++17", "-O2", "-Wall", f"-I{ROOT / 'include'}", str(source),
+           f"-L{PACKAGE}", "-lduck_hip", "-Wl,-rpath,$ORIGIN/../../duck_gym_amd",
+           "-Wl,-rpath-link,/opt/rocm/lib", "-o", str(CPP_TEST)]
+    subprocess.run(cmd, check=True)
+    return CPP_TEST
 
 
 if __name__ == "__main__":

@@ -43,6 +43,7 @@ def library():
             "duck_reset": (ip, [vp, vp, vp, vp, vp, vp]),
             "duck_step": (ip, [vp, vp, vp, ip, dbl, dbl, vp]),
             "duck_step_motor": (ip, [vp, vp, vp, vp]),
+            "duck_advance": (ip, [vp, ip, vp]),
             "duck_state": (ip, [vp, vp, vp, vp, vp]),
             "duck_contact_forces": (ip, [vp, ip, vp, vp]),
             "duck_self_contact_stats": (ip, [vp, vp, vp]),
@@ -70,7 +71,7 @@ def library():
 
 EXPORTED = (
     "duck_create", "duck_destroy", "duck_model_info", "duck_dims", "duck_num_envs", "duck_fp_bits",
-    "duck_state_bytes", "duck_joint_name", "duck_reset", "duck_step", "duck_step_motor",
+    "duck_state_bytes", "duck_joint_name", "duck_reset", "duck_step", "duck_step_motor", "duck_advance",
     "duck_state", "duck_contact_forces", "duck_self_contact_stats", "duck_contact_counts",
     "duck_generalized_loads", "duck_reference", "duck_reference_noalloc", "duck_state_layout",
     "duck_export_state",
@@ -223,6 +224,15 @@ class CudaBatch:
             code = library().duck_step_motor(self._h, m, f, self._stream())
         if code:
             _raise(code, "step_motor")
+
+    def advance(self, substeps=1):
+        """`substeps` steps with the controls the state holds (duck_advance:
+        kernel.cuh's State::advance; CudaBatch has no such method -- the
+        C++ duck::Solver steps this way)."""
+        with torch.cuda.device(self.device):
+            code = library().duck_advance(self._h, int(substeps), self._stream())
+        if code:
+            _raise(code, "advance")
 
     def state(self):
         E = self.num_envs

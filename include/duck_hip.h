@@ -77,6 +77,14 @@ int duck_step(void *handle, const void *target, const void *force, int substeps,
  * one step with explicit (torque, dry-friction budget, damping) per hinge. */
 int duck_step_motor(void *handle, const void *motor, const void *force, void *hip_stream);
 
+/* `substeps` physics steps with the controls each environment's state holds
+ * (per-hinge target, kp, torque limit, torque, friction budget, damping, and
+ * the root force), as the reference's State::advance (kernel.cuh:421-443)
+ * runs them after its callers have set the controls.  No input is read or
+ * validated; set the controls through duck_import_state (the C++ duck::Solver
+ * does).  substeps > 0. */
+int duck_advance(void *handle, int substeps, void *hip_stream);
+
 /* CudaBatch.state() (extension.cu:321-335): bodies[E,B,13] (COM xyz, wxyz,
  * v, w), joints[E,J,2] (angle, rate), diag[E,6] (joint error, penetration,
  * contacts, converged, axis error, failed). */

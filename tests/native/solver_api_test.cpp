@@ -1,0 +1,215 @@
+// The duck C++ interface (include/duck/{math,solver}.hpp) over libduck_hip.so.
+//
+//   solver_api_test math          host-only checks of the math and the hinge
+//                                 constraint Jacobians (tests/math_test.cpp's
+//                                 invariants)
+//   solver_api_test gpu MODEL     environments of a duck::Batch stepped on the
+//                                 GPU: independence, reset, replay and reload
+//                                 (tests/state_test.cpp's invariants)
+//   solver_api_test trace MODEL N body poses after each of N steps
+// Prints one line per passed check; exits non-zero on the first failure.
+#include "duck/solver.hpp"
+
+#include <algorithm>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+
+using namespace duck;
+
+static void check(bool ok, const char *what) {
+  if (!ok) {
+    std::fprintf(stderr, "FAILED: %s\n", what);
+    std::exit(1);
+  }
+  std::printf("ok %s\n", what);
+}
+
+static int math() {
+  for (Vec3 v : {Vec3{0, 0, 0}, Vec3{1e-10, -2e-10, 3e-10}, Vec3{0.4, -0.2, 1.3},
+                 Vec3{3.1, 0, 0}}) {
+    check(norm(log(exp(v)) - v) < 1e-12, "log(exp(v)) == v");
+    const Vec3 a{1, 2, 3};
+    check(norm(rotate(conjugate(exp(v)), rotate(exp(v), a)) - a) < 1e-12, "rotation inverse");
+    check(std::abs(norm(rotate(exp(v), a)) - norm(a)) < 1e-12, "rotation keeps length");
+  }
+  // the rotation vector of a product of rotations about one axis adds up
+  check(norm(log(exp({0, 0, 0.3}) * exp({0, 0, 0.5})) - Vec3{0, 0, 0.8}) < 1e-14,
+        "exp(a) exp(b) == exp(a + b) about one axis");
+  check(std::abs(wrap(7.0) - (7.0 - 2 * std::acos(-1.0))) < 1e-15, "wrap");
+  M6 H{};
+  V6 x{1, -2, 3, -4, 5, -6}, g{};
+  for (int i = 0; i < 6; ++i)
+    for (int j = 0; j < 6; ++j)
+      H[i][j] = (i == j ? 8 : 0) + 1.0 / (1 + i + j);
+  for (int i = 0; i < 6; ++i)
+    for (int j = 0; j < 6; ++j)
+      g[i] -= H[i][j] * x[j];
+  const V6 y = solve(H, g);
+  double err = 0;
+  for (int i = 0; i < 6; ++i)
+    err = std::max(err, std::abs(y[i] - x[i]));
+  check(err < 1e-12, "solve(H, g) = -H^-1 g");
+  bool threw = false;
+  try {
+    solve(M6{}, V6{});
+  } catch (const std::runtime_error &) {
+    threw = true;
+  }
+  check(threw, "singular system rejected");
+  M6 S{};
+  V6 gs{};
+  stamp(S, gs, row({1, 2, 3}, {4, 5, 6}), 0.5, 2.0);
+  check(S[1][2] == 2.0 * 2 * 3 && gs[5] == 3.0, "stamp");
+
+  // Hinge rows against central differences of C, for body rotations applied
+  // in the world frame (q <- exp(d) q).  The anchor and axis rows (0-4) are
+  // exact everywhere; the limit rows' +-axis Jacobian is exact where the two
+  // hinge axes coincide, so they are checked on an aligned hinge.
+  auto worstDifference = [](Solver &sim, const Joint &j, int rows) {
+    std::array<double, 7> C{};
+    std::array<V6, 7> JA{}, JB{};
+    sim.evaluateJoint(j, C, JA, JB);
+    double worst = 0;
+    for (int body = 0; body < 2; ++body)
+      for (int dof = 0; dof < 6; ++dof) {
+        const Body saved = sim.bodies[body];
+        std::array<double, 7> plus{}, minus{};
+        std::array<V6, 7> ja{}, jb{};
+        for (int s = -1; s <= 1; s += 2) {
+          Vec3 d{};
+          d[dof % 3] = 1e-6 * s;
+          if (dof < 3)
+            sim.bodies[body].x = saved.x + d;
+          else
+            sim.bodies[body].q = exp(d) * saved.q;
+          sim.evaluateJoint(j, s > 0 ? plus : minus, ja, jb);
+          sim.bodies[body] = saved;
+        }
+        for (int k = 0; k < rows; ++k)
+          worst = std::max(worst, std::abs((plus[k] - minus[k]) / 2e-6 -
+                                           (body == 0 ? JA : JB)[k][dof]));
+      }
+    return worst;
+  };
+  Solver sim;
+  sim.bodies.resize(2);
+  sim.bodies[0].x = {0.1, 0.2, 0.3};
+  sim.bodies[1].x = {-0.2, 0.3, 0.4};
+  sim.bodies[0].q = exp({0.2, -0.3, 0.1});
+  sim.bodies[1].q = exp({-0.4, 0.1, 0.2});
+  Joint j;
+  j.a = 0;
+  j.b = 1;
+  j.ra = {0.03, -0.02, 0.07};
+  j.rb = {-0.01, 0.05, 0.03};
+  j.axisA = {0, 0, 1};
+  j.axisB = {0, 1, 0};
+  j.tangentA = {1, 0, 0};
+  j.tangentB = {1, 0, 0};
+  j.lo = -0.5;
+  j.hi = 0.7;
+  check(worstDifference(sim, j, 5) < 1e-8, "anchor and axis Jacobians match central differences");
+  // aligned: b is a turned 0.3 rad about the hinge axis
+  j.axisB = j.axisA;
+  const Vec3 axisWorld = rotate(sim.bodies[0].q, j.axisA);
+  sim.bodies[1].q = exp(axisWorld * 0.3) * sim.bodies[0].q;
+  check(std::abs(sim.angle(j) - 0.3) < 1e-14, "hinge angle");
+  check(worstDifference(sim, j, 7) < 1e-8, "all seven Jacobians on an aligned hinge");
+  std::array<double, 7> C{};
+  std::array<V6, 7> JA{}, JB{};
+  sim.evaluateJoint(j, C, JA, JB);
+  check(std::abs(C[5] - 0.8) < 1e-14 && std::abs(C[6] - 0.4) < 1e-14, "limit rows");
+  std::printf("math checks passed\n");
+  return 0;
+}
+
+static double distance(const Body &a, const Body &b) { return norm(a.x - b.x); }
+
+static int gpu(const char *model) {
+  Solver original;
+  original.load(model);
+  original.options.dt = 0.005;
+  original.options.iterations = 10;
+  check(original.bodies.size() >= 2 && original.joints.size() >= 1, "model loaded");
+  Batch batch(original, 3);
+  batch.environments[1].bodies[1].v.x = 0.1;
+  for (int i = 0; i < 50; ++i)
+    batch.step();
+  auto &env = batch.environments;
+  check(distance(env[0].bodies[1], env[2].bodies[1]) == 0, "identical environments agree");
+  check(distance(env[0].bodies[1], env[1].bodies[1]) > 1e-7, "a perturbed environment differs");
+  check(distance(env[0].bodies[1], original.bodies[1]) > 1e-6, "the environments moved");
+  const Body reference = env[2].bodies[1];
+  const auto referenceJoints = env[2].joints;
+  batch.reset(0);
+  check(distance(env[0].bodies[1], original.bodies[1]) == 0, "reset restores the file state");
+  check(distance(env[2].bodies[1], reference) == 0, "reset leaves the others");
+  for (int i = 0; i < 50; ++i)
+    env[0].step();
+  check(distance(env[0].bodies[1], reference) == 0 &&
+            norm(env[0].bodies[1].v - reference.v) == 0,
+        "a reset environment replays bit for bit");
+  check(env[0].joints[0].lambda == referenceJoints[0].lambda, "replayed multipliers agree");
+  env[0].load(model);
+  bool zero = true;
+  for (auto &jt : env[0].joints)
+    for (double l : jt.lambda)
+      zero = zero && l == 0;
+  check(zero, "reload clears the multipliers");
+  bool rejected = false;
+  try {
+    Batch invalid(original, 0);
+  } catch (const std::exception &) {
+    rejected = true;
+  }
+  check(rejected, "an empty batch is rejected");
+  // options the device step does not run are refused, not ignored
+  Solver changed = original;
+  changed.options.alpha = 0.5;
+  rejected = false;
+  try {
+    changed.step();
+  } catch (const std::invalid_argument &) {
+    rejected = true;
+  }
+  check(rejected, "unsupported options rejected");
+  std::printf("gpu checks passed: %s\n", model);
+  return 0;
+}
+
+// One environment stepped STEPS times (dt 5 ms, 10 iterations, the file's
+// controls); prints "step body x y z qw qx qy qz" for every body after every
+// step, full precision.
+static int trace(const char *model, int steps) {
+  Solver sim;
+  sim.load(model);
+  sim.options.dt = 0.005;
+  sim.options.iterations = 10;
+  for (int s = 1; s <= steps; ++s) {
+    sim.step();
+    for (size_t b = 0; b < sim.bodies.size(); ++b) {
+      const Body &x = sim.bodies[b];
+      std::printf("%d %zu %.17g %.17g %.17g %.17g %.17g %.17g %.17g\n", s, b, x.x.x, x.x.y,
+                  x.x.z, x.q.w, x.q.x, x.q.y, x.q.z);
+    }
+  }
+  return 0;
+}
+
+int main(int argc, char **argv) {
+  try {
+    if (argc >= 2 && std::strcmp(argv[1], "math") == 0)
+      return math();
+    if (argc >= 3 && std::strcmp(argv[1], "gpu") == 0)
+      return gpu(argv[2]);
+    if (argc >= 4 && std::strcmp(argv[1], "trace") == 0)
+      return trace(argv[2], std::atoi(argv[3]));
+    std::fprintf(stderr, "usage: solver_api_test math | gpu MODEL | trace MODEL STEPS\n");
+    return 2;
+  } catch (const std::exception &e) {
+    std::fprintf(stderr, "FAILED: %s\n", e.what());
+    return 1;
+  }
+}
