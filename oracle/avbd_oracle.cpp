@@ -1407,22 +1407,25 @@ void *oracle_create(const char *path, double dt, int iterations, int fp64, int m
     fail(!(dt > 0) || !std::isfinite(dt) || iterations < 1, "Invalid batch parameters");
     fail(mode != 0 && mode != 1, "Unknown oracle mode");
     ModelFile file = parse(path);
+    // owned until every step has succeeded (a rejected model frees it)
+    std::unique_ptr<Handle> made;
     if (fp64) {
-      auto *h = new HandleT<double>();
+      auto h = std::make_unique<HandleT<double>>();
       h->model = flatten<double>(file, dt, iterations, mode);
       h->env.initialize(h->model);
       h->env.mode = mode;
-      out = h;
+      made = std::move(h);
     } else {
-      auto *h = new HandleT<float>();
+      auto h = std::make_unique<HandleT<float>>();
       h->model = flatten<float>(file, dt, iterations, mode);
       h->env.initialize(h->model);
       h->env.mode = mode;
-      out = h;
+      made = std::move(h);
     }
-    out->fp64 = fp64;
-    out->nb = file.bodies.size();
-    out->nj = file.joints.size();
+    made->fp64 = fp64;
+    made->nb = file.bodies.size();
+    made->nj = file.joints.size();
+    out = made.release();
   });
   return out;
 }
