@@ -12,6 +12,9 @@ reward and termination assembly, evaluated on a state snapshot
   step_outputs       tensor_env.py:294-327, 358-368 (failure, reward, returns,
                      counters, timeouts)
   targets            tensor_env.py:279-285, 331-335
+  gait_reference     tensor_env.py:260-277 (gait=True)
+  foot_clearance_penalty, load_transfer_penalty
+                     tensor_env.py:338-357 (the gait-table reward terms)
 
 Pinned by tests/test_task_oracle.py against independent rotation matrices
 (scipy), closed-form states (upright, pure tilt, pure yaw, known local
@@ -117,3 +120,53 @@ def step_outputs(kind, bodies, joints, diag, action, last_action, meta, *, contr
     new_episode = np.asarray(episode) + 1
     timeout = (new_episode >= max_episode_length) & ~failed
     return failed, reward, new_episode, timeout, failed | timeout, new_filtered
+
+
+GAIT_DIRECTIONS = np.array([[1.0, 0], [-1, 0], [0, 1], [0, -1]])
+
+
+def gait_reference(episode, commands, table, period, home, control_dt):
+    """Servo reference with the gait table (tensor_env.py:260-277): the table
+    row of the direction the command points to most ([4, count, J]: forward,
+    backward, left, right), linearly interpolated at phase
+    episode * control_dt / period (wrapping from the last node to the first),
+    blended in from HOME over the first second of the episode."""
+    episode = np.asarray(episode, dtype=np.float64)
+    count = table.shape[1]
+    index = (episode * control_dt / period % 1) * count
+    lo = np.floor(index).astype(int)
+    frac = (index - lo)[:, None]
+    d = np.argmax(np.asarray(commands) @ GAIT_DIRECTIONS.T, axis=-1)
+    ref = table[d, lo] * (1 - frac) + table[d, (lo + 1) % count] * frac
+    blend = np.clip(episode * control_dt, 0, 1)[:, None]
+    return home + (ref - home) * blend
+
+
+def foot_clearance_penalty(bodies, foot_bodies, foot_points, episode_after, control_dt,
+                           period, lift):
+    """Foot-clearance term (tensor_env.py:338-351), before the control_dt
+    factor: -20000 sum over both feet of (max(0, h) - desired)^2, with h the
+    lowest of the foot's points (body frame [2, V, 3]) above the ground and
+    desired = lift sin^2(pi s), s = clip((phase - 0.6) / 0.4, 0, 1), phase the
+    gait phase after the step (the right foot's half a period later)."""
+    poses = bodies[:, foot_bodies]
+    up = np.broadcast_to(np.array([0.0, 0, 1]), poses[:, :, :3].shape)
+    local_up = inverse_rotate(poses[:, :, 3:7], up)
+    heights = (local_up[:, :, None, :] * foot_points[None]).sum(-1) + poses[:, :, None, 2]
+    clearance = heights.min(-1)
+    phase = (np.asarray(episode_after, float)[:, None] * control_dt / period
+             + np.array([0.0, 0.5])) % 1
+    swing = np.clip((phase - 0.6) / 0.4, 0, 1)
+    desired = lift * np.sin(np.pi * swing) ** 2
+    return -20000 * ((np.maximum(clearance, 0) - desired) ** 2).sum(-1)
+
+
+def load_transfer_penalty(foot_forces_z, total_mass, episode_after, control_dt, period):
+    """Load-transfer term (tensor_env.py:352-357), before the control_dt
+    factor: -3 sum over both feet of (clip(F_z / (m g), 0, 3) - wanted)^2,
+    wanted = (l, 1 - l), l = 1/2 + sin(2 pi (cycle - 0.05)) / 2."""
+    forces = np.asarray(foot_forces_z, float) / (total_mass * 9.81)
+    cycle = np.asarray(episode_after, float) * control_dt / period
+    left = 0.5 + 0.5 * np.sin(2 * np.pi * (cycle - 0.05))
+    wanted = np.stack((left, 1 - left), axis=-1)
+    return -3 * ((np.clip(forces, 0, 3) - wanted) ** 2).sum(-1)

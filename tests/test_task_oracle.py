@@ -184,3 +184,79 @@ def test_targets_clamp():
     assert target[0, 0] == upper[0] and target[0, 1] == lower[1]
     a, target = T.targets(np.zeros((1, J)), HOME_V, lower, upper, 0.3)
     assert np.array_equal(target[0], HOME_V)
+
+
+# ------------------------------------------------------- gait-table terms
+def test_gait_reference_closed_forms():
+    """Nodes of the table are reached exactly at their phases (after the
+    first second's blend), midway between nodes gives the mean of the two,
+    the last node interpolates towards the first, the command selects the
+    direction, and the first control step is HOME."""
+    J, count, period, dt = 3, 5, 0.8, 0.02
+    home = np.array([0.1, -0.2, 0.3])
+    table = np.arange(4 * count * J, dtype=float).reshape(4, count, J) / 10
+    speed = 0.05
+    commands = np.array([[speed, 0], [-speed, 0], [0, speed], [0, -speed]])
+    # 80 steps = 1.6 s = 2 periods: phase 0, node 0; every direction
+    ep = np.full(4, 80)
+    ref = T.gait_reference(ep, commands, table, period, home, dt)
+    assert np.allclose(ref, table[[0, 1, 2, 3], 0])
+    # 88 steps: phase 0.2 -> node 1 exactly (count 5)
+    ref = T.gait_reference(np.array([88]), commands[2:3], table, period, home, dt)
+    assert np.allclose(ref[0], table[2, 1])
+    # 90 steps: phase 0.25 -> index 1.25; 92: 1.5 -> mean of nodes 1 and 2
+    ref = T.gait_reference(np.array([92]), commands[:1], table, period, home, dt)
+    assert np.allclose(ref[0], (table[0, 1] + table[0, 2]) / 2)
+    # phase 0.9 -> index 4.5: between the last node and the first
+    ref = T.gait_reference(np.array([116]), commands[3:], table, period, home, dt)
+    assert np.allclose(ref[0], (table[3, 4] + table[3, 0]) / 2)
+    # first step HOME; after half a second half way from HOME (phase 0.625 -> 3.125)
+    assert np.allclose(T.gait_reference(np.array([0]), commands[:1], table, period, home, dt),
+                       home)
+    ref = T.gait_reference(np.array([25]), commands[:1], table, period, home, dt)
+    node = table[0, 3] * 0.875 + table[0, 4] * 0.125
+    assert np.allclose(ref[0], home + (node - home) * 0.5)
+
+
+def _foot_bodies(z_left, z_right, tilt=0.0):
+    bodies = np.zeros((1, 3, 13))
+    bodies[0, :, 3] = 1
+    bodies[0, 1, 2], bodies[0, 2, 2] = z_left, z_right
+    if tilt:
+        bodies[0, 1, 3:7] = [np.cos(tilt / 2), np.sin(tilt / 2), 0, 0]
+    return bodies
+
+
+def test_foot_clearance_closed_forms():
+    """A foot's clearance is its lowest point's height; in stance (phase <
+    0.6) the desired height is zero, at mid-swing (phase 0.8) it is the lift,
+    and the two feet are half a period apart."""
+    points = np.array([[[0.01, 0, -0.006], [-0.01, 0, -0.004]]] * 2)
+    period, dt, lift = 1.0, 0.01, 0.008
+    # left foot phase 0.3 (stance), right 0.8 (mid-swing)
+    pen = T.foot_clearance_penalty(_foot_bodies(0.016, 0.020, 0), [1, 2], points, [30], dt,
+                                   period, lift)
+    clear_left, clear_right = 0.016 - 0.006, 0.020 - 0.006
+    assert np.isclose(pen[0], -20000 * (clear_left ** 2 + (clear_right - lift) ** 2))
+    # below the ground counts as zero clearance
+    pen = T.foot_clearance_penalty(_foot_bodies(0.002, 0.0, 0), [1, 2], points, [30], dt,
+                                   period, lift)
+    assert np.isclose(pen[0], -20000 * lift ** 2)
+    # a foot rolled by 90 degrees about x: its points' z offsets become -y offsets
+    rolled = np.array([[[0.0, 0.01, 0.0], [0.0, -0.01, 0.0]]] * 2)
+    pen = T.foot_clearance_penalty(_foot_bodies(0.05, 0.0, np.pi / 2), [1, 2], rolled, [30],
+                                   dt, period, lift)
+    assert np.isclose(pen[0], -20000 * ((0.05 - 0.01) ** 2 + lift ** 2))
+
+
+def test_load_transfer_closed_forms():
+    """Weight split as the cycle asks costs nothing; cycle 0.3 wants
+    (1, 0) -- all weight on the left foot; forces are clipped to 3 m g."""
+    mass, period, dt = 0.8, 1.0, 0.01
+    mg = mass * 9.81
+    assert np.isclose(T.load_transfer_penalty([[mg, 0.0]], mass, [30], dt, period)[0], 0)
+    assert np.isclose(T.load_transfer_penalty([[0.0, mg]], mass, [30], dt, period)[0], -6)
+    assert np.isclose(T.load_transfer_penalty([[10 * mg, -mg]], mass, [30], dt, period)[0],
+                      -3 * (2 ** 2 + 0))
+    # cycle 0.05: half the weight on each foot
+    assert np.isclose(T.load_transfer_penalty([[mg / 2, mg / 2]], mass, [5], dt, period)[0], 0)
