@@ -47,6 +47,17 @@ _INSTRUCTION = re.compile(r"^\s+(\S+)\s*(.*?)\s*//\s*([0-9A-Fa-f]+):")
 _TARGET = re.compile(r"<([^>+]+)\+0x([0-9a-f]+)>")
 
 
+def _offset(pc, n, word, operand):
+    """Record a literal half of the offset added to the address that
+    s_getpc_b64 left in s[n:n+1]; an added register makes the address
+    unknown, so the pair is no longer followed (a jump through it then adds
+    no target, which can only report more, never less)."""
+    try:
+        pc[n][word] = int(operand, 0) & 0xFFFFFFFF
+    except ValueError:
+        pc.pop(n)
+
+
 def exec_zero_writes(text: str):
     """(function, address, instruction) of every vector or memory instruction
     reached only by falling through `s_cbranch_execnz` (exec is zero there)
@@ -76,9 +87,9 @@ def exec_zero_writes(text: str):
             n = int(re.match(r"s\[(\d+):", regs[0]).group(1))
             pc[n] = [address + 4, 0, 0]
         elif op == "s_add_u32" and regs[0] == regs[1] and int(regs[0][1:]) in pc:
-            pc[int(regs[0][1:])][1] = int(regs[2], 0) & 0xFFFFFFFF
+            _offset(pc, int(regs[0][1:]), 1, regs[2])
         elif op == "s_addc_u32" and regs[0] == regs[1] and int(regs[0][1:]) - 1 in pc:
-            pc[int(regs[0][1:]) - 1][2] = int(regs[2], 0) & 0xFFFFFFFF
+            _offset(pc, int(regs[0][1:]) - 1, 2, regs[2])
         elif op == "s_setpc_b64":
             n = int(re.match(r"s\[(\d+):", regs[0]).group(1))
             if n in pc:

@@ -175,27 +175,48 @@ template <class S> __device__ void storeEnv(S *dst, const S &src, int lane, int 
   copyWords<4>(d, s, scStart, scStart + src.nsc * scWords, lane, L);
 }
 
-// MPR narrow phase between two shapes (convex.cuh:124-217), one lane.
-template <class R> struct MprQuery {
+// MPR narrow phase between two shapes (convex.cuh:124-217), one lane.  The
+// shape data come from the workgroup's staged copy (Frames: type, staged
+// points or sphere/capsule data, interior point, radius); only point sets
+// of more than kCachedPoints points are read from the model's point array.
+template <class R, int B, int J> struct MprQuery {
+  const Frames<R, B, J> &F;
   const DeviceModel<R> &M;
   const V3<R> *points;
   int sa, sb;
   V3<R> xa, xb;
   Q4<R> qa, qb;
   R inflation;
-  DUCK_HD V3<R> support1(int s, V3<R> x, Q4<R> q, V3<R> dir, R infl) const {
+  __device__ V3<R> staged(int k, int s) const { return V3<R>{F.spt[k][0][s], F.spt[k][1][s], F.spt[k][2][s]}; }
+  __device__ V3<R> support1(int s, V3<R> x, Q4<R> q, V3<R> dir, R infl) const {
     V3<R> ld = rotate(conj(q), dir), local;
-    int type = M.stype[s];
-    V3<R> c{M.center[0][s], M.center[1][s], M.center[2][s]};
+    const int flags = F.sflags[s], type = flags >> 4;
     if (type == 0 || type == 2) {
-      local = c + unitOrNan(ld) * M.size[0][s];
+      local = staged(0, s) + unitOrNan(ld) * F.spt[1][0][s];
       if (type == 2) {
-        Q4<R> sq{M.sq[0][s], M.sq[1][s], M.sq[2][s], M.sq[3][s]};
-        V3<R> axis = rotate(sq, V3<R>{0, 0, 1});
-        local = local + axis * (dot(axis, ld) >= 0 ? M.size[1][s] : -M.size[1][s]);
+        const V3<R> axis = staged(2, s);
+        local = local + axis * (dot(axis, ld) >= 0 ? F.spt[1][1][s] : -F.spt[1][1][s]);
       }
+    } else if (flags & 2) {
+      // every staged slot loaded at once (slots past the count hold zeros
+      // and are never chosen), then the first maximum in index order
+      const int n = F.scount[s];
+      R cand[kCachedPoints];
+#pragma unroll
+      for (int i = 0; i < kCachedPoints; ++i)
+        cand[i] = dot(staged(i, s), ld);
+      R value = R(-INFINITY);
+      int best = 0;
+#pragma unroll
+      for (int i = 0; i < kCachedPoints; ++i) {
+        if (i < n && cand[i] > value) {
+          value = cand[i];
+          best = i;
+        }
+      }
+      local = staged(best, s);
     } else {
-      int best = -1, off = M.soffset[s], n = M.scount[s];
+      int best = -1, off = M.soffset[s], n = F.scount[s];
       R value = R(-INFINITY);
       for (int i = 0; i < n; ++i) {
         R cand = dot(points[off + i], ld);
@@ -211,7 +232,7 @@ template <class R> struct MprQuery {
   struct SP {
     V3<R> v, a, b;
   };
-  DUCK_HD SP support(V3<R> dir) const {
+  __device__ SP support(V3<R> dir) const {
     SP p;
     p.a = support1(sa, xa, qa, dir, inflation / R(2));
     p.b = support1(sb, xb, qb, -dir, inflation / R(2));
@@ -253,20 +274,20 @@ template <class R> DUCK_HD V3<R> closestToOrigin(V3<R> a, V3<R> b, V3<R> c) {
 
 // The portal is four named points (p0 the interior point) whose updates are
 // selected, never addressed: an indexed array here became scratch memory.
-template <class R> DUCK_HD MprHit<R> mprContact(const MprQuery<R> &Qy, R tolerance) {
-  using SP = typename MprQuery<R>::SP;
+template <class R, class Query> __device__ MprHit<R> mprContact(const Query &Qy, R tolerance) {
+  using SP = typename Query::SP;
   auto pick = [](bool c, const SP &x, const SP &y) {
     return SP{c ? x.v : y.v, c ? x.a : y.a, c ? x.b : y.b};
   };
   MprHit<R> hit{0, {0, 0, 0}, {0, 0, 0}, 0};
   SP p0, p1, p2, p3;
-  const auto &M = Qy.M;
-  V3<R> ia{M.interior[0][Qy.sa], M.interior[1][Qy.sa], M.interior[2][Qy.sa]};
-  V3<R> ib{M.interior[0][Qy.sb], M.interior[1][Qy.sb], M.interior[2][Qy.sb]};
+  const auto &F = Qy.F;
+  V3<R> ia{F.sinterior[0][Qy.sa], F.sinterior[1][Qy.sa], F.sinterior[2][Qy.sa]};
+  V3<R> ib{F.sinterior[0][Qy.sb], F.sinterior[1][Qy.sb], F.sinterior[2][Qy.sb]};
   p0.a = Qy.xa + rotate(Qy.qa, ia);
   p0.b = Qy.xb + rotate(Qy.qb, ib);
   p0.v = p0.a - p0.b;
-  R size = mx(R(0.001), M.radius[Qy.sa] + M.radius[Qy.sb]);
+  R size = mx(R(0.001), F.sradius[Qy.sa] + F.sradius[Qy.sb]);
   R eps = tolerance * R(0.01);
   if (norm(p0.v) < eps)
     p0.v.x += eps * R(10);
@@ -468,19 +489,36 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
   }
   for (int i = t; i < ns; i += 64) {
     F.sbody[i] = M.sbody[i];
-    F.sflags[i] = M.sflags[i];
+    F.sflags[i] = M.sflags[i] | M.stype[i] << 4;
     F.scount[i] = M.scount[i];
     F.sradius[i] = M.radius[i];
+#pragma unroll
+    for (int k = 0; k < 3; ++k)
+      F.sinterior[k][i] = M.interior[k][i];
   }
+  for (int i = t; i < np; i += 64)
+    F.pair[i] = M.pa[i] | M.pb[i] << 8;
   for (int i = t; i < kCachedPoints * 3 * ns; i += 64) {
     const int si = i % ns, c = (i / ns) % 3, k = i / (3 * ns);
-    F.spt[k][c][si] = M.spts[k][c][si];
+    const int type = M.stype[si];
+    R v = M.spts[k][c][si];
+    if (type == 0 || type == 2) {
+      // the shape formula's data, in the operations the narrow phase used
+      // to evaluate on each support query
+      const Q4<R> sq{M.sq[0][si], M.sq[1][si], M.sq[2][si], M.sq[3][si]};
+      v = k == 0   ? M.center[c][si]
+          : k == 1 ? (c < 2 ? M.size[c][si] : R(0))
+          : k == 2 ? comp(rotate(sq, V3<R>{0, 0, 1}), c)
+                   : R(0);
+    }
+    F.spt[k][c][si] = v;
   }
   if (t < 3)
     F.colorStart[t] = M.colorStart[t];
 
   State *gs = valid ? &blobAt<State>(args.states, args.blobBytes, e) : nullptr;
   static_assert(L >= 4, "blob copies give each of the first three lanes an end word");
+  static_assert(CS <= B, "the staged pair table holds B pairs");
   if (valid)
     loadEnv<State>(E.s, gs, lane, L);
   __syncthreads();
@@ -597,16 +635,16 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
       if (!active || pi >= np)
         continue;
       E.pairHit[pi] = 0;
-      const int sa = M.pa[pi], sb = M.pb[pi], A = M.sbody[sa], Bb = M.sbody[sb];
+      const int sa = F.pair[pi] & 255, sb = F.pair[pi] >> 8, A = F.sbody[sa], Bb = F.sbody[sb];
       if (E.s.mass[A] == 0 && E.s.mass[Bb] == 0)
         continue;
       V3<R> xa = stp.X(A), xb = stp.X(Bb);
       Q4<R> qa = stp.Q(A), qb = stp.Q(Bb);
-      R skin = R(.003) + h * (norm(stp.Vel(A) - stp.Vel(Bb)) + norm(stp.Omega(A)) * M.radius[sa] +
-                              norm(stp.Omega(Bb)) * M.radius[sb]);
-      if (norm(xa - xb) > M.radius[sa] + M.radius[sb] + skin)
+      R skin = R(.003) + h * (norm(stp.Vel(A) - stp.Vel(Bb)) + norm(stp.Omega(A)) * F.sradius[sa] +
+                              norm(stp.Omega(Bb)) * F.sradius[sb]);
+      if (norm(xa - xb) > F.sradius[sa] + F.sradius[sb] + skin)
         continue;
-      MprQuery<R> qy{M, points, sa, sb, xa, xb, qa, qb, skin};
+      MprQuery<R, B, J> qy{F, M, points, sa, sb, xa, xb, qa, qb, skin};
       MprHit<R> hit = mprContact(qy, mx(R(1e-8), M.tolerance * R(.1)));
       if (hit.status < 0) {
         E.s.failed = 1;
@@ -912,9 +950,9 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
           continue;
         }
         const PairGeom &o = pg[r];
-        const int sa = M.pa[pi], sb = M.pb[pi];
+        const int sa = F.pair[pi] & 255, sb = F.pair[pi] >> 8;
         SelfContact<R> c;
-        c.id = scPack(M.sbody[sa], M.sbody[sb], sa, sb, false);
+        c.id = scPack(F.sbody[sa], F.sbody[sb], sa, sb, false);
         R lam[3] = {0, 0, 0}, pen[3] = {1000, 1000, 1000};
         if (o.src >= 0) {
           for (int d = 0; d < 3; ++d) {
@@ -944,45 +982,64 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
     int pairHits = 0;
     for (int pi = 0; pi < np; ++pi)
       pairHits += E.pairHit[pi];
-    if (active && pairHits == 0 && defaultSchedule) {
+    const bool fresh = active && !(pairHits == 0 && defaultSchedule);
+    if (active) {
       for (int b = lane; b < nb; b += L) {
         E.s.colors[b] = M.colors[b];
-        E.order[b] = F.order[b];
+        if (!fresh)
+          E.order[b] = F.order[b];
       }
-      if (lane < 3)
+      if (!fresh && lane < 3)
         E.colorStart[lane] = F.colorStart[lane];
       if (lane < 8)
         E.stepDiag[lane] = 0;
-      if (lane == 0) {
+      if (!fresh && lane == 0) {
         E.s.nsc = 0;
         E.s.colorCount = 2;
       }
-    } else if (active && lane == 0) {
-      int nsc = pairHits;
-      E.s.nsc = nsc < CS ? nsc : CS;
-      for (int b = 0; b < nb; ++b)
-        E.s.colors[b] = M.colors[b];
+    }
+    __syncthreads();
+    if (fresh && lane == 0) {
+      // each body contact between bodies of one colour gives its second
+      // body a new colour, in list order (later contacts see the change)
+      const int nsc = pairHits < CS ? pairHits : CS;
+      E.s.nsc = nsc;
       int cc = 2;
-      for (int i = 0; i < E.s.nsc; ++i) {
+      for (int i = 0; i < nsc; ++i) {
         int a = scBody(E.s.sc[i].id), b = scOther(E.s.sc[i].id);
         if (E.s.mass[a] > 0 && E.s.mass[b] > 0 && E.s.colors[a] == E.s.colors[b])
           E.s.colors[b] = cc++;
       }
       E.s.colorCount = cc;
-      for (int c = 0; c <= cc; ++c)
-        E.colorStart[c] = 0;
-      for (int b = 0; b < nb; ++b)
-        if (E.s.mass[b] > 0)
-          E.colorStart[E.s.colors[b] + 1] += 1;
-      for (int c = 0; c < cc; ++c)
-        E.colorStart[c + 1] += E.colorStart[c];
-      int pos = 0;
-      for (int c = 0; c < cc; ++c)
-        for (int b = 0; b < nb; ++b)
-          if (E.s.mass[b] > 0 && E.s.colors[b] == c)
-            E.order[pos++] = b;
-      for (int k = 0; k < 8; ++k)
-        E.stepDiag[k] = 0;
+    }
+    __syncthreads();
+    // The fresh schedule: the dynamic bodies of each colour in index order,
+    // placed by ballots over the environment's lanes (body b = lane + r L).
+    const int freshColours = __builtin_amdgcn_readfirstlane(waveMaxInt(fresh ? E.s.colorCount : 0));
+    if (freshColours > 0) {
+      constexpr int BR = (B + L - 1) / L;
+      const uint64_t group = (L == 64 ? ~uint64_t(0) : (uint64_t(1) << L) - 1) << (g * L);
+      int col[BR];
+#pragma unroll
+      for (int r = 0; r < BR; ++r) {
+        const int b = lane + r * L;
+        col[r] = fresh && b < nb && E.s.mass[b] > 0 ? E.s.colors[b] : -1;
+      }
+      int start = 0;
+      for (int c = 0; c <= freshColours; ++c) {
+        if (fresh && lane == 0)
+          E.colorStart[c] = start;
+        if (c == freshColours)
+          break;
+#pragma unroll
+        for (int r = 0; r < BR; ++r) {
+          const uint64_t m = __ballot(col[r] == c) & group;
+          const int below = __builtin_amdgcn_mbcnt_hi(uint32_t(m >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(m), 0));
+          if (col[r] == c)
+            E.order[start + below] = lane + r * L;
+          start += __popcll(m);
+        }
+      }
     }
     __syncthreads();
     if (active && E.s.failed)

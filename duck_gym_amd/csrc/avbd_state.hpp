@@ -73,10 +73,16 @@ template <class R, int B, int J> struct Frames {
   // Colour schedule without body-body contacts (model colours, bodies of
   // non-zero model mass in index order within each colour).
   int order[B], colorStart[3];
-  // Ground-detection data per shape (shapes <= B) and model masses.
+  // Detection data per shape (shapes <= B) and model masses.  sflags: the
+  // model's bits (1 ground contact, 2 staged point set) | shape type << 4.
+  // spt holds the points of a staged point set; a sphere or capsule has no
+  // points and holds its centre (spt[0]), radius and half length (spt[1]
+  // [0..1]) and capsule axis (spt[2]) there instead.
   int sbody[B], sflags[B], scount[B];
   R sradius[B], mass[B];
   R spt[kCachedPoints][3][B];
+  R sinterior[3][B];
+  int pair[B]; // body-contact pairs: shape a | shape b << 8 (pairs <= B)
 };
 
 // Ground contact (normal = +z, anchor on the plane).  id packs

@@ -58,6 +58,19 @@ def test_lane_addressed_instructions_and_branch_targets_are_fine():
         "v_cndmask_b32_e64 v2, 0, 1, s[4:5]"]
 
 
+def test_address_plus_register_is_not_followed():
+    # s_getpc followed by a register offset (a table address, say) has no
+    # known value: no jump target is taken from it, and reading it does not
+    # fail
+    text = _asm(LOOP + ["s_getpc_b64 s[12:13]", "s_add_u32 s12, s12, s14",
+                        "s_addc_u32 s13, s13, 0", "s_setpc_b64 s[12:13]",
+                        "v_mov_b32_e32 v2, v1", "s_endpgm"])
+    assert C.exec_zero_writes(text) == []
+    text = _asm(LOOP + ["s_getpc_b64 s[12:13]", "s_add_u32 s12, s12, s14",
+                        "v_mov_b32_e32 v2, v1", "s_or_b64 exec, exec, s[4:5]", "s_endpgm"])
+    assert [f[2] for f in C.exec_zero_writes(text)] == ["v_mov_b32_e32 v2, v1"]
+
+
 @pytest.mark.skipif(not (C.LLVM_BIN / "llvm-objdump").exists(), reason="llvm-objdump absent")
 def test_built_library_has_no_vector_writes_with_exec_zero():
     library = Path(__file__).resolve().parents[1] / "duck_gym_amd" / "libduck_hip.so"
