@@ -19,6 +19,21 @@ template <int N> __device__ __forceinline__ double rowRor(double v) {
 
 // Maximum over the L lanes of an environment, on every one of them.  For
 // L == 16 (one DPP row) four row rotations replace the LDS-crossbar shuffles.
+// c ? a : b on copies: a conditional on two lvalues of a struct type selects
+// between their addresses, which keeps the object they belong to in memory.
+template <class T> __device__ __forceinline__ T pickValue(bool c, T a, T b) { return c ? a : b; }
+
+// The value of lane ^ 1 (DPP quad_perm [1, 0, 3, 2]).
+__device__ __forceinline__ float laneSwap1(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));
+}
+__device__ __forceinline__ double laneSwap1(double v) {
+  const long long b = __double_as_longlong(v);
+  const int lo = __builtin_amdgcn_mov_dpp(int(b), 0xB1, 0xF, 0xF, false);
+  const int hi = __builtin_amdgcn_mov_dpp(int(b >> 32), 0xB1, 0xF, 0xF, false);
+  return __longlong_as_double((static_cast<long long>(hi) << 32) | static_cast<unsigned>(lo));
+}
+
 template <class T> __device__ __forceinline__ T swizzle16(T v);
 template <> __device__ __forceinline__ int swizzle16(int v) {
   return __builtin_amdgcn_ds_swizzle(v, 0x401F); // lane ^ 16 within 32-lane groups
@@ -175,11 +190,14 @@ template <class S> __device__ void storeEnv(S *dst, const S &src, int lane, int 
   copyWords<4>(d, s, scStart, scStart + src.nsc * scWords, lane, L);
 }
 
-// MPR narrow phase between two shapes (convex.cuh:124-217), one lane.  The
-// shape data come from the workgroup's staged copy (Frames: type, staged
-// points or sphere/capsule data, interior point, radius); only point sets
-// of more than kCachedPoints points are read from the model's point array.
-template <class R, int B, int J> struct MprQuery {
+// MPR narrow phase between two shapes (convex.cuh:124-217).  The shape data
+// come from the workgroup's staged copy (Frames: type, staged points or
+// sphere/capsule data, interior point, radius); only point sets of more than
+// kCachedPoints points are read from the model's point array.  With MQ == 2
+// a query runs on two adjacent lanes (2k, 2k + 1): each evaluates the support
+// point of one shape and the two exchange them, so both hold the same
+// support point and run the same portal steps on the same values.
+template <class R, int B, int J, int MQ> struct MprQuery {
   const Frames<R, B, J> &F;
   const DeviceModel<R> &M;
   const V3<R> *points;
@@ -187,8 +205,65 @@ template <class R, int B, int J> struct MprQuery {
   V3<R> xa, xb;
   Q4<R> qa, qb;
   R inflation;
-  __device__ V3<R> staged(int k, int s) const { return V3<R>{F.spt[k][0][s], F.spt[k][1][s], F.spt[k][2][s]}; }
-  __device__ V3<R> support1(int s, V3<R> x, Q4<R> q, V3<R> dir, R infl) const {
+  bool second; // MQ == 2: this lane evaluates shape b's support
+  // MQ == 2: the lane's own shape (index, flags, point count, pose and its
+  // staged slots), read once per query so that a support point is register
+  // work.
+  int ownS = 0, ownFlags = 0, ownCount = 0;
+  V3<R> ownX{}, ownPts[MQ == 2 ? kCachedPoints : 1];
+  Q4<R> ownQ{};
+  __device__ __forceinline__ V3<R> staged(int k, int s) const { return V3<R>{F.spt[k][0][s], F.spt[k][1][s], F.spt[k][2][s]}; }
+  __device__ __forceinline__ void loadOwn() {
+    if constexpr (MQ == 2) {
+      ownS = second ? sb : sa;
+      ownFlags = F.sflags[ownS];
+      ownCount = F.scount[ownS];
+      ownX = pickValue(second, xb, xa);
+      ownQ = pickValue(second, qb, qa);
+#pragma unroll
+      for (int i = 0; i < kCachedPoints; ++i)
+        ownPts[i] = staged(i, ownS);
+    }
+  }
+  // support1 of the lane's own shape, from the registers loadOwn filled (a
+  // sphere or capsule holds its centre, radius and half length, and axis in
+  // slots 0, 1 and 2, as staged)
+  __device__ __forceinline__ V3<R> supportOwn(V3<R> dir, R infl) const {
+    V3<R> ld = rotate(conj(ownQ), dir), local;
+    const int type = ownFlags >> 4;
+    if (type == 0 || type == 2) {
+      local = ownPts[0] + unitOrNan(ld) * ownPts[1].x;
+      if (type == 2) {
+        const V3<R> axis = ownPts[2];
+        local = local + axis * (dot(axis, ld) >= 0 ? ownPts[1].y : -ownPts[1].y);
+      }
+    } else if (ownFlags & 2) {
+      R value = R(-INFINITY);
+      local = ownPts[0];
+#pragma unroll
+      for (int i = 0; i < kCachedPoints; ++i) {
+        const R cand = dot(ownPts[i], ld);
+        if (i < ownCount && cand > value) {
+          value = cand;
+          local = ownPts[i];
+        }
+      }
+    } else {
+      int best = -1;
+      const int off = M.soffset[ownS];
+      R value = R(-INFINITY);
+      for (int i = 0; i < ownCount; ++i) {
+        R cand = dot(points[off + i], ld);
+        if (cand > value) {
+          best = i;
+          value = cand;
+        }
+      }
+      local = points[off + (best < 0 ? 0 : best)];
+    }
+    return (ownX + rotate(ownQ, local)) + dir * infl;
+  }
+  __device__ __forceinline__ V3<R> support1(int s, V3<R> x, Q4<R> q, V3<R> dir, R infl) const {
     V3<R> ld = rotate(conj(q), dir), local;
     const int flags = F.sflags[s], type = flags >> 4;
     if (type == 0 || type == 2) {
@@ -229,14 +304,25 @@ template <class R, int B, int J> struct MprQuery {
     }
     return (x + rotate(q, local)) + dir * infl;
   }
+  // A support point of the Minkowski difference: v = a - b, and s = a + b
+  // (the two shapes' points enter the contact position only as their sum).
   struct SP {
-    V3<R> v, a, b;
+    V3<R> v, s;
   };
-  __device__ SP support(V3<R> dir) const {
+  __device__ __forceinline__ SP support(V3<R> dir) const {
     SP p;
-    p.a = support1(sa, xa, qa, dir, inflation / R(2));
-    p.b = support1(sb, xb, qb, -dir, inflation / R(2));
-    p.v = p.a - p.b;
+    V3<R> a, b;
+    if constexpr (MQ == 2) {
+      const V3<R> mine = supportOwn(second ? -dir : dir, inflation / R(2));
+      const V3<R> other{laneSwap1(mine.x), laneSwap1(mine.y), laneSwap1(mine.z)};
+      a = pickValue(second, other, mine);
+      b = pickValue(second, mine, other);
+    } else {
+      a = support1(sa, xa, qa, dir, inflation / R(2));
+      b = support1(sb, xb, qb, -dir, inflation / R(2));
+    }
+    p.v = a - b;
+    p.s = a + b;
     return p;
   }
 };
@@ -274,19 +360,21 @@ template <class R> DUCK_HD V3<R> closestToOrigin(V3<R> a, V3<R> b, V3<R> c) {
 
 // The portal is four named points (p0 the interior point) whose updates are
 // selected, never addressed: an indexed array here became scratch memory.
-template <class R, class Query> __device__ MprHit<R> mprContact(const Query &Qy, R tolerance) {
+template <class R, class Query> __device__ __forceinline__ MprHit<R> mprContact(const Query &Qy, R tolerance) {
   using SP = typename Query::SP;
-  auto pick = [](bool c, const SP &x, const SP &y) {
-    return SP{c ? x.v : y.v, c ? x.a : y.a, c ? x.b : y.b};
+  auto pick = [](bool c, const SP &x, const SP &y) __attribute__((always_inline)) {
+    return SP{c ? x.v : y.v, c ? x.s : y.s};
   };
   MprHit<R> hit{0, {0, 0, 0}, {0, 0, 0}, 0};
   SP p0, p1, p2, p3;
   const auto &F = Qy.F;
   V3<R> ia{F.sinterior[0][Qy.sa], F.sinterior[1][Qy.sa], F.sinterior[2][Qy.sa]};
   V3<R> ib{F.sinterior[0][Qy.sb], F.sinterior[1][Qy.sb], F.sinterior[2][Qy.sb]};
-  p0.a = Qy.xa + rotate(Qy.qa, ia);
-  p0.b = Qy.xb + rotate(Qy.qb, ib);
-  p0.v = p0.a - p0.b;
+  {
+    const V3<R> a = Qy.xa + rotate(Qy.qa, ia), b = Qy.xb + rotate(Qy.qb, ib);
+    p0.v = a - b;
+    p0.s = a + b;
+  }
   R size = mx(R(0.001), F.sradius[Qy.sa] + F.sradius[Qy.sb]);
   R eps = tolerance * R(0.01);
   if (norm(p0.v) < eps)
@@ -300,7 +388,7 @@ template <class R, class Query> __device__ MprHit<R> mprContact(const Query &Qy,
     hit.status = 1;
     hit.depth = norm(p1.v);
     hit.normal = hit.depth > eps ? -unitOrNan(p1.v) : unitOrNan(p0.v);
-    hit.position = divide(p1.a + p1.b, R(2));
+    hit.position = divide(p1.s, R(2));
     return hit;
   }
   dir = unitOrNan(dir);
@@ -335,14 +423,14 @@ template <class R, class Query> __device__ MprHit<R> mprContact(const Query &Qy,
     hit.status = -1;
     return hit;
   }
-  auto portalDir = [&]() { return unitOrNan(cross(p2.v - p1.v, p3.v - p1.v)); };
-  auto advanceOf = [&](const SP &v, V3<R> d) {
+  auto portalDir = [&]() __attribute__((always_inline)) { return unitOrNan(cross(p2.v - p1.v, p3.v - p1.v)); };
+  auto advanceOf = [&](const SP &v, V3<R> d) __attribute__((always_inline)) {
     return dot(v.v, d) - mx(dot(p1.v, d), mx(dot(p2.v, d), dot(p3.v, d)));
   };
   // The new support point replaces p1 (both sides positive, or both
   // negative), p3 (p1's side positive, p2's not) or p2 (p1's side negative,
   // p3's positive) -- the reference's choice of the portal face to keep.
-  auto expand = [&](const SP &v) {
+  auto expand = [&](const SP &v) __attribute__((always_inline)) {
     const V3<R> c = cross(v.v, p0.v);
     const bool s1 = dot(p1.v, c) > 0, s2 = dot(p2.v, c) > 0, s3 = dot(p3.v, c) > 0;
     const bool to1 = s1 ? s2 : !s3, to3 = s1 && !s2, to2 = !s1 && s3;
@@ -392,10 +480,10 @@ template <class R, class Query> __device__ MprHit<R> mprContact(const Query &Qy,
         hit.position = {R(NAN), R(NAN), R(NAN)};
       } else {
         V3<R> pos{0, 0, 0};
-        pos = pos + (p0.a + p0.b) * (w0 / (R(2) * sum));
-        pos = pos + (p1.a + p1.b) * (w1 / (R(2) * sum));
-        pos = pos + (p2.a + p2.b) * (w2 / (R(2) * sum));
-        pos = pos + (p3.a + p3.b) * (w3 / (R(2) * sum));
+        pos = pos + p0.s * (w0 / (R(2) * sum));
+        pos = pos + p1.s * (w1 / (R(2) * sum));
+        pos = pos + p2.s * (w2 / (R(2) * sum));
+        pos = pos + p3.s * (w3 / (R(2) * sum));
         hit.position = pos;
       }
       hit.status = mfinite(hit.position.x) ? 1 : -1;
@@ -411,7 +499,10 @@ template <class R, class Query> __device__ MprHit<R> mprContact(const Query &Qy,
 template <class R, int B, int J, int CG, int CS, int L, int PL = defaultSolveLanes(L)>
 __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
   constexpr int G = 64 / L;
-  constexpr int PPL = (CS + L - 1) / L; // pairs per lane (pairs <= CS)
+  // Lanes per body-pair query, pairs per round and rounds (pairs <= CS).
+  constexpr int MQ = sizeof(R) == sizeof(float) && 2 * CS <= L ? 2 : 1;
+  constexpr int PR = L / MQ;
+  constexpr int PPL = (CS + PR - 1) / PR;
   constexpr int SPL = (B + L - 1) / L;  // shapes per lane (shapes <= B)
   using Env = EnvLds<R, B, J, CG, CS>;
   using State = EnvState<R, B, J, CG, CS>;
@@ -631,10 +722,14 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
     PairGeom pg[PPL];
 #pragma unroll
     for (int r = 0; r < PPL; ++r) {
-      const int pi = lane + r * L;
+      // the lanes of a query compute the same values and branch alike; the
+      // first of them records the outcome
+      const int pi = lane / MQ + r * PR;
+      const bool lead = lane % MQ == 0;
       if (!active || pi >= np)
         continue;
-      E.pairHit[pi] = 0;
+      if (lead)
+        E.pairHit[pi] = 0;
       const int sa = F.pair[pi] & 255, sb = F.pair[pi] >> 8, A = F.sbody[sa], Bb = F.sbody[sb];
       if (E.s.mass[A] == 0 && E.s.mass[Bb] == 0)
         continue;
@@ -644,7 +739,8 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
                               norm(stp.Omega(Bb)) * F.sradius[sb]);
       if (norm(xa - xb) > F.sradius[sa] + F.sradius[sb] + skin)
         continue;
-      MprQuery<R, B, J> qy{F, M, points, sa, sb, xa, xb, qa, qb, skin};
+      MprQuery<R, B, J, MQ> qy{F, M, points, sa, sb, xa, xb, qa, qb, skin, lane % MQ == 1};
+      qy.loadOwn();
       MprHit<R> hit = mprContact(qy, mx(R(1e-8), M.tolerance * R(.1)));
       if (hit.status < 0) {
         E.s.failed = 1;
@@ -685,7 +781,8 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
         for (int d = 0; d < 3; ++d)
           o.penalty[d] = old.penalty[d];
       }
-      E.pairHit[pi] = 1;
+      if (lead)
+        E.pairHit[pi] = 1;
     }
     // ---------------- detection: ground manifolds (kernel.cuh:601-653) ----
     // Per pick: point index | (warm-start source + 1) << 20, so that only
@@ -939,8 +1036,8 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
         E.s.ngc = total > CG ? CG : total;
 #pragma unroll
       for (int r = 0; r < PPL; ++r) {
-        const int pi = lane + r * L;
-        if (pi >= np || !E.pairHit[pi])
+        const int pi = lane / MQ + r * PR;
+        if (lane % MQ != 0 || pi >= np || !E.pairHit[pi])
           continue;
         int slot = 0;
         for (int k = 0; k < pi; ++k)
