@@ -155,37 +155,70 @@ __device__ __forceinline__ void copyWords(unsigned *dst, const unsigned *src, in
   }
 }
 
-// One environment's blob into LDS: the header and the first kWarmContacts
-// ground contacts in one round (most steps hold no more), then the rest of
-// the live contacts once the counts are known.
+// Two 16-byte-aligned word ranges [a0, b0) and [a1, b1) as one sequence of
+// dwordx4 chunks: every lane's loads are issued before its first store.
+template <int Chunks>
+__device__ __forceinline__ void copyRanges(unsigned *dst, const unsigned *src, int a0, int b0, int a1,
+                                           int b1, int lane, int L) {
+  const int n0 = (b0 - a0) / 4, n = n0 + (b1 - a1) / 4;
+  for (int c = lane; c < n; c += Chunks * L) {
+    uint4 v[Chunks];
+    int w[Chunks];
+#pragma unroll
+    for (int k = 0; k < Chunks; ++k) {
+      const int i = c + k * L < n ? c + k * L : n - 1;
+      w[k] = i < n0 ? a0 + 4 * i : a1 + 4 * (i - n0);
+      v[k] = *reinterpret_cast<const uint4 *>(src + w[k]);
+    }
+#pragma unroll
+    for (int k = 0; k < Chunks; ++k)
+      if (c + k * L < n)
+        *reinterpret_cast<uint4 *>(dst + w[k]) = v[k];
+  }
+}
+
+// One environment's blob into LDS.  First round: the group every step reads
+// and writes (poses through the counts), the first kWarmContacts ground
+// contacts and, with `bodies`, the reset-only group; second round, once the
+// counts are known: the further live contacts and, when the launch may keep
+// them (`keep`, or a failed environment), the last controls and colouring.
+// Returns whether the controls were read.
 constexpr int kWarmContacts = 8;
-template <class S> __device__ void loadEnv(S &dst, const S *src, int lane, int L) {
+template <class S>
+__device__ bool loadEnv(S &dst, const S *src, int lane, int L, bool bodies, bool keep) {
   constexpr int header = int(headerBytes<S>() / 4);
+  constexpr int xStart = int(offsetof(S, x) / 4), tStart = int(offsetof(S, target) / 4);
   constexpr int CGcap = int(sizeof(S::gc) / sizeof(S::gc[0]));
   constexpr int CScap = int(sizeof(S::sc) / sizeof(S::sc[0]));
   constexpr int gcWords = int(sizeof(decltype(S::gc[0])) / 4);
   constexpr int scStart = int(offsetof(S, sc) / 4), scWords = int(sizeof(decltype(S::sc[0])) / 4);
   constexpr int warm = header + (kWarmContacts < CGcap ? kWarmContacts : CGcap) * gcWords;
+  static_assert(xStart % 4 == 0 && tStart % 4 == 0 && header % 4 == 0 && warm % 4 == 0,
+                "copied groups start on 16-byte boundaries");
   int ngc = src->ngc, nsc = src->nsc;
+  keep = keep || src->failed;
   unsigned *d = reinterpret_cast<unsigned *>(&dst);
   const unsigned *s = reinterpret_cast<const unsigned *>(src);
-  copyWords<16>(d, s, 0, warm, lane, L);
+  copyRanges<16>(d, s, bodies ? 0 : xStart, tStart, header, warm, lane, L);
   ngc = ngc < 0 ? 0 : (ngc > CGcap ? CGcap : ngc);
   nsc = nsc < 0 ? 0 : (nsc > CScap ? CScap : nsc);
   copyWords<4>(d, s, warm, header + ngc * gcWords, lane, L);
   copyWords<4>(d, s, scStart, scStart + nsc * scWords, lane, L);
+  if (keep)
+    copyWords<4>(d, s, tStart, int(coloursEndBytes<S>() / 4), lane, L);
+  return keep;
 }
 
-// LDS -> HBM after a step: the header from `from` (the step's write-back
-// starts at x: mass, inertia and friction only change on reset) and exactly
-// the live contacts.
+// LDS -> HBM after a step: the groups from `from` (the step's write-back
+// starts at x: mass, inertia and friction only change on reset) through the
+// colouring, and exactly the live contacts.
 template <class S> __device__ void storeEnv(S *dst, const S &src, int lane, int L, int from) {
   constexpr int header = int(headerBytes<S>() / 4);
   constexpr int gcWords = int(sizeof(decltype(S::gc[0])) / 4);
   constexpr int scStart = int(offsetof(S, sc) / 4), scWords = int(sizeof(decltype(S::sc[0])) / 4);
   unsigned *d = reinterpret_cast<unsigned *>(dst);
   const unsigned *s = reinterpret_cast<const unsigned *>(&src);
-  copyWords<16>(d, s, from, header, lane, L);
+  copyWords<16>(d, s, from, int(coloursEndBytes<S>() / 4), lane, L);
   copyWords<4>(d, s, header, header + src.ngc * gcWords, lane, L);
   copyWords<4>(d, s, scStart, scStart + src.nsc * scWords, lane, L);
 }
@@ -504,7 +537,7 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
   constexpr int PR = L / MQ;
   constexpr int PPL = (CS + PR - 1) / PR;
   constexpr int SPL = (B + L - 1) / L;  // shapes per lane (shapes <= B)
-  using Env = EnvLds<R, B, J, CG, CS>;
+  using Env = EnvLds<R, B, J, CG, CS, L>;
   using State = EnvState<R, B, J, CG, CS>;
   __shared__ Frames<R, B, J> F;
   __shared__ Env envs[G];
@@ -544,13 +577,19 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
   if (valid && lane < 3 && args.motorMode != kHeldControls)
     fin = static_cast<const R *>(args.forces)[size_t(e) * 3 + lane];
 
-  // Stage the joint model (all 64 lanes); the slots of absent hinges hold
-  // zero frames (a lane without a hinge evaluates slot 0).
+  // Stage the joint model (all 64 lanes).  The slots of absent hinges hold
+  // a zero hinge between body 0 and itself: a lane without a hinge evaluates
+  // one (slot 0 of a model without hinges), masked, and its finite values
+  // keep the masked stamps zero.
   for (int j = t + nj; j < J; j += 64) {
+    F.a[j] = F.b[j] = F.limited[j] = 0;
+    F.lo[j] = F.hi[j] = F.armature[j] = 0;
 #pragma unroll
     for (int k = 0; k < 3; ++k)
       F.ra[k][j] = F.rb[k][j] = F.axisA[k][j] = F.axisB[k][j] = F.tangentA[k][j] = F.tangentB[k][j] = 0;
   }
+  for (int i = t + 2 * nj; i < 2 * J; i += 64)
+    F.adj[i] = 0;
   for (int j = t; j < nj; j += 64) {
     F.a[j] = M.ja[j];
     F.b[j] = M.jb[j];
@@ -610,8 +649,21 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
   State *gs = valid ? &blobAt<State>(args.states, args.blobBytes, e) : nullptr;
   static_assert(L >= 4, "blob copies give each of the first three lanes an end word");
   static_assert(CS <= B, "the staged pair table holds B pairs");
-  if (valid)
-    loadEnv<State>(E.s, gs, lane, L);
+  bool kept = false; // the last controls and colouring were read
+  if (valid) {
+    kept = loadEnv<State>(E.s, gs, lane, L, args.bodies != 0, args.motorMode != kTargetControls);
+    if (!args.bodies) {
+      // the model's masses, inertia and shape friction, as reset writes them
+      for (int b = lane; b < B; b += L) {
+        E.s.mass[b] = b < nb ? M.mass[b] : R(0);
+#pragma unroll
+        for (int k = 0; k < 3; ++k)
+          E.s.inertia[k][b] = b < nb ? M.inertia[k][b] : R(0);
+      }
+      if (lane == 0)
+        E.s.friction = R(-1);
+    }
+  }
   __syncthreads();
   // The staged default schedule applies to this env while no body-body
   // contact recolours it and its dynamic bodies are the model's.
@@ -669,19 +721,27 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
 #pragma unroll
       for (int r = 0; r < JPL; ++r) {
         const int j = lane + r * L;
-        if (j >= nj)
+        if (j >= J)
           continue;
-        E.s.target[j] = ctl[r][0];
-        E.s.kp[j] = R(args.kp);
-        E.s.maxTorque[j] = R(args.limit);
-        E.s.torque[j] = defs[r][0];
-        E.s.frictionloss[j] = defs[r][1];
-        E.s.damping[j] = defs[r][2];
+        // slots past the last hinge hold zeros, as the state was created
+        const bool in = j < nj;
+        E.s.target[j] = in ? ctl[r][0] : R(0);
+        E.s.kp[j] = in ? R(args.kp) : R(0);
+        E.s.maxTorque[j] = in ? R(args.limit) : R(0);
+        E.s.torque[j] = in ? defs[r][0] : R(0);
+        E.s.frictionloss[j] = in ? defs[r][1] : R(0);
+        E.s.damping[j] = in ? defs[r][2] : R(0);
       }
       if (lane < 3)
         E.s.force[lane] = fin;
       active = true;
     } else {
+      // invalid controls: the environment keeps its last controls and
+      // colouring, which this launch has not read yet
+      constexpr int tStart = int(offsetof(State, target) / 4), cEnd = int(coloursEndBytes<State>() / 4);
+      if (!kept)
+        copyWords<4>(reinterpret_cast<unsigned *>(&E.s), reinterpret_cast<const unsigned *>(gs), tStart,
+                     cEnd, lane, L);
       if (lane == 0)
         E.s.failed = 1;
     }
@@ -1081,9 +1141,10 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
       pairHits += E.pairHit[pi];
     const bool fresh = active && !(pairHits == 0 && defaultSchedule);
     if (active) {
-      for (int b = lane; b < nb; b += L) {
-        E.s.colors[b] = M.colors[b];
-        if (!fresh)
+      for (int b = lane; b < B; b += L) {
+        // slots past the last body hold zeros, as the state was created
+        E.s.colors[b] = b < nb ? M.colors[b] : 0;
+        if (!fresh && b < nb)
           E.order[b] = F.order[b];
       }
       if (!fresh && lane < 3)

@@ -127,25 +127,36 @@ DUCK_HD int scPack(int body, int other, int shape, int otherShape, bool stick) {
 
 enum DiagSlot { kJointError, kPenetration, kContacts, kConverged, kAxisError, kIterations };
 
-// Persistent per-env state; the HBM blob is exactly this struct.
+// Persistent per-env state; the HBM blob is exactly this struct.  Its fields
+// are grouped by what a step does with them, each group starting on a 16-byte
+// boundary so that a launch copies whole groups:
+//  1. set by reset only; a launch reads them only when some environment's
+//     may differ from the model's (reset with per-env extensions, imported
+//     states), and never writes them back;
+//  2. read and written by every step;
+//  3. the last controls: written by every step, read only when a launch may
+//     keep some of them (held or motor controls, a failed environment);
+//  4. the colouring of the last step: written by every step, read only when
+//     a launch may keep it (a failed environment);
+//  5. the compacted contact lists (live entries only).
 template <class R, int B, int J, int CG, int CS> struct EnvState {
-  // Set by reset only (the step reads them and never writes them back).
   R mass[B], inertia[3][B];
   R friction; // per-env ground friction; < 0 selects the shape friction
-  // Advanced by every step.
-  R x[3][B], q[4][B], v[3][B], w[3][B];
+  alignas(16) R x[3][B];
+  R q[4][B], v[3][B], w[3][B];
   R force[3];
   R lambda[7][J], penalty[7][J];
   R lambdaF[J], penaltyF[J];
-  R target[J], kp[J], maxTorque[J], torque[J], frictionloss[J], damping[J];
   R diag[8];
   int failed, ngc, nsc, colorCount;
-  int colors[B]; // colouring of the last step (model colours + fresh ones)
-  GroundContact<R> gc[CG];
+  alignas(16) R target[J];
+  R kp[J], maxTorque[J], torque[J], frictionloss[J], damping[J];
+  alignas(16) int colors[B]; // model colours + fresh ones
+  alignas(16) GroundContact<R> gc[CG];
   SelfContact<R> sc[CS];
 };
 
-template <class R, int B, int J, int CG, int CS> struct alignas(16) EnvLds {
+template <class R, int B, int J, int CG, int CS> struct EnvLdsCore {
   EnvState<R, B, J, CG, CS> s;
   // per-step scratch
   R x0[3][B], q0[4][B], xp[3][B], qp[4][B];
@@ -158,12 +169,27 @@ template <class R, int B, int J, int CG, int CS> struct alignas(16) EnvLds {
   uint32_t smask[B];
   int order[B], colorStart[CS + 3];
   int done, pad0, pad1, pad2;
-  int shapeCount[kMaxModelShapes];
-  int pairHit[kMaxModelPairs];
+  int shapeCount[B]; // shapes <= B
+  int pairHit[CS];   // body-contact pairs <= CS
 };
 
-// Word offset of the contact lists inside the blob (everything before them is
-// copied unconditionally; only the live contacts after them are copied).
+// One environment's LDS record.  A wave holds 64 / L environments and their
+// lanes read the same field at consecutive words, so the record stride is
+// padded to an odd multiple of L words: the environments of a wave then fall
+// on disjoint LDS banks (32 or 64 banks of 4 bytes).
+template <int Words, int L> constexpr int bankPadWords() { return (L - Words % (2 * L) + 2 * L) % (2 * L); }
+template <class R, int B, int J, int CG, int CS, int L,
+          int Pad = bankPadWords<int(sizeof(EnvLdsCore<R, B, J, CG, CS>) / 4), L>()>
+struct EnvLds : EnvLdsCore<R, B, J, CG, CS> {
+  int bankPad[Pad];
+};
+template <class R, int B, int J, int CG, int CS, int L>
+struct EnvLds<R, B, J, CG, CS, L, 0> : EnvLdsCore<R, B, J, CG, CS> {};
+
+// Word offset of the contact lists inside the blob (only their live entries
+// are copied), and the end of the colouring: the alignment padding between
+// the two is never copied, so it keeps the zeros the state was created with.
 template <class S> constexpr size_t headerBytes() { return offsetof(S, gc); }
+template <class S> constexpr size_t coloursEndBytes() { return offsetof(S, colors) + sizeof(S::colors); }
 
 } // namespace duckhip

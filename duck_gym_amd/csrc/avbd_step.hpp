@@ -37,6 +37,8 @@ struct StepArgs {
   double kp, limit;
   int nb, nj, ns, np; // model counts (also in the model), here so that the
                       // first loads need only the kernel arguments
+  int bodies;         // read the reset-only block (masses, inertia, friction)
+                      // of each state; else they are the model's
 };
 
 DUCK_HD constexpr int tri(int i, int j) { return i * (i + 1) / 2 + j; }
@@ -340,7 +342,7 @@ constexpr int defaultSolveLanes(int L) { return L >= 32 ? 4 : (L >= 16 ? 2 : 1);
 
 template <class R, int B, int J, int CG, int CS, int L, int PL = defaultSolveLanes(L)>
 struct Stepper {
-  using Env = EnvLds<R, B, J, CG, CS>;
+  using Env = EnvLds<R, B, J, CG, CS, L>;
   using Fr = Frames<R, B, J>;
   const DeviceModel<R> &M;
   const V3<R> *points;

@@ -227,6 +227,10 @@ class Batch final : public BatchBase {
   unsigned char *dStates = nullptr;
   hipEvent_t ready = nullptr;
   void *dScratch = nullptr; // this device's `scratch`
+  // Whether an environment's masses, inertia or friction may differ from the
+  // model's (a reset with per-env extensions, an imported state): then every
+  // launch reads them from the states, else it takes the model's.
+  bool customBodies = false;
 
   void wait(hipStream_t s) { hipCheck(hipStreamWaitEvent(s, ready, 0), "hipStreamWaitEvent"); }
   void record(hipStream_t s) { hipCheck(hipEventRecord(ready, s), "hipEventRecord"); }
@@ -241,7 +245,7 @@ class Batch final : public BatchBase {
     StepArgs args{dModel, dPoints, states, blobBytes, n, targets, forces, motor,
                   substeps, mode, kp, limit,
                   int(host.bodies.size()), int(host.joints.size()), int(host.shapes.size()),
-                  int(host.pairs.size())};
+                  int(host.pairs.size()), states == dStates && customBodies ? 1 : 0};
     advanceKernel<R, B, J, CG, CS, L, PL><<<(n + G - 1) / G, 64, 0, s>>>(args);
     launched("advanceKernel");
   }
@@ -316,6 +320,8 @@ public:
         dModel, dStates, blobBytes, count, mask, static_cast<const R *>(q),
         static_cast<const R *>(root), static_cast<const R *>(ext));
     launched("resetKernel");
+    if (ext)
+      customBodies = true;
     record(s);
   }
   void step(const void *target, const void *force, int substeps, double kp, double limit,
@@ -497,6 +503,7 @@ public:
     wait(s);
     hipCheck(hipMemcpyAsync(dStates, src, size_t(blobBytes) * count, hipMemcpyDeviceToDevice, s),
              "import_state");
+    customBodies = true;
     record(s);
   }
 };
