@@ -234,6 +234,47 @@ def other_workload(args):
                   "envs": E, "iterations": ITERATIONS, "dt_s": DT,
                   "physics_steps_per_control_step": substeps,
                   "control_steps_per_s": E * args.steps / wall}
+    elif args.workload == "servo":
+        from duck_gym_amd.servo import SYNTHETIC_SUPPLY, ServoLoop, servo_params
+
+        E, substeps, lag = args.envs or 4096, 4, 2
+        meta = model_text(self_contact=True)[1]
+        model = write_model(Path(tmp.name) / "m", self_contact=True)
+        names = meta["body_names"]
+        feet = [names.index("left_foot"), names.index("right_foot")]
+        envs = np.arange(E)
+        t = lambda a: torch.tensor(a, dtype=torch.float32, device=dev)  # noqa: E731
+        targets = [t(W.servo_targets(home, envs, 4 * k, seed))
+                   for k in range(args.warmup + args.steps + 1)]
+        timing = {}
+        for fused in (True, False):
+            batch = CudaBatch(model, E, DT, ITERATIONS, 0, False)
+            batch.reset(torch.ones(E, dtype=torch.bool, device=dev), t(np.tile(home, (E, 1))),
+                        t(np.zeros((E, 6))))
+            loop = ServoLoop(batch, servo_params(**SYNTHETIC_SUPPLY, lag=lag), home,
+                             [0.0, 0.0, 0.01], root_principal_quat=meta["root_iquat"], feet=feet,
+                             foot_sites=[[0.01, 0.0, -0.006]] * 2, fused=fused)
+            for k in range(args.warmup):
+                loop.substeps(targets[k], substeps)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for k in range(args.warmup, args.warmup + args.steps):
+                loop.substeps(targets[k], substeps)
+            torch.cuda.synchronize()
+            timing[fused] = time.perf_counter() - t0
+        wall = timing[True]
+        value = E * args.steps * substeps / wall
+        ms = wall / args.steps * 1e3
+        config = {"workload": "BAM servo substeps: XL330 actuator with a 2-substep delay and "
+                              "load-dependent friction, servo targets HOME + U(-0.3, 0.3) per "
+                              "control step, body contacts between the leg chains, refresh "
+                              "quantities (root frame, foot forces and sites, timers) per "
+                              "substep; one launch per substep",
+                  "envs": E, "iterations": ITERATIONS, "dt_s": DT,
+                  "physics_steps_per_control_step": substeps,
+                  "unfused_env_steps_per_s": E * args.steps * substeps / timing[False],
+                  "unfused": "servo kernel, motor step, state/contact-force/self-contact "
+                             "queries and torch refresh arithmetic per substep"}
     elif args.workload == "train":
         from duck_gym_amd.on_policy import STANDING, OnPolicyRunner
         from duck_gym_amd.tensor_env import TensorEnv
@@ -278,7 +319,7 @@ def main():
     p.add_argument("--substeps", type=int, default=1,
                    help="physics steps per kernel launch (default 1, the tensor-env contract; "
                         "K > 1 runs K steps inside one launch, the reference's chunked form)")
-    p.add_argument("--workload", choices=("home", "sweep", "drop", "rollout", "train"),
+    p.add_argument("--workload", choices=("home", "sweep", "drop", "rollout", "train", "servo"),
                    default="home",
                    help="home: fixed HOME, 4096 envs (default, the headline line); sweep: "
                         "servo-target sweep with body contacts and per-env friction; drop: "

@@ -1,5 +1,6 @@
 // gfx950 kernels of the batched AVBD environment step.
 #pragma once
+#include "../../include/duck_hip.h"
 #include "avbd_step.hpp"
 
 namespace duckhip {
@@ -528,9 +529,40 @@ template <class R, class Query> __device__ __forceinline__ MprHit<R> mprContact(
   return hit;
 }
 
-// Per-launch kernel: controls, `substeps` physics steps, write-back.
-template <class R, int B, int J, int CG, int CS, int L, int PL = defaultSolveLanes(L)>
-__global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
+// The fused servo substep's buffers and frame data (DuckServoSubstep of
+// include/duck_hip.h in the batch dtype, the root rotation already inverted).
+template <class R> struct ServoArgs {
+  DuckServo p;
+  int cursor;
+  const R *target;
+  R *history;
+  unsigned char *initialized;
+  const R *rootOffset;
+  R *previousMotor, *previousApplied, *motor, *supply, *selfContacts, *selfPenetration;
+  R rootInv[4];
+  int numFeet;
+  int feet[DUCK_MAX_FEET];
+  R sites[DUCK_MAX_FEET][3];
+  R *gravity, *angularVelocity, *linearVelocity, *originVelocity, *footForces, *sitePositions,
+      *siteVelocities, *airTime, *contactTime;
+};
+
+// The servo substep's prologue (the motor channels of this substep into
+// `ctl`) and epilogue (statistics and refresh quantities), defined with the
+// actuator model in avbd_servo.hpp.
+template <class R, int B, int J, int CG, int CS, int L, int JPL, class Env>
+__device__ __forceinline__ void servoPrologue(const ServoArgs<R> &sv, const DeviceModel<R> &M, Env &E,
+                                              int e, int lane, bool valid, int count,
+                                              R (&ctl)[JPL][3]);
+template <class R, int B, int J, int CG, int CS, class Env>
+__device__ __forceinline__ void servoEpilogue(const ServoArgs<R> &sv, const DeviceModel<R> &M, Env &E,
+                                              int e);
+
+// Per-launch step: controls, `substeps` physics steps, write-back; with
+// Servo, the controls are the motor channels of one servo substep and the
+// launch ends with the substep's statistics and refresh quantities.
+template <class R, int B, int J, int CG, int CS, int L, int PL, bool Servo>
+__device__ __forceinline__ void stepBody(const StepArgs &args, const ServoArgs<R> &sv) {
   constexpr int G = 64 / L;
   // Lanes per body-pair query, pairs per round and rounds (pairs <= CS).
   constexpr int MQ = sizeof(R) == sizeof(float) && 2 * CS <= L ? 2 : 1;
@@ -560,7 +592,7 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
     const bool in = valid && j < nj;
     const int jc = j < nj ? j : 0;
     ctl[r][0] = ctl[r][1] = ctl[r][2] = 0;
-    if (in && args.motorMode != kHeldControls) {
+    if (!Servo && in && args.motorMode != kHeldControls) {
       if (args.motorMode == kMotorControls) {
         const R *motor = static_cast<const R *>(args.motor) + size_t(e) * nj * 3;
         ctl[r][0] = motor[3 * j];
@@ -574,7 +606,7 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
     defs[r][1] = M.frictionloss[jc];
     defs[r][2] = M.damping[jc];
   }
-  if (valid && lane < 3 && args.motorMode != kHeldControls)
+  if (!Servo && valid && lane < 3 && args.motorMode != kHeldControls)
     fin = static_cast<const R *>(args.forces)[size_t(e) * 3 + lane];
 
   // Stage the joint model (all 64 lanes).  The slots of absent hinges hold
@@ -672,6 +704,8 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
     for (int b = lane; b < nb; b += L)
       massPattern |= (E.s.mass[b] > 0) != (F.mass[b] > 0);
   const bool defaultSchedule = groupOr<L>(massPattern) == 0;
+  if constexpr (Servo)
+    servoPrologue<R, B, J, CG, CS, L>(sv, M, E, e, lane, valid, args.count, ctl);
 
   // ---- controls (extension.cu:87-110 / kernel.cuh:448-466) ----
   int bad = 0;
@@ -1563,8 +1597,23 @@ __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
     __syncthreads();
     __syncthreads();
   }
+  if constexpr (Servo)
+    if (valid && lane == 0)
+      servoEpilogue<R, B, J, CG, CS>(sv, M, E, e);
   if (valid)
     storeEnv<State>(gs, E.s, lane, L, int(offsetof(State, x) / 4));
+}
+
+template <class R, int B, int J, int CG, int CS, int L, int PL = defaultSolveLanes(L)>
+__global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
+  const ServoArgs<R> none{};
+  stepBody<R, B, J, CG, CS, L, PL, false>(args, none);
+}
+
+// One servo substep per launch (bam_env.py:307-337 with refresh()).
+template <class R, int B, int J, int CG, int CS, int L, int PL = defaultSolveLanes(L)>
+__global__ __launch_bounds__(64) void servoStepKernel(StepArgs args, ServoArgs<R> servo) {
+  stepBody<R, B, J, CG, CS, L, PL, true>(args, servo);
 }
 
 } // namespace duckhip

@@ -258,14 +258,21 @@ __global__ void contactCountsKernel(unsigned char *states, long long blobBytes, 
   out[2 * e + 1] = R(s.nsc);
 }
 
+// The per-body quantities of the Newton-Euler pass.
+template <class R, int B> struct RneaWork {
+  V3<R> acc[B], alpha[B], force[B], moment[B], contact[B], contactMoment[B];
+};
+
 // Recursive Newton-Euler at zero joint acceleration (kernel.cuh:504-554):
 // per hinge [bias, contact/limit, applied actuator torque] into o[3 j + k];
-// `off` is the root COM offset of the acceleration reference point.
+// `off` is the root COM offset of the acceleration reference point.  `work`
+// holds the per-body quantities (private memory, or a caller's LDS scratch).
 template <class R, int B, int J, int CG, int CS>
-DUCK_HD void rneaLoads(const DeviceModel<R> &M, const EnvState<R, B, J, CG, CS> &s, const R *off,
-                       R *o) {
+DUCK_HD void rneaLoadsIn(const DeviceModel<R> &M, const EnvState<R, B, J, CG, CS> &s, const R *off,
+                         R *o, RneaWork<R, B> &work) {
   StateView<R, B, J, CG, CS> v{M, const_cast<EnvState<R, B, J, CG, CS> &>(s)};
-  V3<R> acc[B], alpha[B], force[B], moment[B], contact[B], contactMoment[B];
+  V3<R> *acc = work.acc, *alpha = work.alpha, *force = work.force, *moment = work.moment,
+        *contact = work.contact, *contactMoment = work.contactMoment;
   for (int b = 0; b < M.nb; ++b)
     acc[b] = alpha[b] = force[b] = moment[b] = contact[b] = contactMoment[b] = V3<R>{0, 0, 0};
   acc[1] = cross(v.W(1), cross(v.W(1), rotate(v.Q(1), V3<R>{off[0], off[1], off[2]})));
@@ -328,6 +335,12 @@ DUCK_HD void rneaLoads(const DeviceModel<R> &M, const EnvState<R, B, J, CG, CS> 
     contactMoment[a] = contactMoment[a] + (contactMoment[b] + cross(shift, contact[b]));
     contact[a] = contact[a] + contact[b];
   }
+}
+template <class R, int B, int J, int CG, int CS>
+DUCK_HD void rneaLoads(const DeviceModel<R> &M, const EnvState<R, B, J, CG, CS> &s, const R *off,
+                       R *o) {
+  RneaWork<R, B> work;
+  rneaLoadsIn<R, B, J, CG, CS>(M, s, off, o, work);
 }
 
 template <class R, int B, int J, int CG, int CS>

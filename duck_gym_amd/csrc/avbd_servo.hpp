@@ -113,4 +113,157 @@ __global__ void servoKernel(DuckServo p, const DeviceModel<R> *model, unsigned c
     static_cast<R *>(io.supply)[e] = supply;
 }
 
+// The servo substep inside the step launch (servoStepKernel): the operations
+// of servoKernel on the state the launch staged in LDS, before the motor
+// step.  Lanes take hinges; the environment's first lane runs the load pass
+// (its per-body quantities in the step's per-step scratch, which the step
+// fills later) and the supply sum, in servoKernel's order.  The channels go
+// into `ctl`, where the motor step takes them.
+template <class R, int B, int J, int CG, int CS, int L, int JPL, class Env>
+__device__ __forceinline__ void servoPrologue(const ServoArgs<R> &sv, const DeviceModel<R> &M, Env &E,
+                                              int e, int lane, bool valid, int count,
+                                              R (&ctl)[JPL][3]) {
+  static_assert(sizeof(RneaWork<R, B>) <= sizeof(R) * 20 * B, "the load pass fits x0 .. Iw");
+  static_assert(3 * J < 7 * J - 1, "loads and supply fit c0");
+  const int nj = M.nj, slots = sv.p.lag + 1;
+  const size_t row = size_t(e) * nj, plane = size_t(count) * nj;
+  R *loads = &E.c0[0][0];
+  R delayed[JPL];
+  if (valid) {
+    // bam_env.py:308-314: this substep's target into the ring (every slot
+    // of a fresh ring), the target `lag` substeps old out
+    const bool fresh = !sv.initialized[e];
+    const int delayedSlot = ((sv.cursor - sv.p.lag) % slots + slots) % slots;
+#pragma unroll
+    for (int r = 0; r < JPL; ++r) {
+      const int j = lane + r * L;
+      delayed[r] = 0;
+      if (j >= nj)
+        continue;
+      const R t = sv.target[row + j];
+      sv.history[size_t(sv.cursor) * plane + row + j] = t;
+      if (fresh)
+        for (int k = 0; k < slots; ++k)
+          sv.history[size_t(k) * plane + row + j] = t;
+      delayed[r] = sv.history[size_t(delayedSlot) * plane + row + j];
+    }
+    if (lane == 0) {
+      rneaLoadsIn<R, B, J, CG, CS>(M, E.s, sv.rootOffset + size_t(e) * 3, loads,
+                                   *reinterpret_cast<RneaWork<R, B> *>(&E.x0[0][0]));
+      R total = 0;
+      for (int j = 0; j < nj; ++j)
+        total += mabs(sv.previousMotor[row + j]);
+      R supply = R(sv.p.vin) - R(sv.p.vin_drop_gain) * total;
+      supply = supply < R(sv.p.vin_min) ? R(sv.p.vin_min) : supply;
+      E.c0[6][J - 1] = supply;
+      if (sv.supply)
+        sv.supply[e] = supply;
+      sv.initialized[e] = 1;
+    }
+  }
+  __syncthreads();
+  if (valid) {
+    StateView<R, B, J, CG, CS> view{M, E.s};
+    const R supply = E.c0[6][J - 1];
+#pragma unroll
+    for (int r = 0; r < JPL; ++r) {
+      const int j = lane + r * L;
+      if (j >= nj)
+        continue;
+      R position = view.angle(j);
+      R velocity = dot(view.W(M.jb[j]) - view.W(M.ja[j]), rotate(view.Q(M.ja[j]), view.mv(M.axisA, j)));
+      R external = -loads[3 * j] + loads[3 * j + 1];
+      R applied, budget, damping, raw;
+      xl330(sv.p, supply, delayed[r], position, velocity, sv.previousApplied[row + j], external,
+            applied, budget, damping, raw);
+      if (sv.motor) {
+        sv.motor[(row + j) * 3] = applied;
+        sv.motor[(row + j) * 3 + 1] = budget;
+        sv.motor[(row + j) * 3 + 2] = damping;
+      }
+      sv.previousMotor[row + j] = raw;
+      sv.previousApplied[row + j] = applied;
+      ctl[r][0] = applied;
+      ctl[r][1] = budget;
+      ctl[r][2] = damping;
+    }
+  }
+  __syncthreads(); // the load pass's scratch is the step's
+}
+
+// torch.maximum: NaN when either operand is NaN.
+template <class R> DUCK_HD R maximumNan(R a, R b) { return a != a || b != b ? R(NAN) : (a > b ? a : b); }
+
+// The end of the servo substep, on the environment's first lane after the
+// motor step: self_contact_stats (selfContactStatsKernel's loop) folded into
+// the running maxima (bam_env.py:333-335), then refresh() (bam_env.py:128-
+// 155) on the new state: gravity and velocities in the root frame, the
+// ground contact force on each foot (contactForcesKernel's sums), the foot
+// sites and the air/contact timers.
+template <class R, int B, int J, int CG, int CS, class Env>
+__device__ __forceinline__ void servoEpilogue(const ServoArgs<R> &sv, const DeviceModel<R> &M, Env &E,
+                                              int e) {
+  auto &s = E.s;
+  StateView<R, B, J, CG, CS> v{M, s};
+  R n = 0, depthMax = 0;
+  for (int i = 0; i < s.nsc; ++i) {
+    const auto &c = s.sc[i];
+    int a = scBody(c.id), b = scOther(c.id);
+    V3<R> ra = rotate(v.Q(a), V3<R>{c.local[0], c.local[1], c.local[2]});
+    V3<R> rb = rotate(v.Q(b), V3<R>{c.localB[0], c.localB[1], c.localB[2]});
+    V3<R> delta = ((v.X(a) + ra) - v.X(b)) - rb;
+    R cz = dot(delta, V3<R>{c.n[0], c.n[1], c.n[2]}) - M.alpha * c.c0;
+    R depth = mx(R(0), -(cz + M.alpha * c.c0));
+    if (c.lambda[2] < R(-1e-5) || depth > R(1e-6))
+      n += 1;
+    depthMax = mx(depthMax, depth);
+  }
+  if (sv.selfContacts)
+    sv.selfContacts[e] = maximumNan(sv.selfContacts[e], n);
+  if (sv.selfPenetration)
+    sv.selfPenetration[e] = maximumNan(sv.selfPenetration[e], depthMax);
+  auto put = [](R *out, size_t i, V3<R> u) {
+    if (out) {
+      out[3 * i] = u.x;
+      out[3 * i + 1] = u.y;
+      out[3 * i + 2] = u.z;
+    }
+  };
+  const Q4<R> q1 = v.Q(1), root = q1 * Q4<R>{sv.rootInv[0], sv.rootInv[1], sv.rootInv[2], sv.rootInv[3]};
+  const V3<R> w1 = v.W(1), v1{s.v[0][1], s.v[1][1], s.v[2][1]};
+  put(sv.gravity, e, rotate(conj(root), V3<R>{0, 0, -1}));
+  put(sv.angularVelocity, e, rotate(conj(root), w1));
+  const R *off = sv.rootOffset + size_t(e) * 3;
+  const V3<R> rootR = -rotate(q1, V3<R>{off[0], off[1], off[2]});
+  const V3<R> origin = v1 + cross(w1, rootR);
+  put(sv.originVelocity, e, origin);
+  put(sv.linearVelocity, e, rotate(conj(root), origin));
+  const R h = M.dt;
+  for (int f = 0; f < sv.numFeet; ++f) {
+    const int body = sv.feet[f];
+    const size_t k = size_t(e) * sv.numFeet + f;
+    V3<R> force{0, 0, 0};
+    for (int i = 0; i < s.ngc; ++i) {
+      const auto &c = s.gc[i];
+      if (gcBody(c.id) != body)
+        continue;
+      V3<R> g = -((V3<R>{1, 0, 0} * c.lambda[0] + V3<R>{0, 1, 0} * c.lambda[1]) +
+                  V3<R>{0, 0, 1} * c.lambda[2]);
+      force.x += g.x;
+      force.y += g.y;
+      force.z += g.z;
+    }
+    put(sv.footForces, k, force);
+    const V3<R> r = rotate(v.Q(body), V3<R>{sv.sites[f][0], sv.sites[f][1], sv.sites[f][2]});
+    const V3<R> vb{s.v[0][body], s.v[1][body], s.v[2][body]};
+    put(sv.sitePositions, k, v.X(body) + r);
+    put(sv.siteVelocities, k, vb + cross(v.W(body), r));
+    const bool contact = norm(force) > R(1e-5);
+    if (sv.airTime)
+      sv.airTime[k] = contact ? R(0) : sv.airTime[k] + h;
+    if (sv.contactTime)
+      sv.contactTime[k] = contact ? sv.contactTime[k] + h : R(0);
+  }
+}
+
 } // namespace duckhip

@@ -216,6 +216,7 @@ struct BatchBase {
                            hipStream_t) = 0;
   virtual void task(const DuckTask &, int, const TaskBuffers &, hipStream_t) = 0;
   virtual void servo(const DuckServo &, const ServoBuffers &, hipStream_t) = 0;
+  virtual void servoSubstep(const DuckServo &, const DuckServoSubstep &, hipStream_t) = 0;
 };
 
 template <class R, int B, int J, int CG, int CS, int L, int PL = defaultSolveLanes(L)>
@@ -478,6 +479,53 @@ public:
     taskKernel<R, B, J, CG, CS><<<blocks64(count), 64, 0, s>>>(t, mode, dModel, dStates, blobBytes,
                                                                 count, io);
     launched("taskKernel");
+    record(s);
+  }
+  void servoSubstep(const DuckServo &p, const DuckServoSubstep &io, hipStream_t s) override {
+    DeviceGuard guard(device);
+    const int nb = host.bodies.size();
+    require(nb >= 2, "servo substep: the model needs a root body (body 1)");
+    require(io.num_feet >= 0 && io.num_feet <= DUCK_MAX_FEET, "servo substep: invalid foot count");
+    ServoArgs<R> sv{};
+    sv.p = p;
+    sv.cursor = io.cursor;
+    sv.target = static_cast<const R *>(io.target);
+    sv.history = static_cast<R *>(io.history);
+    sv.initialized = io.initialized;
+    sv.rootOffset = static_cast<const R *>(io.root_offset);
+    sv.previousMotor = static_cast<R *>(io.previous_motor);
+    sv.previousApplied = static_cast<R *>(io.previous_applied);
+    sv.motor = static_cast<R *>(io.motor);
+    sv.supply = static_cast<R *>(io.supply);
+    sv.selfContacts = static_cast<R *>(io.self_contacts);
+    sv.selfPenetration = static_cast<R *>(io.self_penetration);
+    // root frame = q1 * conj(root principal rotation) (bam_env.py:64, 130-132)
+    sv.rootInv[0] = R(io.root_principal_quat[0]);
+    for (int k = 1; k < 4; ++k)
+      sv.rootInv[k] = -R(io.root_principal_quat[k]);
+    sv.numFeet = io.num_feet;
+    for (int f = 0; f < io.num_feet; ++f) {
+      require(io.foot_bodies[f] >= 0 && io.foot_bodies[f] < nb, "servo substep: invalid foot body");
+      sv.feet[f] = io.foot_bodies[f];
+      for (int k = 0; k < 3; ++k)
+        sv.sites[f][k] = R(io.foot_sites[f][k]);
+    }
+    sv.gravity = static_cast<R *>(io.gravity);
+    sv.angularVelocity = static_cast<R *>(io.angular_velocity);
+    sv.linearVelocity = static_cast<R *>(io.linear_velocity);
+    sv.originVelocity = static_cast<R *>(io.origin_velocity);
+    sv.footForces = static_cast<R *>(io.foot_forces);
+    sv.sitePositions = static_cast<R *>(io.site_positions);
+    sv.siteVelocities = static_cast<R *>(io.site_velocities);
+    sv.airTime = static_cast<R *>(io.air_time);
+    sv.contactTime = static_cast<R *>(io.contact_time);
+    StepArgs args{dModel, dPoints, dStates, blobBytes, count, nullptr, nullptr, nullptr,
+                  1, kMotorControls, 0, 0,
+                  nb, int(host.joints.size()), int(host.shapes.size()), int(host.pairs.size()),
+                  customBodies ? 1 : 0};
+    wait(s);
+    servoStepKernel<R, B, J, CG, CS, L, PL><<<(count + G - 1) / G, 64, 0, s>>>(args, sv);
+    launched("servoStepKernel");
     record(s);
   }
   void servo(const DuckServo &p, const ServoBuffers &io, hipStream_t s) override {
@@ -812,6 +860,25 @@ int duck_servo(void *handle, const DuckServo *servo, const void *target, void *h
     ServoBuffers io{target, history, cursor, initialized, root_offset, previous_motor,
                     previous_applied, motor, supply};
     b->servo(*servo, io, st(hip_stream));
+  });
+}
+int duck_servo_substep(void *handle, const DuckServo *servo, const DuckServoSubstep *io,
+                       void *hip_stream) {
+  return guarded([&] {
+    auto *b = as(handle);
+    require(servo != nullptr && io != nullptr, "null servo parameters");
+    require(io->target && io->history && io->initialized && io->root_offset &&
+                io->previous_motor && io->previous_applied,
+            "servo: null buffer");
+    require(servo->lag >= 0 && servo->lag < 1024 && io->cursor >= 0 && io->cursor <= servo->lag,
+            "servo: invalid lag or cursor");
+    const double values[] = {servo->kt, servo->resistance, servo->dtheta_stribeck, servo->alpha,
+                             servo->vin, servo->vin_min, servo->kp_fw, servo->force_limit};
+    for (double v : values)
+      require(std::isfinite(v), "servo: non-finite parameter");
+    require(servo->resistance != 0 && servo->dtheta_stribeck != 0 && servo->vin_min > 0,
+            "servo: resistance, dtheta_stribeck and vin_min must be nonzero");
+    b->servoSubstep(*servo, *io, st(hip_stream));
   });
 }
 int duck_reference(void *handle, const void *target, const void *force, int substeps, double kp,

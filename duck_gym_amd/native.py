@@ -60,6 +60,8 @@ def library():
             "duck_task_step": (ip, [vp, ctypes.POINTER(DuckTask)] + [vp] * 13),
             "duck_task_observe": (ip, [vp, ctypes.POINTER(DuckTask)] + [vp] * 9),
             "duck_servo": (ip, [vp, ctypes.POINTER(DuckServo), vp, vp, ip] + [vp] * 7),
+            "duck_servo_substep": (ip, [vp, ctypes.POINTER(DuckServo),
+                                        ctypes.POINTER(DuckServoSubstep), vp]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(lib, name)
@@ -76,7 +78,7 @@ EXPORTED = (
     "duck_generalized_loads", "duck_reference", "duck_reference_noalloc", "duck_state_layout",
     "duck_export_state",
     "duck_import_state", "duck_last_error", "duck_task_obs_dim", "duck_task_targets",
-    "duck_task_step", "duck_task_observe", "duck_servo",
+    "duck_task_step", "duck_task_observe", "duck_servo", "duck_servo_substep",
 )
 
 MAX_JOINTS = 32
@@ -92,6 +94,28 @@ class DuckServo(ctypes.Structure):
         "load_friction_motor_quad", "friction_viscous", "vin", "vin_drop_gain", "vin_min",
         "kp_fw", "kp_scale", "kd_scale", "friction_scale", "force_limit")] + [
         ("lag", ctypes.c_int)]
+MAX_FEET = 4
+
+
+class DuckServoSubstep(ctypes.Structure):
+    """`DuckServoSubstep` of include/duck_hip.h: buffers and frame data of
+    one fused servo substep."""
+
+    _fields_ = [
+        ("target", ctypes.c_void_p), ("history", ctypes.c_void_p), ("cursor", ctypes.c_int),
+        ("initialized", ctypes.c_void_p), ("root_offset", ctypes.c_void_p),
+        ("previous_motor", ctypes.c_void_p), ("previous_applied", ctypes.c_void_p),
+        ("motor", ctypes.c_void_p), ("supply", ctypes.c_void_p),
+        ("self_contacts", ctypes.c_void_p), ("self_penetration", ctypes.c_void_p),
+        ("root_principal_quat", ctypes.c_double * 4), ("num_feet", ctypes.c_int),
+        ("foot_bodies", ctypes.c_int * MAX_FEET), ("foot_sites", (ctypes.c_double * 3) * MAX_FEET),
+        ("gravity", ctypes.c_void_p), ("angular_velocity", ctypes.c_void_p),
+        ("linear_velocity", ctypes.c_void_p), ("origin_velocity", ctypes.c_void_p),
+        ("foot_forces", ctypes.c_void_p), ("site_positions", ctypes.c_void_p),
+        ("site_velocities", ctypes.c_void_p), ("air_time", ctypes.c_void_p),
+        ("contact_time", ctypes.c_void_p)]
+
+
 TASK_STANDING, TASK_LOCOMOTION, TASK_ROLLOUT = 0, 1, 2
 
 
@@ -164,6 +188,7 @@ class CudaBatch:
         self.device = torch.device("cuda", int(device))
         self.dtype = torch.float64 if fp64 else torch.float32
         self.num_envs = int(num_envs)
+        self.dt = float(dt)
         b, j, c = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
         lib.duck_dims(self._h, ctypes.byref(b), ctypes.byref(j), ctypes.byref(c))
         self.num_bodies, self.num_joints, self.contact_capacity = b.value, j.value, c.value
@@ -329,6 +354,56 @@ class CudaBatch:
     # ---------------------------------------------- tensor-env control step
     def _ptr(self, t, shape, dtype=None):
         return None if t is None else self._check(t, shape, dtype)
+
+    def servo_substep(self, params, target, history, cursor, initialized, root_offset,
+                      previous_motor, previous_applied, *, root_principal_quat=(1.0, 0, 0, 0),
+                      feet=(), foot_sites=None, motor=None, supply=None, self_contacts=None,
+                      self_penetration=None, gravity=None, angular_velocity=None,
+                      linear_velocity=None, origin_velocity=None, foot_forces=None,
+                      site_positions=None, site_velocities=None, air_time=None,
+                      contact_time=None):
+        """One fused BAM substep (include/duck_hip.h duck_servo_substep): the
+        servo, the motor step with zero root force, the self-contact maxima and
+        the refresh() quantities, in one launch.  Outputs are written into the
+        tensors given (any may be None); in/out tensors are updated in place."""
+        E, J = self.num_envs, self.num_joints
+        F = len(feet)
+        if F > MAX_FEET:
+            raise RuntimeError("servo substep: invalid foot count")
+        io = DuckServoSubstep()
+        io.target = self._check(target, [E, J]).value
+        io.history = self._check(history, [int(params.lag) + 1, E, J]).value
+        io.cursor = int(cursor)
+        io.initialized = self._check(initialized, [E], torch.bool).value
+        io.root_offset = self._check(root_offset, [E, 3]).value
+        io.previous_motor = self._check(previous_motor, [E, J]).value
+        io.previous_applied = self._check(previous_applied, [E, J]).value
+        for name, t, shape in (("motor", motor, [E, J, 3]), ("supply", supply, [E]),
+                               ("self_contacts", self_contacts, [E]),
+                               ("self_penetration", self_penetration, [E]),
+                               ("gravity", gravity, [E, 3]),
+                               ("angular_velocity", angular_velocity, [E, 3]),
+                               ("linear_velocity", linear_velocity, [E, 3]),
+                               ("origin_velocity", origin_velocity, [E, 3]),
+                               ("foot_forces", foot_forces, [E, F, 3]),
+                               ("site_positions", site_positions, [E, F, 3]),
+                               ("site_velocities", site_velocities, [E, F, 3]),
+                               ("air_time", air_time, [E, F]), ("contact_time", contact_time, [E, F])):
+            ptr = self._ptr(t, shape)
+            setattr(io, name, None if ptr is None else ptr.value)
+        for k in range(4):
+            io.root_principal_quat[k] = float(root_principal_quat[k])
+        io.num_feet = F
+        sites = [[0.0, 0.0, 0.0]] * F if foot_sites is None else foot_sites
+        for f in range(F):
+            io.foot_bodies[f] = int(feet[f])
+            for k in range(3):
+                io.foot_sites[f][k] = float(sites[f][k])
+        with torch.cuda.device(self.device):
+            code = library().duck_servo_substep(self._h, ctypes.byref(params), ctypes.byref(io),
+                                                self._stream())
+        if code:
+            _raise(code, "servo_substep")
 
     def task_obs_dim(self, task):
         return int(library().duck_task_obs_dim(ctypes.byref(task), self.num_joints))

@@ -214,6 +214,51 @@ int duck_servo(void *handle, const DuckServo *servo, const void *target, void *h
                void *previous_motor, void *previous_applied, void *motor, void *supply,
                void *hip_stream);
 
+#define DUCK_MAX_FEET 4
+
+/* Buffers and frame data of one fused servo substep (duck_servo_substep).
+ * All real buffers are in the batch dtype; the optional ones may be NULL. */
+typedef struct DuckServoSubstep {
+  const void *target;           /* [E,J] targets of this control step */
+  void *history;                /* [lag+1,E,J] ring of targets */
+  int cursor;                   /* slot this substep writes */
+  unsigned char *initialized;   /* [E] ring filled since the last reset */
+  const void *root_offset;      /* [E,3] root COM offset (load pass, origin velocity) */
+  void *previous_motor;         /* [E,J] raw motor torque of the last substep, in/out */
+  void *previous_applied;       /* [E,J] clamped torque of the last substep, in/out */
+  void *motor;                  /* [E,J,3] motor channels of this substep, out */
+  void *supply;                 /* [E] supply voltage, out */
+  void *self_contacts;          /* [E] running maximum of active body contacts, in/out */
+  void *self_penetration;       /* [E] running maximum of body-contact depth, in/out */
+  double root_principal_quat[4]; /* (w, x, y, z): root frame = body 1 frame * its conjugate */
+  int num_feet;                 /* 0 .. DUCK_MAX_FEET */
+  int foot_bodies[DUCK_MAX_FEET];
+  double foot_sites[DUCK_MAX_FEET][3]; /* foot site in its body's frame */
+  void *gravity;                /* [E,3] gravity direction in the root frame, out */
+  void *angular_velocity;       /* [E,3] root angular velocity in the root frame, out */
+  void *linear_velocity;        /* [E,3] root-origin velocity in the root frame, out */
+  void *origin_velocity;        /* [E,3] root-origin velocity in the world, out */
+  void *foot_forces;            /* [E,F,3] ground contact force on each foot body, out */
+  void *site_positions;         /* [E,F,3] foot sites in the world, out */
+  void *site_velocities;        /* [E,F,3] foot site velocities, out */
+  void *air_time;               /* [E,F] seconds since the foot last touched, in/out */
+  void *contact_time;           /* [E,F] seconds the foot has touched, in/out */
+} DuckServoSubstep;
+
+/* One substep of the BAM-actuated environment in one launch
+ * (python/duck_gym/bam_env.py:307-337 with refresh(), bam_env.py:128-155):
+ * the servo substep of duck_servo, the motor step of duck_step_motor with a
+ * zero root force, then the self-contact statistics folded into their
+ * running maxima (bam_env.py:333-335) and the quantities refresh() derives
+ * from the new state: gravity and velocities in the root frame, the ground
+ * contact force on each foot (duck_contact_forces with ground_only), foot
+ * site positions and velocities, and the air/contact timers (a foot touches
+ * when its force exceeds 1e-5 N).  The caller advances `cursor` per
+ * substep as for duck_servo.  No reference counterpart as one call: it
+ * replaces the reference loop's five calls and torch arithmetic. */
+int duck_servo_substep(void *handle, const DuckServo *servo, const DuckServoSubstep *io,
+                       void *hip_stream);
+
 const char *duck_last_error(void);
 
 #ifdef __cplusplus
