@@ -119,6 +119,18 @@ template <class S> __device__ __forceinline__ S &blobAt(unsigned char *base, lon
   return *reinterpret_cast<S *>(base + bytes * e);
 }
 
+// The dispatcher hands consecutive workgroups to the 8 XCDs in turn, and
+// each XCD has its own L2.  Workgroup b runs the environments of block
+// xcdBlock(b, n) instead of block b: the workgroups of one XCD take one
+// contiguous run of blocks, so the rows of the per-env inputs (targets,
+// forces) that neighbouring environments share come from one L2 once.  A
+// bijection of [0, n), whatever the placement, so only the speed depends on it.
+constexpr int kXcds = 8;
+__device__ __forceinline__ int xcdBlock(int b, int n) {
+  const int q = n / kXcds, r = n % kXcds, x = b % kXcds, k = b / kXcds;
+  return x < r ? x * (q + 1) + k : r * (q + 1) + (x - r) * q + k;
+}
+
 // Copy words [a, b) of one environment's blob between HBM and LDS (both
 // 16-byte aligned) with the L lanes of its group: the 16-byte interior in
 // dwordx4 chunks, up to `Chunks` per lane loaded before any is stored (one
@@ -179,49 +191,64 @@ __device__ __forceinline__ void copyRanges(unsigned *dst, const unsigned *src, i
 }
 
 // One environment's blob into LDS.  First round: the group every step reads
-// and writes (poses through the counts), the first kWarmContacts ground
-// contacts and, with `bodies`, the reset-only group; second round, once the
-// counts are known: the further live contacts and, when the launch may keep
-// them (`keep`, or a failed environment), the last controls and colouring.
-// Returns whether the controls were read.
+// and writes (poses through the counts) with the first kWarmContacts ground
+// contacts as one range and, with `bodies`, the reset-only group; second
+// round, once the counts are known: the further live contacts, for a launch
+// that holds its controls (`held`) or sets motor channels (`motor`) the
+// targets and force, and for a held launch the drive parameters.
 constexpr int kWarmContacts = 8;
 template <class S>
-__device__ bool loadEnv(S &dst, const S *src, int lane, int L, bool bodies, bool keep) {
-  constexpr int header = int(headerBytes<S>() / 4);
-  constexpr int xStart = int(offsetof(S, x) / 4), tStart = int(offsetof(S, target) / 4);
+__device__ void loadEnv(S &dst, const S *src, int lane, int L, bool bodies, bool held, bool motor) {
+  constexpr int header = int(headerBytes<S>() / 4), hot = int(hotBegin<S>() / 4);
   constexpr int CGcap = int(sizeof(S::gc) / sizeof(S::gc[0]));
   constexpr int CScap = int(sizeof(S::sc) / sizeof(S::sc[0]));
   constexpr int gcWords = int(sizeof(decltype(S::gc[0])) / 4);
   constexpr int scStart = int(offsetof(S, sc) / 4), scWords = int(sizeof(decltype(S::sc[0])) / 4);
   constexpr int warm = header + (kWarmContacts < CGcap ? kWarmContacts : CGcap) * gcWords;
-  static_assert(xStart % 4 == 0 && tStart % 4 == 0 && header % 4 == 0 && warm % 4 == 0,
-                "copied groups start on 16-byte boundaries");
+  constexpr int reset = int(resetBegin<S>() / 4), end = int(sizeof(S) / 4);
+  static_assert(hot % 32 == 0 && header % 4 == 0 && warm % 4 == 0 && reset % 4 == 0 && end % 4 == 0,
+                "copied groups start on 16-byte boundaries, group 1 on a 128-byte one");
   int ngc = src->ngc, nsc = src->nsc;
-  keep = keep || src->failed;
   unsigned *d = reinterpret_cast<unsigned *>(&dst);
   const unsigned *s = reinterpret_cast<const unsigned *>(src);
-  copyRanges<16>(d, s, bodies ? 0 : xStart, tStart, header, warm, lane, L);
+  copyRanges<16>(d, s, hot, warm, reset, bodies ? end : reset, lane, L);
   ngc = ngc < 0 ? 0 : (ngc > CGcap ? CGcap : ngc);
   nsc = nsc < 0 ? 0 : (nsc > CScap ? CScap : nsc);
   copyWords<4>(d, s, warm, header + ngc * gcWords, lane, L);
   copyWords<4>(d, s, scStart, scStart + nsc * scWords, lane, L);
-  if (keep)
-    copyWords<4>(d, s, tStart, int(coloursEndBytes<S>() / 4), lane, L);
-  return keep;
+  if (held || motor)
+    copyWords<4>(d, s, int(targetBegin<S>() / 4), hot, lane, L);
+  // the lead words in the targets' first 32-byte sector: a launch that sets
+  // the targets writes whole sectors (a partial one would make the L2 read
+  // it first), and these words hold zeros, as the state was created
+  for (int i = int(targetBegin<S>() / 32 * 8) + lane; i < int(targetBegin<S>() / 4); i += L)
+    d[i] = 0;
+  if (held)
+    copyWords<4>(d, s, int(driveBegin<S>() / 4), int(driveEnd<S>() / 4), lane, L);
 }
 
-// LDS -> HBM after a step: the groups from `from` (the step's write-back
-// starts at x: mass, inertia and friction only change on reset) through the
-// colouring, and exactly the live contacts.
-template <class S> __device__ void storeEnv(S *dst, const S &src, int lane, int L, int from) {
+// What a step writes of the drive parameters and of the colouring.
+enum DriveWrite { kWriteNoDrive = 0, kWriteDrive = 1, kWriteMotorDrive = 2 };
+
+// LDS -> HBM after a step: from word `from` (the targets, the force or group
+// 1, by what the launch set) through the live ground contacts as one range,
+// the live body contacts, and the drive parameters (all, the motor-written
+// three, or none) and the colouring where they changed.  Mass, inertia and
+// friction only change on reset.
+template <class S>
+__device__ void storeEnv(S *dst, const S &src, int lane, int L, int from, int driveWrite, bool colours) {
   constexpr int header = int(headerBytes<S>() / 4);
   constexpr int gcWords = int(sizeof(decltype(S::gc[0])) / 4);
   constexpr int scStart = int(offsetof(S, sc) / 4), scWords = int(sizeof(decltype(S::sc[0])) / 4);
   unsigned *d = reinterpret_cast<unsigned *>(dst);
   const unsigned *s = reinterpret_cast<const unsigned *>(&src);
-  copyWords<16>(d, s, from, int(coloursEndBytes<S>() / 4), lane, L);
-  copyWords<4>(d, s, header, header + src.ngc * gcWords, lane, L);
+  copyWords<16>(d, s, from, header + src.ngc * gcWords, lane, L);
   copyWords<4>(d, s, scStart, scStart + src.nsc * scWords, lane, L);
+  if (driveWrite != kWriteNoDrive)
+    copyWords<4>(d, s, int((driveWrite == kWriteDrive ? driveBegin<S>() : motorBegin<S>()) / 4),
+                 int(driveEnd<S>() / 4), lane, L);
+  if (colours)
+    copyWords<4>(d, s, int(coloursBegin<S>() / 4), int(coloursEnd<S>() / 4), lane, L);
 }
 
 // MPR narrow phase between two shapes (convex.cuh:124-217).  The shape data
@@ -577,7 +604,7 @@ __device__ __forceinline__ void stepBody(const StepArgs &args, const ServoArgs<R
   const DeviceModel<R> &M = *static_cast<const DeviceModel<R> *>(args.model);
   const V3<R> *points = static_cast<const V3<R> *>(args.points);
   const int t = threadIdx.x, lane = t % L, g = t / L;
-  const int e = blockIdx.x * G + g;
+  const int e = xcdBlock(blockIdx.x, gridDim.x) * G + g;
   const bool valid = e < args.count;
   Env &E = envs[g];
   const int nb = args.nb, nj = args.nj, ns = args.ns, np = args.np;
@@ -681,9 +708,9 @@ __device__ __forceinline__ void stepBody(const StepArgs &args, const ServoArgs<R
   State *gs = valid ? &blobAt<State>(args.states, args.blobBytes, e) : nullptr;
   static_assert(L >= 4, "blob copies give each of the first three lanes an end word");
   static_assert(CS <= B, "the staged pair table holds B pairs");
-  bool kept = false; // the last controls and colouring were read
   if (valid) {
-    kept = loadEnv<State>(E.s, gs, lane, L, args.bodies != 0, args.motorMode != kTargetControls);
+    loadEnv<State>(E.s, gs, lane, L, args.bodies != 0, args.motorMode == kHeldControls,
+                   args.motorMode == kMotorControls);
     if (!args.bodies) {
       // the model's masses, inertia and shape friction, as reset writes them
       for (int b = lane; b < B; b += L) {
@@ -728,30 +755,45 @@ __device__ __forceinline__ void stepBody(const StepArgs &args, const ServoArgs<R
   bad = groupOr<L>(bad);
   __syncthreads();
   bool active = false;
+  // What the blob's drive parameters and colouring hold before this launch
+  // (read before any lane rewrites the stamps).
+  int driveWrite = kWriteNoDrive;
+  int writeFrom = int(hotBegin<State>() / 4);
+  const int driveIn = valid ? E.s.drive : kDriveOther;
+  const bool modelColoursIn = valid && E.s.modelColours != 0;
   if (valid) {
     if (args.motorMode == kHeldControls) {
       // State::advance (kernel.cuh:421-443): the controls in the state as
       // they stand
       active = !E.s.failed;
     } else if (args.motorMode == kMotorControls) {
-      // setMotor applies the channels even when they are invalid.
+      // setMotor applies the channels even when they are invalid (slots
+      // past the last hinge hold zeros, as the state was created).
 #pragma unroll
       for (int r = 0; r < JPL; ++r) {
         const int j = lane + r * L;
-        if (j >= nj)
+        if (j >= J)
           continue;
+        const bool in = j < nj;
         E.s.kp[j] = 0;
         E.s.maxTorque[j] = 0;
-        E.s.torque[j] = ctl[r][0];
-        E.s.frictionloss[j] = ctl[r][1];
-        E.s.damping[j] = ctl[r][2];
+        E.s.torque[j] = in ? ctl[r][0] : R(0);
+        E.s.frictionloss[j] = in ? ctl[r][1] : R(0);
+        E.s.damping[j] = in ? ctl[r][2] : R(0);
       }
       if (lane < 3)
         E.s.force[lane] = fin;
-      if (bad && lane == 0)
-        E.s.failed = 1;
+      if (lane == 0) {
+        if (bad)
+          E.s.failed = 1;
+        E.s.drive = kDriveMotor;
+      }
+      driveWrite = driveIn == kDriveMotor ? kWriteMotorDrive : kWriteDrive;
+      writeFrom = int(forceBegin<State>() / 32 * 8);
       active = !E.s.failed && !bad;
     } else if (!E.s.failed && !bad) {
+      const R kp = R(args.kp), limit = R(args.limit);
+      const bool same = driveIn == kDriveTarget && sameBits(E.s.driveKp, kp) && sameBits(E.s.driveLimit, limit);
 #pragma unroll
       for (int r = 0; r < JPL; ++r) {
         const int j = lane + r * L;
@@ -760,24 +802,26 @@ __device__ __forceinline__ void stepBody(const StepArgs &args, const ServoArgs<R
         // slots past the last hinge hold zeros, as the state was created
         const bool in = j < nj;
         E.s.target[j] = in ? ctl[r][0] : R(0);
-        E.s.kp[j] = in ? R(args.kp) : R(0);
-        E.s.maxTorque[j] = in ? R(args.limit) : R(0);
+        E.s.kp[j] = in ? kp : R(0);
+        E.s.maxTorque[j] = in ? limit : R(0);
         E.s.torque[j] = in ? defs[r][0] : R(0);
         E.s.frictionloss[j] = in ? defs[r][1] : R(0);
         E.s.damping[j] = in ? defs[r][2] : R(0);
       }
       if (lane < 3)
         E.s.force[lane] = fin;
+      if (lane == 0) {
+        E.s.drive = kDriveTarget;
+        E.s.driveKp = kp;
+        E.s.driveLimit = limit;
+      }
+      driveWrite = same ? kWriteNoDrive : kWriteDrive;
+      writeFrom = int(targetBegin<State>() / 32 * 8);
       active = true;
-    } else {
+    } else if (lane == 0) {
       // invalid controls: the environment keeps its last controls and
-      // colouring, which this launch has not read yet
-      constexpr int tStart = int(offsetof(State, target) / 4), cEnd = int(coloursEndBytes<State>() / 4);
-      if (!kept)
-        copyWords<4>(reinterpret_cast<unsigned *>(&E.s), reinterpret_cast<const unsigned *>(gs), tStart,
-                     cEnd, lane, L);
-      if (lane == 0)
-        E.s.failed = 1;
+      // colouring, which stay in the blob as they are
+      E.s.failed = 1;
     }
   }
   const bool ran = active;
@@ -1460,9 +1504,10 @@ __device__ __forceinline__ void stepBody(const StepArgs &args, const ServoArgs<R
           for (int k = 3; k < 5; ++k)
             dAxis = mx(dAxis, mabs(jd.C[k]));
         };
-        static_assert(L <= J && L <= CG, "a lane's first hinge and contact slots exist");
+        static_assert(L <= CG, "a lane's first contact slot exists");
+        // a lane without a hinge evaluates an existing slot and stores nothing
         const bool hasJoint = dualJoint >= 0;
-        auto j0 = stp.jointDual(hasJoint ? dualJoint : lane, hasJoint, error, ends0);
+        auto j0 = stp.jointDual(hasJoint ? dualJoint : (lane < J ? lane : 0), hasJoint, error, ends0);
         const auto g0 = stp.groundDual(lane, lane < ngc, errC0, owner0);
         if (__any(j0.wide) && j0.wide)
           error = stp.frictionDual(j0, wrapAngle(j0.angle));
@@ -1600,8 +1645,16 @@ __device__ __forceinline__ void stepBody(const StepArgs &args, const ServoArgs<R
   if constexpr (Servo)
     if (valid && lane == 0)
       servoEpilogue<R, B, J, CG, CS>(sv, M, E, e);
+  // The colouring of an environment that stepped is the model's exactly when
+  // no body took a fresh colour; it is written when the blob holds another.
+  const bool modelColours = E.s.colorCount == 2;
+  const bool writeColours = ran && !(modelColours && modelColoursIn);
+  __syncthreads();
+  if (ran && lane == 0)
+    E.s.modelColours = modelColours ? 1 : 0;
+  __syncthreads();
   if (valid)
-    storeEnv<State>(gs, E.s, lane, L, int(offsetof(State, x) / 4));
+    storeEnv<State>(gs, E.s, lane, L, writeFrom, driveWrite, writeColours);
 }
 
 template <class R, int B, int J, int CG, int CS, int L, int PL = defaultSolveLanes(L)>

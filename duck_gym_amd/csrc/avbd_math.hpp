@@ -38,6 +38,13 @@ DUCK_HD float mabs(float x) { return fabsf(x); }
 DUCK_HD double mabs(double x) { return fabs(x); }
 DUCK_HD bool mfinite(float x) { return __builtin_isfinite(x); }
 DUCK_HD bool mfinite(double x) { return __builtin_isfinite(x); }
+// Bitwise equality (distinguishes -0 from +0; a NaN equals its own bits).
+DUCK_HD bool sameBits(float a, float b) {
+  return __builtin_bit_cast(unsigned, a) == __builtin_bit_cast(unsigned, b);
+}
+DUCK_HD bool sameBits(double a, double b) {
+  return __builtin_bit_cast(unsigned long long, a) == __builtin_bit_cast(unsigned long long, b);
+}
 
 // Solver arithmetic.  The float solver uses the gfx950 reciprocal, square
 // root and reciprocal square root instructions (about 1 ulp) instead of the

@@ -62,11 +62,42 @@ template <class R, int B, int J, int CG, int CS> struct StateView {
       s.diag[k] = 0;
     s.friction = -1;
     s.colorCount = 2;
-    for (int b = 0; b < M.nb; ++b)
-      s.colors[b] = M.colors[b];
+    for (int b = 0; b < B; ++b)
+      s.colors[b] = b < M.nb ? M.colors[b] : 0;
+    s.modelColours = 1;
+    s.drive = kDriveOther;
     s.failed = 0;
     s.ngc = 0;
     s.nsc = 0;
+  }
+  // Clears the claims of `drive` and `modelColours` that the blob's bytes do
+  // not bear out (an imported state); keeps every true one, so that an export
+  // and import of the same batch's state is the identity.
+  DUCK_HD void checkStamps() {
+    bool ok = true;
+    if (s.drive == kDriveTarget || s.drive == kDriveMotor) {
+      const bool target = s.drive == kDriveTarget;
+      for (int j = 0; j < J; ++j) {
+        const bool in = j < M.nj;
+        ok = ok && sameBits(s.kp[j], in && target ? s.driveKp : R(0)) &&
+             sameBits(s.maxTorque[j], in && target ? s.driveLimit : R(0));
+        if (target)
+          ok = ok && sameBits(s.torque[j], in ? M.torque[j] : R(0)) &&
+               sameBits(s.frictionloss[j], in ? M.frictionloss[j] : R(0)) &&
+               sameBits(s.damping[j], in ? M.damping[j] : R(0));
+      }
+    } else {
+      ok = s.drive == kDriveOther;
+    }
+    if (!ok)
+      s.drive = kDriveOther;
+    if (s.modelColours != 0) {
+      bool same = s.modelColours == 1;
+      for (int b = 0; b < B; ++b)
+        same = same && s.colors[b] == (b < M.nb ? M.colors[b] : 0);
+      if (!same)
+        s.modelColours = 0;
+    }
   }
   // Root offset and forward kinematics down the hinge list (kernel.cuh:397-420).
   DUCK_HD void resetPose(const R *q, const R *root) {
@@ -100,6 +131,16 @@ __global__ void initializeKernel(const DeviceModel<R> *model, unsigned char *sta
     return;
   StateView<R, B, J, CG, CS> v{*model, blobAt<EnvState<R, B, J, CG, CS>>(states, blobBytes, e)};
   v.initialize();
+}
+
+template <class R, int B, int J, int CG, int CS>
+__global__ void checkStampsKernel(const DeviceModel<R> *model, unsigned char *states,
+                                  long long blobBytes, int count) {
+  int e = blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= count)
+    return;
+  StateView<R, B, J, CG, CS> v{*model, blobAt<EnvState<R, B, J, CG, CS>>(states, blobBytes, e)};
+  v.checkStamps();
 }
 
 // ext (optional, per env): [friction (<0 keeps the shape friction),

@@ -128,32 +128,56 @@ DUCK_HD int scPack(int body, int other, int shape, int otherShape, bool stick) {
 enum DiagSlot { kJointError, kPenetration, kContacts, kConverged, kAxisError, kIterations };
 
 // Persistent per-env state; the HBM blob is exactly this struct.  Its fields
-// are grouped by what a step does with them, each group starting on a 16-byte
-// boundary so that a launch copies whole groups:
-//  1. set by reset only; a launch reads them only when some environment's
+// are grouped by what a step does with them:
+//  0. the last controls' targets and external force: written by every launch
+//     that sets them, read only by one that holds them or sets motor
+//     channels (which keep the targets); they end where group 1 starts, so a
+//     launch writes them and group 1 as one range;
+//  1. read and written by every step, from a 128-byte boundary of the blob
+//     through the live entries of the ground-contact list (one contiguous
+//     range), then the live body contacts;
+//  2. the drive parameters of the last controls (kp through damping): read
+//     only by a launch that holds its controls, written only when they
+//     change.  `drive` records what they hold: kDriveTarget -- kp and
+//     maxTorque are `driveKp`/`driveLimit` and torque, frictionloss and
+//     damping the model's, on every hinge (zeros past the last); kDriveMotor
+//     -- kp and maxTorque are zero; kDriveOther -- no claim.  A target launch
+//     with the same kp and limit, and a motor launch after a motor launch,
+//     find their values in place and skip the rewrite;
+//  3. the colouring of the last step: written only when it differs from what
+//     the blob holds; `modelColours` records that the blob holds the model's
+//     colours (zeros past the last body);
+//  4. set by reset only; a launch reads them only when some environment's
 //     may differ from the model's (reset with per-env extensions, imported
-//     states), and never writes them back;
-//  2. read and written by every step;
-//  3. the last controls: written by every step, read only when a launch may
-//     keep some of them (held or motor controls, a failed environment);
-//  4. the colouring of the last step: written by every step, read only when
-//     a launch may keep it (a failed environment);
-//  5. the compacted contact lists (live entries only).
+//     states), and never writes them back.
+// Every claim of `drive` and `modelColours` holds for the blob's bytes: the
+// writers keep them so, and an import clears any that the imported bytes do
+// not bear out.  `lead` (never copied, zero as created) places group 1 on the
+// 128-byte boundary.
+enum DriveKind { kDriveOther = 0, kDriveTarget = 1, kDriveMotor = 2 };
+template <class R, int J> constexpr int leadBytes() {
+  constexpr int controls = int(sizeof(R)) * (J + 3);
+  return (controls + 4 + 127) / 128 * 128 - controls;
+}
 template <class R, int B, int J, int CG, int CS> struct EnvState {
-  R mass[B], inertia[3][B];
-  R friction; // per-env ground friction; < 0 selects the shape friction
-  alignas(16) R x[3][B];
-  R q[4][B], v[3][B], w[3][B];
+  unsigned char lead[leadBytes<R, J>()];
+  R target[J];
   R force[3];
+  R x[3][B];
+  R q[4][B], v[3][B], w[3][B];
   R lambda[7][J], penalty[7][J];
   R lambdaF[J], penaltyF[J];
   R diag[8];
   int failed, ngc, nsc, colorCount;
-  alignas(16) R target[J];
-  R kp[J], maxTorque[J], torque[J], frictionloss[J], damping[J];
-  alignas(16) int colors[B]; // model colours + fresh ones
+  int drive, modelColours;
+  R driveKp, driveLimit;
   alignas(16) GroundContact<R> gc[CG];
   SelfContact<R> sc[CS];
+  alignas(16) R kp[J];
+  R maxTorque[J], torque[J], frictionloss[J], damping[J];
+  alignas(16) int colors[B]; // model colours + fresh ones
+  alignas(16) R mass[B], inertia[3][B];
+  R friction; // per-env ground friction; < 0 selects the shape friction
 };
 
 template <class R, int B, int J, int CG, int CS> struct EnvLdsCore {
@@ -186,10 +210,20 @@ struct EnvLds : EnvLdsCore<R, B, J, CG, CS> {
 template <class R, int B, int J, int CG, int CS, int L>
 struct EnvLds<R, B, J, CG, CS, L, 0> : EnvLdsCore<R, B, J, CG, CS> {};
 
-// Word offset of the contact lists inside the blob (only their live entries
-// are copied), and the end of the colouring: the alignment padding between
-// the two is never copied, so it keeps the zeros the state was created with.
+// Byte offsets of the ground-contact list inside the blob (only its live
+// entries are copied), of the targets, the force and group 1, and the byte
+// ranges of the drive parameters, of the
+// three motor-written ones (torque through damping), of the colouring and of
+// the reset-only group.
 template <class S> constexpr size_t headerBytes() { return offsetof(S, gc); }
-template <class S> constexpr size_t coloursEndBytes() { return offsetof(S, colors) + sizeof(S::colors); }
+template <class S> constexpr size_t targetBegin() { return offsetof(S, target); }
+template <class S> constexpr size_t forceBegin() { return offsetof(S, force); }
+template <class S> constexpr size_t hotBegin() { return offsetof(S, x); }
+template <class S> constexpr size_t driveBegin() { return offsetof(S, kp); }
+template <class S> constexpr size_t motorBegin() { return offsetof(S, torque); }
+template <class S> constexpr size_t driveEnd() { return offsetof(S, damping) + sizeof(S::damping); }
+template <class S> constexpr size_t coloursBegin() { return offsetof(S, colors); }
+template <class S> constexpr size_t coloursEnd() { return offsetof(S, colors) + sizeof(S::colors); }
+template <class S> constexpr size_t resetBegin() { return offsetof(S, mass); }
 
 } // namespace duckhip

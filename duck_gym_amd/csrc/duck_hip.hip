@@ -258,7 +258,7 @@ public:
     device = gpu;
     fpBits = sizeof(R) * 8;
     contactCapacity = host.groundCapacity + host.selfCapacity;
-    blobBytes = (sizeof(State) + 255) / 256 * 256;
+    blobBytes = (sizeof(State) + 127) / 128 * 128;
     for (auto &j : host.joints)
       names.push_back(j.name);
     DeviceGuard guard(device);
@@ -551,6 +551,8 @@ public:
     wait(s);
     hipCheck(hipMemcpyAsync(dStates, src, size_t(blobBytes) * count, hipMemcpyDeviceToDevice, s),
              "import_state");
+    checkStampsKernel<R, B, J, CG, CS><<<blocks64(count), 64, 0, s>>>(dModel, dStates, blobBytes, count);
+    launched("checkStampsKernel");
     customBodies = true;
     record(s);
   }
@@ -588,7 +590,8 @@ const char *kMicroDuckJoints[14] = {
     "head_roll",       "right_hip_yaw",  "right_hip_roll", "right_hip_pitch",
     "right_knee",      "right_ankle"};
 
-// MicroDuck-sized models: float runs 4 environments per wave with two lanes
+// MicroDuck-sized models (16 bodies and 14 hinges, the reference's
+// MicroDuckState, kernel.cuh:1098): float runs 4 environments per wave with two lanes
 // per block solve (16 lanes per env); double runs 8 environments per wave
 // with one lane per block solve, which keeps the reference's accumulation
 // order (DUCK_FLAG_SPLIT selects the float layout for double too).  Four
@@ -599,11 +602,11 @@ template <class R>
 BatchBase *makeBatch(HostModel &&m, int n, double dt, int iterations, int device, bool split) {
   const int nb = m.bodies.size(), nj = m.joints.size(), ns = m.shapes.size(),
             np = m.pairs.size();
-  if (nb <= 16 && nj <= 16 && ns <= 16 && np <= 8 && m.groundCapacity <= 64) {
+  if (nb <= 16 && nj <= 14 && ns <= 16 && np <= 8 && m.groundCapacity <= 64) {
     if constexpr (sizeof(R) == sizeof(double))
       if (!split)
-        return new Batch<R, 16, 16, 64, 8, 8>(std::move(m), n, dt, iterations, device);
-    return new Batch<R, 16, 16, 64, 8, 16>(std::move(m), n, dt, iterations, device);
+        return new Batch<R, 16, 14, 64, 8, 8>(std::move(m), n, dt, iterations, device);
+    return new Batch<R, 16, 14, 64, 8, 16>(std::move(m), n, dt, iterations, device);
   }
   // The generic state: 32 bodies and hinges, 4 ground contacts for each of
   // up to 32 shapes and one per body-contact pair (the reference's
