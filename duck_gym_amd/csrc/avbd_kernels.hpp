@@ -825,6 +825,9 @@ __device__ __forceinline__ void stepBody(const StepArgs &args, const ServoArgs<R
     }
   }
   const bool ran = active;
+  // the write-back's plan waits in LDS, not in registers across the solve
+  if (valid && lane == 0)
+    E.writeback = (modelColoursIn ? 1 : 0) | driveWrite << 1 | writeFrom << 8;
   if (ran && lane == 0) {
     for (int k = 0; k < 8; ++k)
       E.stepDiag[k] = 0;
@@ -1647,14 +1650,15 @@ __device__ __forceinline__ void stepBody(const StepArgs &args, const ServoArgs<R
       servoEpilogue<R, B, J, CG, CS>(sv, M, E, e);
   // The colouring of an environment that stepped is the model's exactly when
   // no body took a fresh colour; it is written when the blob holds another.
+  const int plan = valid ? E.writeback : 0;
   const bool modelColours = E.s.colorCount == 2;
-  const bool writeColours = ran && !(modelColours && modelColoursIn);
+  const bool writeColours = ran && !(modelColours && (plan & 1));
   __syncthreads();
   if (ran && lane == 0)
     E.s.modelColours = modelColours ? 1 : 0;
   __syncthreads();
   if (valid)
-    storeEnv<State>(gs, E.s, lane, L, writeFrom, driveWrite, writeColours);
+    storeEnv<State>(gs, E.s, lane, L, plan >> 8, (plan >> 1) & 3, writeColours);
 }
 
 template <class R, int B, int J, int CG, int CS, int L, int PL = defaultSolveLanes(L)>

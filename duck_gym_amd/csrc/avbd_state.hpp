@@ -192,7 +192,10 @@ template <class R, int B, int J, int CG, int CS> struct EnvLdsCore {
   uint64_t gmask[(CG + 63) / 64][B];
   uint32_t smask[B];
   int order[B], colorStart[CS + 3];
-  int done, pad0, pad1, pad2;
+  // what the write-back copies, decided with the controls: the first word
+  // (bits 8-), the drive parameters (bits 1-2), and whether the blob held the
+  // model's colours (bit 0)
+  int writeback, pad0, pad1, pad2;
   int shapeCount[B]; // shapes <= B
   int pairHit[CS];   // body-contact pairs <= CS
 };
