@@ -588,6 +588,87 @@ __device__ __forceinline__ void servoEpilogue(const ServoArgs<R> &sv, const Devi
 // Per-launch step: controls, `substeps` physics steps, write-back; with
 // Servo, the controls are the motor channels of one servo substep and the
 // launch ends with the substep's statistics and refresh quantities.
+// The model's solve-time view (Frames), built once per batch by framesKernel
+// into device memory; every workgroup of a step copies it into LDS whole (one
+// round of loads instead of a round trip per field).  Thread t of T.
+template <class R, int B, int J>
+__device__ void stageFrames(Frames<R, B, J> &F, const DeviceModel<R> &M, int t, int T) {
+  const int nb = M.nb, nj = M.nj, ns = M.ns, np = M.np;
+  // The joint model.  The slots of absent hinges hold
+  // a zero hinge between body 0 and itself: a lane without a hinge evaluates
+  // one (slot 0 of a model without hinges), masked, and its finite values
+  // keep the masked stamps zero.
+  for (int j = t + nj; j < J; j += T) {
+    F.a[j] = F.b[j] = F.limited[j] = 0;
+    F.lo[j] = F.hi[j] = F.armature[j] = 0;
+#pragma unroll
+    for (int k = 0; k < 3; ++k)
+      F.ra[k][j] = F.rb[k][j] = F.axisA[k][j] = F.axisB[k][j] = F.tangentA[k][j] = F.tangentB[k][j] = 0;
+  }
+  for (int i = t + 2 * nj; i < 2 * J; i += T)
+    F.adj[i] = 0;
+  for (int j = t; j < nj; j += T) {
+    F.a[j] = M.ja[j];
+    F.b[j] = M.jb[j];
+    F.limited[j] = M.limited[j];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      F.ra[k][j] = M.ra[k][j];
+      F.rb[k][j] = M.rb[k][j];
+      F.axisA[k][j] = M.axisA[k][j];
+      F.axisB[k][j] = M.axisB[k][j];
+      F.tangentA[k][j] = M.tangentA[k][j];
+      F.tangentB[k][j] = M.tangentB[k][j];
+    }
+    F.lo[j] = M.lo[j];
+    F.hi[j] = M.hi[j];
+    F.armature[j] = M.armature[j];
+  }
+  for (int i = t; i <= nb; i += T)
+    F.adjStart[i] = M.adjStart[i];
+  for (int i = t; i < 2 * nj; i += T)
+    F.adj[i] = M.adjPacked[i];
+  for (int i = t; i < ns; i += T)
+    F.shapeFriction[i] = M.sfriction[i];
+  for (int i = t; i < nb; i += T) {
+    F.order[i] = M.order[i];
+    F.mass[i] = M.mass[i];
+  }
+  for (int i = t; i < ns; i += T) {
+    F.sbody[i] = M.sbody[i];
+    F.sflags[i] = M.sflags[i] | M.stype[i] << 4;
+    F.scount[i] = M.scount[i];
+    F.sradius[i] = M.radius[i];
+#pragma unroll
+    for (int k = 0; k < 3; ++k)
+      F.sinterior[k][i] = M.interior[k][i];
+  }
+  for (int i = t; i < np; i += T)
+    F.pair[i] = M.pa[i] | M.pb[i] << 8;
+  for (int i = t; i < kCachedPoints * 3 * ns; i += T) {
+    const int si = i % ns, c = (i / ns) % 3, k = i / (3 * ns);
+    const int type = M.stype[si];
+    R v = M.spts[k][c][si];
+    if (type == 0 || type == 2) {
+      // the shape formula's data, in the operations the narrow phase used
+      // to evaluate on each support query
+      const Q4<R> sq{M.sq[0][si], M.sq[1][si], M.sq[2][si], M.sq[3][si]};
+      v = k == 0   ? M.center[c][si]
+          : k == 1 ? (c < 2 ? M.size[c][si] : R(0))
+          : k == 2 ? comp(rotate(sq, V3<R>{0, 0, 1}), c)
+                   : R(0);
+    }
+    F.spt[k][c][si] = v;
+  }
+  if (t < 3)
+    F.colorStart[t] = M.colorStart[t];
+}
+
+template <class R, int B, int J>
+__global__ void framesKernel(const DeviceModel<R> *model, Frames<R, B, J> *out) {
+  stageFrames<R, B, J>(*out, *model, threadIdx.x, blockDim.x);
+}
+
 template <class R, int B, int J, int CG, int CS, int L, int PL, bool Servo>
 __device__ __forceinline__ void stepBody(const StepArgs &args, const ServoArgs<R> &sv) {
   constexpr int G = 64 / L;
@@ -636,74 +717,19 @@ __device__ __forceinline__ void stepBody(const StepArgs &args, const ServoArgs<R
   if (!Servo && valid && lane < 3 && args.motorMode != kHeldControls)
     fin = static_cast<const R *>(args.forces)[size_t(e) * 3 + lane];
 
-  // Stage the joint model (all 64 lanes).  The slots of absent hinges hold
-  // a zero hinge between body 0 and itself: a lane without a hinge evaluates
-  // one (slot 0 of a model without hinges), masked, and its finite values
-  // keep the masked stamps zero.
-  for (int j = t + nj; j < J; j += 64) {
-    F.a[j] = F.b[j] = F.limited[j] = 0;
-    F.lo[j] = F.hi[j] = F.armature[j] = 0;
+  // The model's Frames image straight into LDS (global_load_lds_dwordx4:
+  // lane t's 16 bytes land at chunk t of the destination, no registers held),
+  // in flight together with the controls and the blob copy below.
+  {
+    constexpr int FC = int(sizeof(Frames<R, B, J>) / 16);
+    static_assert(sizeof(Frames<R, B, J>) % 16 == 0, "the Frames image is whole dwordx4 chunks");
+    const uint4 *src = static_cast<const uint4 *>(args.frames);
+    auto *dst = (__attribute__((address_space(3))) uint4 *)(&F);
 #pragma unroll
-    for (int k = 0; k < 3; ++k)
-      F.ra[k][j] = F.rb[k][j] = F.axisA[k][j] = F.axisB[k][j] = F.tangentA[k][j] = F.tangentB[k][j] = 0;
+    for (int k = 0; k < (FC + 63) / 64; ++k)
+      if (t + 64 * k < FC)
+        __builtin_amdgcn_global_load_lds(src + t + 64 * k, dst + 64 * k, 16, 0, 0);
   }
-  for (int i = t + 2 * nj; i < 2 * J; i += 64)
-    F.adj[i] = 0;
-  for (int j = t; j < nj; j += 64) {
-    F.a[j] = M.ja[j];
-    F.b[j] = M.jb[j];
-    F.limited[j] = M.limited[j];
-#pragma unroll
-    for (int k = 0; k < 3; ++k) {
-      F.ra[k][j] = M.ra[k][j];
-      F.rb[k][j] = M.rb[k][j];
-      F.axisA[k][j] = M.axisA[k][j];
-      F.axisB[k][j] = M.axisB[k][j];
-      F.tangentA[k][j] = M.tangentA[k][j];
-      F.tangentB[k][j] = M.tangentB[k][j];
-    }
-    F.lo[j] = M.lo[j];
-    F.hi[j] = M.hi[j];
-    F.armature[j] = M.armature[j];
-  }
-  for (int i = t; i <= nb; i += 64)
-    F.adjStart[i] = M.adjStart[i];
-  for (int i = t; i < 2 * nj; i += 64)
-    F.adj[i] = M.adjPacked[i];
-  for (int i = t; i < ns; i += 64)
-    F.shapeFriction[i] = M.sfriction[i];
-  for (int i = t; i < nb; i += 64) {
-    F.order[i] = M.order[i];
-    F.mass[i] = M.mass[i];
-  }
-  for (int i = t; i < ns; i += 64) {
-    F.sbody[i] = M.sbody[i];
-    F.sflags[i] = M.sflags[i] | M.stype[i] << 4;
-    F.scount[i] = M.scount[i];
-    F.sradius[i] = M.radius[i];
-#pragma unroll
-    for (int k = 0; k < 3; ++k)
-      F.sinterior[k][i] = M.interior[k][i];
-  }
-  for (int i = t; i < np; i += 64)
-    F.pair[i] = M.pa[i] | M.pb[i] << 8;
-  for (int i = t; i < kCachedPoints * 3 * ns; i += 64) {
-    const int si = i % ns, c = (i / ns) % 3, k = i / (3 * ns);
-    const int type = M.stype[si];
-    R v = M.spts[k][c][si];
-    if (type == 0 || type == 2) {
-      // the shape formula's data, in the operations the narrow phase used
-      // to evaluate on each support query
-      const Q4<R> sq{M.sq[0][si], M.sq[1][si], M.sq[2][si], M.sq[3][si]};
-      v = k == 0   ? M.center[c][si]
-          : k == 1 ? (c < 2 ? M.size[c][si] : R(0))
-          : k == 2 ? comp(rotate(sq, V3<R>{0, 0, 1}), c)
-                   : R(0);
-    }
-    F.spt[k][c][si] = v;
-  }
-  if (t < 3)
-    F.colorStart[t] = M.colorStart[t];
 
   State *gs = valid ? &blobAt<State>(args.states, args.blobBytes, e) : nullptr;
   static_assert(L >= 4, "blob copies give each of the first three lanes an end word");
@@ -723,6 +749,8 @@ __device__ __forceinline__ void stepBody(const StepArgs &args, const ServoArgs<R
         E.s.friction = R(-1);
     }
   }
+  // every load of this wave, the Frames image's included, has landed
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   // The staged default schedule applies to this env while no body-body
   // contact recolours it and its dynamic bodies are the model's.

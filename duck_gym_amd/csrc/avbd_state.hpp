@@ -63,7 +63,7 @@ template <class R> struct DeviceModel {
 };
 
 // Joint model used inside the solve, staged in LDS once per workgroup.
-template <class R, int B, int J> struct Frames {
+template <class R, int B, int J> struct alignas(16) Frames {
   int a[J], b[J], limited[J];
   R ra[3][J], rb[3][J], axisA[3][J], axisB[3][J], tangentA[3][J], tangentB[3][J];
   R lo[J], hi[J], armature[J];

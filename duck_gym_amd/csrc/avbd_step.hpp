@@ -25,6 +25,7 @@ enum { kTargetControls = 0, kMotorControls = 1, kHeldControls = 2 };
 
 struct StepArgs {
   const void *model;   // DeviceModel<R>
+  const void *frames;  // Frames<R, B, J> built from the model (framesKernel)
   const void *points;  // shape points, R[3] each
   unsigned char *states; // EnvState blobs
   long long blobBytes;

@@ -224,6 +224,7 @@ class Batch final : public BatchBase {
   using State = EnvState<R, B, J, CG, CS>;
   static constexpr int G = 64 / L;
   DeviceModel<R> *dModel = nullptr;
+  Frames<R, B, J> *dFrames = nullptr; // the model's solve-time view (framesKernel)
   V3<R> *dPoints = nullptr;
   unsigned char *dStates = nullptr;
   hipEvent_t ready = nullptr;
@@ -243,7 +244,7 @@ class Batch final : public BatchBase {
                int mode = -1) {
     if (mode < 0)
       mode = motor != nullptr ? kMotorControls : kTargetControls;
-    StepArgs args{dModel, dPoints, states, blobBytes, n, targets, forces, motor,
+    StepArgs args{dModel, dFrames, dPoints, states, blobBytes, n, targets, forces, motor,
                   substeps, mode, kp, limit,
                   int(host.bodies.size()), int(host.joints.size()), int(host.shapes.size()),
                   int(host.pairs.size()), states == dStates && customBodies ? 1 : 0};
@@ -271,6 +272,10 @@ public:
       hipCheck(hipMalloc(&dPoints, pts.size() * sizeof(V3<R>)), "hipMalloc(points)");
       hipCheck(hipMalloc(&dStates, size_t(blobBytes) * count), "hipMalloc(state)");
       hipCheck(hipMemcpy(dModel, &packed, sizeof(packed), hipMemcpyHostToDevice), "upload model");
+      hipCheck(hipMalloc(&dFrames, sizeof(Frames<R, B, J>)), "hipMalloc(frames)");
+      hipCheck(hipMemset(dFrames, 0, sizeof(Frames<R, B, J>)), "hipMemset(frames)");
+      framesKernel<R, B, J><<<1, 64, 0, 0>>>(dModel, dFrames);
+      launched("framesKernel");
       hipCheck(hipMemcpy(dPoints, pts.data(), pts.size() * sizeof(V3<R>), hipMemcpyHostToDevice),
                "upload points");
       hipCheck(hipMemset(dStates, 0, size_t(blobBytes) * count), "hipMemset(state)");
@@ -298,9 +303,12 @@ public:
       (void)hipFree(dPoints);
     if (dModel)
       (void)hipFree(dModel);
+    if (dFrames)
+      (void)hipFree(dFrames);
     dStates = nullptr;
     dPoints = nullptr;
     dModel = nullptr;
+    dFrames = nullptr;
   }
   ~Batch() override {
     try {
@@ -519,7 +527,7 @@ public:
     sv.siteVelocities = static_cast<R *>(io.site_velocities);
     sv.airTime = static_cast<R *>(io.air_time);
     sv.contactTime = static_cast<R *>(io.contact_time);
-    StepArgs args{dModel, dPoints, dStates, blobBytes, count, nullptr, nullptr, nullptr,
+    StepArgs args{dModel, dFrames, dPoints, dStates, blobBytes, count, nullptr, nullptr, nullptr,
                   1, kMotorControls, 0, 0,
                   nb, int(host.joints.size()), int(host.shapes.size()), int(host.pairs.size()),
                   customBodies ? 1 : 0};
