@@ -168,50 +168,61 @@ __device__ __forceinline__ void copyWords(unsigned *dst, const unsigned *src, in
   }
 }
 
-// Two 16-byte-aligned word ranges [a0, b0) and [a1, b1) as one sequence of
-// dwordx4 chunks: every lane's loads are issued before its first store.
-template <int Chunks>
-__device__ __forceinline__ void copyRanges(unsigned *dst, const unsigned *src, int a0, int b0, int a1,
-                                           int b1, int lane, int L) {
-  const int n0 = (b0 - a0) / 4, n = n0 + (b1 - a1) / 4;
-  for (int c = lane; c < n; c += Chunks * L) {
-    uint4 v[Chunks];
-    int w[Chunks];
+// `n` 16-byte chunks from global memory straight into LDS with the 64 lanes
+// of a wave (global_load_lds_dwordx4: the chunk of lane t of instruction k
+// lands at chunk 64 k + t of the destination; no registers hold the data).
+// Complete once the wave's vector memory count drains.
+template <int N>
+__device__ __forceinline__ void dmaChunks(const unsigned char *src, __attribute__((address_space(3))) unsigned char *dst,
+                                          int t) {
 #pragma unroll
-    for (int k = 0; k < Chunks; ++k) {
-      const int i = c + k * L < n ? c + k * L : n - 1;
-      w[k] = i < n0 ? a0 + 4 * i : a1 + 4 * (i - n0);
-      v[k] = *reinterpret_cast<const uint4 *>(src + w[k]);
-    }
+  for (int k = 0; k < (N + 63) / 64; ++k)
+    if (t + 64 * k < N)
+      __builtin_amdgcn_global_load_lds(src + 16 * (t + 64 * k), dst + 1024 * k, 16, 0, 0);
+}
+
+// The blobs of a wave's environments into LDS, first round, as LDS DMA: the
+// group every step reads and writes (poses through the counts) with the first
+// kWarmContacts ground contacts as one range and, with `bodies`, the
+// reset-only group.  Environment g of the wave is e0 + g.
+constexpr int kWarmContacts = 8;
+template <class S, int G, class Env>
+__device__ void loadHot(Env *envs, unsigned char *states, long long blobBytes, int e0, int count, int t,
+                        bool bodies) {
+  constexpr int CGcap = int(sizeof(S::gc) / sizeof(S::gc[0]));
+  constexpr int gcBytes = int(sizeof(decltype(S::gc[0])));
+  constexpr int hot = int(hotBegin<S>()), header = int(headerBytes<S>());
+  constexpr int warm = header + (kWarmContacts < CGcap ? kWarmContacts : CGcap) * gcBytes;
+  constexpr int reset = int(resetBegin<S>()), end = int(sizeof(S));
+  static_assert(hot % 128 == 0 && warm % 16 == 0 && reset % 16 == 0 && end % 16 == 0,
+                "copied groups are whole 16-byte chunks, group 1 starts on 128 bytes");
 #pragma unroll
-    for (int k = 0; k < Chunks; ++k)
-      if (c + k * L < n)
-        *reinterpret_cast<uint4 *>(dst + w[k]) = v[k];
+  for (int g = 0; g < G; ++g) {
+    if (e0 + g >= count)
+      break;
+    const unsigned char *blob = states + blobBytes * (e0 + g);
+    auto *lds = (__attribute__((address_space(3))) unsigned char *)(&envs[g].s);
+    dmaChunks<(warm - hot) / 16>(blob + hot, lds + hot, t);
+    if (bodies)
+      dmaChunks<(end - reset) / 16>(blob + reset, lds + reset, t);
   }
 }
 
-// One environment's blob into LDS.  First round: the group every step reads
-// and writes (poses through the counts) with the first kWarmContacts ground
-// contacts as one range and, with `bodies`, the reset-only group; second
-// round, once the counts are known: the further live contacts, for a launch
-// that holds its controls (`held`) or sets motor channels (`motor`) the
-// targets and force, and for a held launch the drive parameters.
-constexpr int kWarmContacts = 8;
+// The rest of one environment's blob, once its counts are known: the
+// further live contacts, for a launch that holds its controls (`held`) or
+// sets motor channels (`motor`) the targets and force, and for a held launch
+// the drive parameters.
 template <class S>
-__device__ void loadEnv(S &dst, const S *src, int lane, int L, bool bodies, bool held, bool motor) {
+__device__ void loadEnv(S &dst, const S *src, int lane, int L, bool held, bool motor) {
   constexpr int header = int(headerBytes<S>() / 4), hot = int(hotBegin<S>() / 4);
   constexpr int CGcap = int(sizeof(S::gc) / sizeof(S::gc[0]));
   constexpr int CScap = int(sizeof(S::sc) / sizeof(S::sc[0]));
   constexpr int gcWords = int(sizeof(decltype(S::gc[0])) / 4);
   constexpr int scStart = int(offsetof(S, sc) / 4), scWords = int(sizeof(decltype(S::sc[0])) / 4);
   constexpr int warm = header + (kWarmContacts < CGcap ? kWarmContacts : CGcap) * gcWords;
-  constexpr int reset = int(resetBegin<S>() / 4), end = int(sizeof(S) / 4);
-  static_assert(hot % 32 == 0 && header % 4 == 0 && warm % 4 == 0 && reset % 4 == 0 && end % 4 == 0,
-                "copied groups start on 16-byte boundaries, group 1 on a 128-byte one");
   int ngc = src->ngc, nsc = src->nsc;
   unsigned *d = reinterpret_cast<unsigned *>(&dst);
   const unsigned *s = reinterpret_cast<const unsigned *>(src);
-  copyRanges<16>(d, s, hot, warm, reset, bodies ? end : reset, lane, L);
   ngc = ngc < 0 ? 0 : (ngc > CGcap ? CGcap : ngc);
   nsc = nsc < 0 ? 0 : (nsc > CScap ? CScap : nsc);
   copyWords<4>(d, s, warm, header + ngc * gcWords, lane, L);
@@ -734,9 +745,9 @@ __device__ __forceinline__ void stepBody(const StepArgs &args, const ServoArgs<R
   State *gs = valid ? &blobAt<State>(args.states, args.blobBytes, e) : nullptr;
   static_assert(L >= 4, "blob copies give each of the first three lanes an end word");
   static_assert(CS <= B, "the staged pair table holds B pairs");
+  loadHot<State, G>(envs, args.states, args.blobBytes, e - g, args.count, t, args.bodies != 0);
   if (valid) {
-    loadEnv<State>(E.s, gs, lane, L, args.bodies != 0, args.motorMode == kHeldControls,
-                   args.motorMode == kMotorControls);
+    loadEnv<State>(E.s, gs, lane, L, args.motorMode == kHeldControls, args.motorMode == kMotorControls);
     if (!args.bodies) {
       // the model's masses, inertia and shape friction, as reset writes them
       for (int b = lane; b < B; b += L) {
