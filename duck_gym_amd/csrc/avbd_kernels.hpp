@@ -229,10 +229,10 @@ __device__ void loadEnv(S &dst, const S *src, int lane, int L, bool held, bool m
   copyWords<4>(d, s, scStart, scStart + nsc * scWords, lane, L);
   if (held || motor)
     copyWords<4>(d, s, int(targetBegin<S>() / 4), hot, lane, L);
-  // the lead words in the targets' first 32-byte sector: a launch that sets
-  // the targets writes whole sectors (a partial one would make the L2 read
-  // it first), and these words hold zeros, as the state was created
-  for (int i = int(targetBegin<S>() / 32 * 8) + lane; i < int(targetBegin<S>() / 4); i += L)
+  // the lead words in the diagnostics' first 32-byte sector: a launch that
+  // steps the environment writes whole sectors (a partial one would make the
+  // L2 read it first), and these words hold zeros, as the state was created
+  for (int i = int(diagBegin<S>() / 32 * 8) + lane; i < int(diagBegin<S>() / 4); i += L)
     d[i] = 0;
   if (held)
     copyWords<4>(d, s, int(driveBegin<S>() / 4), int(driveEnd<S>() / 4), lane, L);
@@ -241,8 +241,8 @@ __device__ void loadEnv(S &dst, const S *src, int lane, int L, bool held, bool m
 // What a step writes of the drive parameters and of the colouring.
 enum DriveWrite { kWriteNoDrive = 0, kWriteDrive = 1, kWriteMotorDrive = 2 };
 
-// LDS -> HBM after a step: from word `from` (the targets, the force or group
-// 1, by what the launch set) through the live ground contacts as one range,
+// LDS -> HBM after a step: from word `from` (the diagnostics, the force or
+// group 1, by what the launch set) through the live ground contacts as one range,
 // the live body contacts, and the drive parameters (all, the motor-written
 // three, or none) and the colouring where they changed.  Mass, inertia and
 // friction only change on reset.
@@ -855,7 +855,6 @@ __device__ __forceinline__ void stepBody(const StepArgs &args, const ServoArgs<R
         E.s.driveLimit = limit;
       }
       driveWrite = same ? kWriteNoDrive : kWriteDrive;
-      writeFrom = int(targetBegin<State>() / 32 * 8);
       active = true;
     } else if (lane == 0) {
       // invalid controls: the environment keeps its last controls and
@@ -864,18 +863,19 @@ __device__ __forceinline__ void stepBody(const StepArgs &args, const ServoArgs<R
     }
   }
   const bool ran = active;
+  // an environment that steps rewrites its diagnostics (and its targets and
+  // force, set or read above)
+  if (ran)
+    writeFrom = int(diagBegin<State>() / 32 * 8);
   // the write-back's plan waits in LDS, not in registers across the solve
   if (valid && lane == 0)
     E.writeback = (modelColoursIn ? 1 : 0) | driveWrite << 1 | writeFrom << 8;
   if (ran && lane == 0) {
-    for (int k = 0; k < 8; ++k)
+    // the step's diagnostics start afresh (slots 6 and 7 unused, zero)
+    for (int k = 0; k < 8; ++k) {
       E.stepDiag[k] = 0;
-    E.s.diag[kJointError] = 0;
-    E.s.diag[kAxisError] = 0;
-    E.s.diag[kPenetration] = 0;
-    E.s.diag[kContacts] = 0;
-    E.s.diag[kConverged] = 1;
-    E.s.diag[kIterations] = 0;
+      E.s.diag[k] = k == kConverged ? R(1) : R(0);
+    }
   }
   __syncthreads();
 

@@ -129,10 +129,11 @@ enum DiagSlot { kJointError, kPenetration, kContacts, kConverged, kAxisError, kI
 
 // Persistent per-env state; the HBM blob is exactly this struct.  Its fields
 // are grouped by what a step does with them:
-//  0. the last controls' targets and external force: written by every launch
-//     that sets them, read only by one that holds them or sets motor
-//     channels (which keep the targets); they end where group 1 starts, so a
-//     launch writes them and group 1 as one range;
+//  0. the step diagnostics, and the last controls' targets and external
+//     force: written by every launch that steps the environment or sets them,
+//     read only by one that holds its controls or sets motor channels (which
+//     keep the targets; a step starts the diagnostics afresh); they end where
+//     group 1 starts, so a launch writes them and group 1 as one range;
 //  1. read and written by every step, from a 128-byte boundary of the blob
 //     through the live entries of the ground-contact list (one contiguous
 //     range), then the live body contacts;
@@ -156,18 +157,18 @@ enum DiagSlot { kJointError, kPenetration, kContacts, kConverged, kAxisError, kI
 // 128-byte boundary.
 enum DriveKind { kDriveOther = 0, kDriveTarget = 1, kDriveMotor = 2 };
 template <class R, int J> constexpr int leadBytes() {
-  constexpr int controls = int(sizeof(R)) * (J + 3);
+  constexpr int controls = int(sizeof(R)) * (8 + J + 3);
   return (controls + 4 + 127) / 128 * 128 - controls;
 }
 template <class R, int B, int J, int CG, int CS> struct EnvState {
   unsigned char lead[leadBytes<R, J>()];
+  R diag[8];
   R target[J];
   R force[3];
   R x[3][B];
   R q[4][B], v[3][B], w[3][B];
   R lambda[7][J], penalty[7][J];
   R lambdaF[J], penaltyF[J];
-  R diag[8];
   int failed, ngc, nsc, colorCount;
   int drive, modelColours;
   R driveKp, driveLimit;
@@ -214,11 +215,13 @@ template <class R, int B, int J, int CG, int CS, int L>
 struct EnvLds<R, B, J, CG, CS, L, 0> : EnvLdsCore<R, B, J, CG, CS> {};
 
 // Byte offsets of the ground-contact list inside the blob (only its live
-// entries are copied), of the targets, the force and group 1, and the byte
+// entries are copied), of the diagnostics, the targets, the force and group 1,
+// and the byte
 // ranges of the drive parameters, of the
 // three motor-written ones (torque through damping), of the colouring and of
 // the reset-only group.
 template <class S> constexpr size_t headerBytes() { return offsetof(S, gc); }
+template <class S> constexpr size_t diagBegin() { return offsetof(S, diag); }
 template <class S> constexpr size_t targetBegin() { return offsetof(S, target); }
 template <class S> constexpr size_t forceBegin() { return offsetof(S, force); }
 template <class S> constexpr size_t hotBegin() { return offsetof(S, x); }
