@@ -44,8 +44,10 @@ ENVS, DT, ITERATIONS, KP = 4096, 0.005, 10, 8.0
 def state_bytes_per_env(contacts, bodies=15, joints=14):
     """Minimal persistent state of one env (float32): bodies (x, q, v, w),
     joint multipliers/penalties (lambda 7, penalty 7, lambdaF, penaltyF),
-    the contact warm-start cache (56 B per live contact) and count/flag."""
-    return bodies * 13 * 4 + joints * 16 * 4 + 56 * contacts + 8
+    the contact warm-start cache (13 words per live contact: shape and
+    feature id, local point, ground anchor, c0, lambda 3, penalty 3) and
+    count/flag."""
+    return bodies * 13 * 4 + joints * 16 * 4 + 52 * contacts + 8
 
 
 def algorithmic_bytes_per_launch(envs, contacts, model_bytes):
