@@ -310,16 +310,24 @@ template <class R, int B, int J, int MQ> struct MprQuery {
         local = local + axis * (dot(axis, ld) >= 0 ? ownPts[1].y : -ownPts[1].y);
       }
     } else if (ownFlags & 2) {
-      R value = R(-INFINITY);
-      local = ownPts[0];
+      // the first maximum in index order, as a pairwise tree (a later point
+      // wins only when strictly greater; slots past the count never do)
+      R val[kCachedPoints];
+      V3<R> pt[kCachedPoints];
 #pragma unroll
       for (int i = 0; i < kCachedPoints; ++i) {
-        const R cand = dot(ownPts[i], ld);
-        if (i < ownCount && cand > value) {
-          value = cand;
-          local = ownPts[i];
-        }
+        val[i] = i < ownCount ? dot(ownPts[i], ld) : R(-INFINITY);
+        pt[i] = ownPts[i];
       }
+#pragma unroll
+      for (int w = 1; w < kCachedPoints; w *= 2)
+#pragma unroll
+        for (int i = 0; i + w < kCachedPoints; i += 2 * w) {
+          const bool later = val[i + w] > val[i];
+          val[i] = later ? val[i + w] : val[i];
+          pt[i] = pickValue(later, pt[i + w], pt[i]);
+        }
+      local = pt[0];
     } else {
       int best = -1;
       const int off = M.soffset[ownS];
@@ -349,19 +357,21 @@ template <class R, int B, int J, int MQ> struct MprQuery {
       // and are never chosen), then the first maximum in index order
       const int n = F.scount[s];
       R cand[kCachedPoints];
-#pragma unroll
-      for (int i = 0; i < kCachedPoints; ++i)
-        cand[i] = dot(staged(i, s), ld);
-      R value = R(-INFINITY);
-      int best = 0;
+      int best[kCachedPoints];
 #pragma unroll
       for (int i = 0; i < kCachedPoints; ++i) {
-        if (i < n && cand[i] > value) {
-          value = cand[i];
-          best = i;
-        }
+        cand[i] = i < n ? dot(staged(i, s), ld) : R(-INFINITY);
+        best[i] = i;
       }
-      local = staged(best, s);
+#pragma unroll
+      for (int w = 1; w < kCachedPoints; w *= 2)
+#pragma unroll
+        for (int i = 0; i + w < kCachedPoints; i += 2 * w) {
+          const bool later = cand[i + w] > cand[i];
+          cand[i] = later ? cand[i + w] : cand[i];
+          best[i] = later ? best[i + w] : best[i];
+        }
+      local = staged(best[0], s);
     } else {
       int best = -1, off = M.soffset[s], n = F.scount[s];
       R value = R(-INFINITY);

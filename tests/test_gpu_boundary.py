@@ -140,22 +140,27 @@ def test_cross_stream_step_is_ordered(models, home):
 
 @pytest.mark.parametrize("fp64", [False, True])
 def test_batch_size_invariance_bit_exact(models, home, fp64):
+    """An environment steps the same alone and in a batch of 37 (10 float
+    workgroups, an uneven split over the 8 XCD blocks; 5 in double): envs
+    from the first, middle and last workgroups, each against its own
+    one-env batch."""
     dtype = torch.float64 if fp64 else torch.float32
     rng = np.random.default_rng(2)
     targets = home + rng.uniform(-0.2, 0.2, (37, 14))
-    single = _batch(models["selfc"], 1, fp64)
+    picks = (0, 5, 21, 33, 36)
+    singles = [_batch(models["selfc"], 1, fp64) for _ in picks]
     many = _batch(models["selfc"], 37, fp64)
-    _reset_home(single, home, dtype)
-    _reset_home(many, home, dtype)
+    for b in singles + [many]:
+        _reset_home(b, home, dtype)
     t_many = torch.tensor(targets, dtype=dtype, device=DEV)
     f_many = torch.zeros(37, 3, dtype=dtype, device=DEV)
-    t_one = t_many[21:22].contiguous()
-    f_one = f_many[21:22].contiguous()
     for _ in range(20):
         many.step(t_many, f_many, 1, KP, 0.0)
-        single.step(t_one, f_one, 1, KP, 0.0)
-    for one, batch in zip(single.state(), many.state()):
-        torch.testing.assert_close(one[0], batch[21], rtol=0, atol=0)
+        for e, single in zip(picks, singles):
+            single.step(t_many[e:e + 1].contiguous(), f_many[e:e + 1].contiguous(), 1, KP, 0.0)
+    for e, single in zip(picks, singles):
+        for one, batch in zip(single.state(), many.state()):
+            torch.testing.assert_close(one[0], batch[e], rtol=0, atol=0)
 
 
 def test_substep_chunking_bit_exact(models, home):
