@@ -95,7 +95,10 @@ def cpu_baseline(model, home, seconds_budget=12.0):
             timed around step() only, as src/main.cpp:63-68 times its solver;
     solver  src/solver.cpp's own CLI (duck_sim) on the same env: its steps/s
             and where the root ends -- its explicit PD drive diverges at
-            kp = 8, dt = 5 ms.
+            kp = 8, dt = 5 ms;
+    port    the oracle's own threaded batch (oracle.OracleBatch, the same
+            CpuBatch semantics over this repository's restatement) on the
+            same workload and threads, for about a third of the budget.
     The reference build is required: without oracle/_ref this raises."""
     import json as _json
     import subprocess
@@ -135,6 +138,19 @@ def cpu_baseline(model, home, seconds_budget=12.0):
         single.step(q1, f1, 1, KP, 1e9)
         spent += time.perf_counter() - t0
 
+    from oracle.oracle import OracleBatch
+
+    port = OracleBatch(model, envs, DT, ITERATIONS, threads=threads)
+    port.reset(np.ones(envs, bool), np.tile(home, (envs, 1)), np.zeros((envs, 6)))
+    q64, f64 = np.tile(home, (envs, 1)), np.zeros((envs, 3))
+    port.step(q64, f64, 1, KP, 1e9)
+    port_steps, start = 0, time.perf_counter()
+    while time.perf_counter() - start < seconds_budget / 3:
+        port.step(q64, f64, 1, KP, 1e9)
+        port_steps += 1
+    port_elapsed = time.perf_counter() - start
+    del port
+
     run = subprocess.run([str(ROOT / "oracle" / "_ref" / "duck_sim"), str(model), "--steps", "200",
                           "--dt", str(DT), "--iterations", str(ITERATIONS), "--output",
                           "/dev/stdout"], capture_output=True, text=True, check=True).stdout
@@ -155,6 +171,10 @@ def cpu_baseline(model, home, seconds_budget=12.0):
             "root_displacement_m": float(np.linalg.norm(roots[200] - roots[0])),
             "unconverged_steps": summary["unconverged_steps"],
             "note": "src/solver.cpp (duck_sim): its explicit PD drive diverges at kp 8, dt 5 ms"},
+        "port": {
+            "value": envs * port_steps / port_elapsed, "unit": "env-steps/s", "threads": threads,
+            "sample": (f"{envs} envs x {port_steps} steps of oracle.OracleBatch (this repository's "
+                       "restatement, CpuBatch semantics, float32)")},
     }
 
 

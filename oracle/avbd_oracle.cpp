@@ -16,6 +16,7 @@
 #include <memory>
 #include <stdexcept>
 #include <string>
+#include <thread>
 #include <type_traits>
 #include <vector>
 
@@ -1716,4 +1717,196 @@ int oracle_convex_query(const double *va, int na, const double *vb, int nb,
 }
 
 long long oracle_flops(void) { return g_flops; }
+}
+
+// ------------------------------------------------------------ batch driver --
+// The reference's CPU batch (src/cuda/cpu_bindings.cpp:20-168, CpuBatch32 and
+// CpuBatch64): one model shared by `n` environments, which `workers` threads
+// step with environment e on worker e mod workers; the same parameter checks
+// and failure rules.  Test infrastructure and a CPU baseline, like the rest of
+// this file.
+namespace {
+struct BatchHandle {
+  virtual ~BatchHandle() = default;
+  bool fp64 = false;
+  int n = 0, nb = 0, nj = 0, workers = 1;
+};
+template <class R> struct BatchT final : BatchHandle {
+  Model<R> model;
+  std::vector<Env<R>> envs;
+};
+// cpu_bindings.cpp:76-111: worker w runs environments w, w + workers, ...
+template <class F> void striped(int n, int workers, F &&work) {
+  auto run = [&](int w) {
+    for (int e = w; e < n; e += workers)
+      work(e);
+  };
+  std::vector<std::thread> threads;
+  for (int w = 1; w < workers; ++w)
+    threads.emplace_back(run, w);
+  run(0);
+  for (auto &t : threads)
+    t.join();
+}
+template <class F> int visitBatch(void *h, F &&f) {
+  auto *base = static_cast<BatchHandle *>(h);
+  return guarded([&] {
+    if (base->fp64)
+      f(*static_cast<BatchT<double> *>(base));
+    else
+      f(*static_cast<BatchT<float> *>(base));
+  });
+}
+} // namespace
+
+extern "C" {
+// cpu_bindings.cpp:35-46
+void *oracle_batch_create(const char *path, int n, double dt, int iterations, int fp64, int threads) {
+  BatchHandle *out = nullptr;
+  guarded([&] {
+    fail(!(n > 0 && n <= 4096 && dt > 0 && std::isfinite(dt) && iterations > 0 && threads > 0 &&
+           threads <= 64),
+         "Invalid batch parameters");
+    ModelFile file = parse(path);
+    auto fill = [&](auto &b) {
+      b.model = flatten<RealOf<std::decay_t<decltype(b)>>>(file, dt, iterations, 0);
+      b.envs.resize(n);
+      for (auto &env : b.envs)
+        env.initialize(b.model);
+    };
+    std::unique_ptr<BatchHandle> made;
+    if (fp64) {
+      auto b = std::make_unique<BatchT<double>>();
+      fill(*b);
+      made = std::move(b);
+    } else {
+      auto b = std::make_unique<BatchT<float>>();
+      fill(*b);
+      made = std::move(b);
+    }
+    made->fp64 = fp64;
+    made->n = n;
+    made->nb = file.bodies.size();
+    made->nj = file.joints.size();
+    made->workers = std::min(n, threads);
+    out = made.release();
+  });
+  return out;
+}
+
+void oracle_batch_destroy(void *h) { delete static_cast<BatchHandle *>(h); }
+
+int oracle_batch_dims(void *h, int *n, int *bodies, int *joints) {
+  auto *b = static_cast<BatchHandle *>(h);
+  *n = b->n;
+  *bodies = b->nb;
+  *joints = b->nj;
+  return 0;
+}
+
+// cpu_bindings.cpp:47-64: masked environments from the model state and the
+// given pose; non-finite inputs mark an environment failed instead.
+int oracle_batch_reset(void *h, const unsigned char *mask, const double *q, const double *root) {
+  return visitBatch(h, [&](auto &b) {
+    using R = RealOf<std::decay_t<decltype(b)>>;
+    for (int e = 0; e < b.n; ++e) {
+      if (!mask[e])
+        continue;
+      std::vector<R> qs(b.nj), rs(6);
+      bool finite = true;
+      for (int j = 0; j < b.nj; ++j) {
+        qs[j] = R(q[size_t(e) * b.nj + j]);
+        finite = finite && std::isfinite(q[size_t(e) * b.nj + j]);
+      }
+      for (int k = 0; k < 6; ++k) {
+        rs[k] = R(root[size_t(e) * 6 + k]);
+        finite = finite && std::isfinite(root[size_t(e) * 6 + k]);
+      }
+      if (!finite) {
+        b.envs[e].failed = 1;
+        continue;
+      }
+      b.envs[e].initialize(b.model);
+      b.envs[e].resetPose(qs.data(), rs.data());
+    }
+  });
+}
+
+// cpu_bindings.cpp:65-111: targets, kp, limit and the model's torque,
+// friction loss and damping on every hinge; a non-finite target or force
+// fails the environment, which then does not step.
+int oracle_batch_step(void *h, const double *target, const double *forces, int substeps, double kp,
+                      double limit) {
+  return visitBatch(h, [&](auto &b) {
+    using R = RealOf<std::decay_t<decltype(b)>>;
+    fail(!(substeps > 0 && kp >= 0 && std::isfinite(kp) && limit > 0 && std::isfinite(limit)),
+         "Invalid controls");
+    striped(b.n, b.workers, [&](int e) {
+      Env<R> &s = b.envs[e];
+      for (int j = 0; j < b.nj; ++j) {
+        const R t = R(target[size_t(e) * b.nj + j]);
+        if (!std::isfinite(t))
+          s.failed = 1;
+        auto &jt = s.joints[j];
+        jt.target = t;
+        jt.kp = R(kp);
+        jt.maxTorque = R(limit);
+        jt.torque = b.model.joints[j].torque;
+        jt.frictionloss = b.model.joints[j].frictionloss;
+        jt.damping = b.model.joints[j].damping;
+      }
+      const double *f = forces + size_t(e) * 3;
+      for (int k = 0; k < 3; ++k)
+        if (!std::isfinite(R(f[k])))
+          s.failed = 1;
+      if (s.failed)
+        return;
+      s.bodies[1].force = {R(f[0]), R(f[1]), R(f[2])};
+      s.advance(substeps);
+    });
+  });
+}
+
+// cpu_bindings.cpp:112-125: one motor step per environment, in index order.
+int oracle_batch_step_motor(void *h, const double *motor, const double *forces) {
+  return visitBatch(h, [&](auto &b) {
+    using R = RealOf<std::decay_t<decltype(b)>>;
+    for (int e = 0; e < b.n; ++e) {
+      Env<R> &s = b.envs[e];
+      std::vector<R> m(3 * b.nj);
+      for (int i = 0; i < 3 * b.nj; ++i)
+        m[i] = R(motor[size_t(e) * 3 * b.nj + i]);
+      R f[3] = {R(forces[size_t(e) * 3]), R(forces[size_t(e) * 3 + 1]), R(forces[size_t(e) * 3 + 2])};
+      s.setMotor(m.data(), f);
+      if (!s.failed)
+        s.advance(1);
+    }
+  });
+}
+
+// cpu_bindings.cpp:156-162: bodies [n, B, 13], joints [n, J, 2], diag [n, 6]
+int oracle_batch_state(void *h, double *bodies, double *joints, double *diag) {
+  return visitBatch(h, [&](auto &b) {
+    using R = RealOf<std::decay_t<decltype(b)>>;
+    std::vector<R> bo(13 * b.nb), jo(2 * b.nj), d(6);
+    for (int e = 0; e < b.n; ++e) {
+      b.envs[e].snapshot(bo.data(), jo.data(), d.data());
+      std::copy(bo.begin(), bo.end(), bodies + size_t(e) * 13 * b.nb);
+      std::copy(jo.begin(), jo.end(), joints + size_t(e) * 2 * b.nj);
+      std::copy(d.begin(), d.end(), diag + size_t(e) * 6);
+    }
+  });
+}
+
+int oracle_batch_contact_counts(void *h, double *out) {
+  return visitBatch(h, [&](auto &b) {
+    using R = RealOf<std::decay_t<decltype(b)>>;
+    for (int e = 0; e < b.n; ++e) {
+      R o[2];
+      b.envs[e].contactCounts(o);
+      out[2 * e] = o[0];
+      out[2 * e + 1] = o[1];
+    }
+  });
+}
 }

@@ -1,7 +1,8 @@
 """ctypes access to the CPU oracle (test infrastructure only).
 
 `Oracle` wraps liboracle.so, this repository's restatement of the reference
-AVBD step.  `ReferenceProbe` wraps oracle/_ref/ref_probe.so, the reference's
+AVBD step, and `OracleBatch` its threaded batch driver (the reference's
+CpuBatch32/64).  `ReferenceProbe` wraps oracle/_ref/ref_probe.so, the reference's
 own src/cuda/kernel.cuh compiled in place by oracle/Makefile (present only
 where the reference tree was available at build time).  Both expose the same
 single-environment API so the tests can check one against the other.
@@ -229,6 +230,87 @@ class Oracle(_Single):
     def set_root_velocity(self, v, w=(0, 0, 0)):
         (_, vp), (_, wp) = _d(v), _d(w)
         self._call("set_root_velocity", vp, wp)
+
+
+class OracleBatch:
+    """The reference's CPU batch (src/cuda/cpu_bindings.cpp:20-168, CpuBatch32
+    and CpuBatch64) over this restatement: `n` environments sharing one model,
+    stepped by `threads` std::thread workers (environment e on worker
+    e mod workers), with the same parameter checks (ValueError) and failure
+    rules.  Arrays are float64 in and out."""
+
+    _sig = {
+        "create": (ctypes.c_void_p, [ctypes.c_char_p, ctypes.c_int, ctypes.c_double, ctypes.c_int,
+                                     ctypes.c_int, ctypes.c_int]),
+        "destroy": (None, [ctypes.c_void_p]),
+        "dims": (ctypes.c_int, [ctypes.c_void_p, _ip, _ip, _ip]),
+        "reset": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(ctypes.c_ubyte), _dp, _dp]),
+        "step": (ctypes.c_int, [ctypes.c_void_p, _dp, _dp, ctypes.c_int, ctypes.c_double,
+                                ctypes.c_double]),
+        "step_motor": (ctypes.c_int, [ctypes.c_void_p, _dp, _dp]),
+        "state": (ctypes.c_int, [ctypes.c_void_p, _dp, _dp, _dp]),
+        "contact_counts": (ctypes.c_int, [ctypes.c_void_p, _dp]),
+    }
+
+    def __init__(self, model, num_envs, dt=0.005, iterations=10, threads=1, fp64=False):
+        self._lib = _lib("oracle")
+        for name, (res, args) in self._sig.items():
+            fn = getattr(self._lib, f"oracle_batch_{name}")
+            fn.restype, fn.argtypes = res, args
+        self._h = self._lib.oracle_batch_create(str(model).encode(), int(num_envs), float(dt),
+                                                int(iterations), int(bool(fp64)), int(threads))
+        if not self._h:
+            raise ValueError(self._lib.oracle_last_error().decode())
+        n, b, j = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+        self._lib.oracle_batch_dims(self._h, ctypes.byref(n), ctypes.byref(b), ctypes.byref(j))
+        self.num_envs, self.bodies, self.joints = n.value, b.value, j.value
+        self.fp64 = bool(fp64)
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h:
+            self._lib.oracle_batch_destroy(h)
+            self._h = None
+
+    def _call(self, name, *args):
+        if getattr(self._lib, f"oracle_batch_{name}")(self._h, *args):
+            raise ValueError(self._lib.oracle_last_error().decode())
+
+    def _shaped(self, a, shape):
+        a = np.ascontiguousarray(a, dtype=np.float64)
+        if a.shape != tuple(shape):
+            raise ValueError("Invalid array shape")
+        return a, a.ctypes.data_as(_dp)
+
+    def reset(self, mask, q, root):
+        m = np.ascontiguousarray(mask, dtype=np.uint8)
+        if m.shape != (self.num_envs,):
+            raise ValueError("Invalid array shape")
+        q, qp = self._shaped(q, (self.num_envs, self.joints))
+        r, rp = self._shaped(root, (self.num_envs, 6))
+        self._call("reset", m.ctypes.data_as(ctypes.POINTER(ctypes.c_ubyte)), qp, rp)
+
+    def step(self, target, forces, substeps, kp, limit):
+        t, tp = self._shaped(target, (self.num_envs, self.joints))
+        f, fp = self._shaped(forces, (self.num_envs, 3))
+        self._call("step", tp, fp, int(substeps), float(kp), float(limit))
+
+    def step_motor(self, motor, forces):
+        m, mp = self._shaped(motor, (self.num_envs, self.joints, 3))
+        f, fp = self._shaped(forces, (self.num_envs, 3))
+        self._call("step_motor", mp, fp)
+
+    def state(self):
+        b = np.zeros((self.num_envs, self.bodies, 13))
+        j = np.zeros((self.num_envs, self.joints, 2))
+        d = np.zeros((self.num_envs, 6))
+        self._call("state", b.ctypes.data_as(_dp), j.ctypes.data_as(_dp), d.ctypes.data_as(_dp))
+        return b, j, d
+
+    def contact_counts(self):
+        out = np.zeros((self.num_envs, 2))
+        self._call("contact_counts", out.ctypes.data_as(_dp))
+        return out
 
 
 class ReferenceProbe(_Single):

@@ -28,7 +28,7 @@ def driver(tmp_path_factory):
            "-fsanitize=address,undefined", "-fno-sanitize-recover=all",
            str(ROOT / "tests" / "native" / "sanitize_driver.cpp"),
            str(ROOT / "duck_gym_amd" / "csrc" / "duck_model.cpp"),
-           str(ROOT / "oracle" / "avbd_oracle.cpp"), "-o", str(out)]
+           str(ROOT / "oracle" / "avbd_oracle.cpp"), "-o", str(out), "-pthread"]
     subprocess.run(cmd, check=True)
     return out
 
