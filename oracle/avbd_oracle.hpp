@@ -42,6 +42,17 @@ int oracle_convex_query(const double *va, int na, const double *vb, int nb,
                         const double *poses, double inflation, double tolerance, int fp64,
                         double *out);
 long long oracle_flops(void);
+// The reference's CPU batch (src/cuda/cpu_bindings.cpp:20-168) over mode 0:
+// n environments on `threads` env-striped std::thread workers.
+void *oracle_batch_create(const char *path, int n, double dt, int iterations, int fp64, int threads);
+void oracle_batch_destroy(void *h);
+int oracle_batch_dims(void *h, int *n, int *bodies, int *joints);
+int oracle_batch_reset(void *h, const unsigned char *mask, const double *q, const double *root);
+int oracle_batch_step(void *h, const double *target, const double *forces, int substeps, double kp,
+                      double limit);
+int oracle_batch_step_motor(void *h, const double *motor, const double *forces);
+int oracle_batch_state(void *h, double *bodies, double *joints, double *diag);
+int oracle_batch_contact_counts(void *h, double *out);
 #ifdef __cplusplus
 }
 #endif

@@ -87,6 +87,45 @@ static int step(int n, char **files) {
                     oracle_failed(h));
         oracle_destroy(h);
       }
+  // the threaded batch: 5 environments on 3 workers, one reset with a
+  // non-finite pose, target and motor steps, every query
+  for (int i = 0; i < n; ++i)
+    for (int fp64 = 0; fp64 < 2; ++fp64) {
+      void *b = oracle_batch_create(files[i], 5, 0.005, 10, fp64, 3);
+      if (!b) {
+        std::printf("batch rejected %s: %s\n", files[i], oracle_last_error());
+        return 1;
+      }
+      int ne = 0, nb = 0, nj = 0;
+      oracle_batch_dims(b, &ne, &nb, &nj);
+      std::vector<unsigned char> mask(ne, 1);
+      std::vector<double> q(ne * nj), root(ne * 6, 0), target(ne * nj), forces(ne * 3, 0),
+          motor(ne * nj * 3), bodies(ne * nb * 13), joints(ne * nj * 2), diag(ne * 6),
+          counts(ne * 2);
+      for (auto &v : q)
+        v = u(rng);
+      root[6 * 2] = NAN;
+      oracle_batch_reset(b, mask.data(), q.data(), root.data());
+      for (int s = 0; s < 6; ++s) {
+        for (auto &v : target)
+          v = u(rng);
+        if (s == 3) {
+          for (int k = 0; k < ne * nj; ++k) {
+            motor[3 * k] = u(rng);
+            motor[3 * k + 1] = std::abs(u(rng)) * 0.1;
+            motor[3 * k + 2] = std::abs(u(rng));
+          }
+          oracle_batch_step_motor(b, motor.data(), forces.data());
+        } else if (oracle_batch_step(b, target.data(), forces.data(), 1, 8.0, 1e9)) {
+          std::printf("batch step error %s: %s\n", files[i], oracle_last_error());
+          return 1;
+        }
+        oracle_batch_state(b, bodies.data(), joints.data(), diag.data());
+        oracle_batch_contact_counts(b, counts.data());
+      }
+      std::printf("batch stepped %s fp64 %d\n", files[i], fp64);
+      oracle_batch_destroy(b);
+    }
   // the stand-alone narrow phase: two boxes' corners, overlapping
   std::vector<double> box;
   for (int c = 0; c < 8; ++c)

@@ -77,8 +77,12 @@ def test_loader_under_sanitizers(driver, models, tmp_path):
 def test_oracle_under_sanitizers(driver, models, tmp_path):
     paths = _valid_models(models, tmp_path)
     out = _run(driver, "step", *paths)
-    rejected = out.count("rejected")
+    lines = out.splitlines()
+    rejected = sum(line.startswith("rejected") for line in lines)
+    stepped = sum(line.startswith("stepped") for line in lines)
     assert all("mode 1" in line and "Body contacts" in line
-               for line in out.splitlines() if line.startswith("rejected"))
-    assert out.count("stepped") + rejected == 4 * len(paths) and "convex query ok" in out
-    assert out.count("stepped") >= 2 * len(paths)
+               for line in lines if line.startswith("rejected"))
+    assert stepped + rejected == 4 * len(paths) and "convex query ok" in out
+    assert stepped >= 2 * len(paths)
+    # the threaded batch driver, both precisions of every model
+    assert sum(line.startswith("batch stepped") for line in lines) == 2 * len(paths)
