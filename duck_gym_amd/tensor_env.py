@@ -212,6 +212,24 @@ class TensorEnv:
                            2 * (q[:, 0] * q[:, 3] + q[:, 1] * q[:, 2])), dim=-1)
         return b, j, d, gravity, v, w, yaw
 
+    def observations(self, state):
+        """Observation rows from a `state()` tuple, assembled in torch
+        (tensor_env.py:238-258); get_observations() assembles the same rows
+        from the device state in one kernel."""
+        b, j, d, g, v, w, yaw = state
+        if self.task == "rollout":
+            pieces = [g, w, j[:, :, 0] - self.home, 0.1 * j[:, :, 1], self.actions]
+        else:
+            pieces = [g, v, w, b[:, 1, 2:3] - self.meta["root_height"], j[:, :, 0] - self.home,
+                      0.1 * j[:, :, 1], self.actions]
+        if self.task == "locomotion":
+            phase = (self.episode_length_buf.to(self.dtype) * self.control_dt
+                     * (2 * torch.pi / getattr(self, "gait_period", 0.8)))
+            pieces.extend([self.commands, yaw, torch.stack((phase.sin(), phase.cos()), dim=-1)])
+            if self.velocity_filter_seconds > 0:
+                pieces.append(self.filtered_velocity)
+        return torch.cat(pieces, dim=-1).float()
+
     def get_observations(self):
         obs = torch.empty(self.num_envs, self.obs_dim, device=self.device)
         self.native.task_observe(self.spec, None, self.actions, self._commands,

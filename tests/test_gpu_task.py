@@ -155,3 +155,19 @@ def test_task_argument_checks(model_dir):
         TensorEnv(model_dir, 8, ITER, DT, 1, backend="cpu")
     with pytest.raises(ValueError):
         TensorEnv(model_dir, 8, ITER, DT, 0)
+
+
+@pytest.mark.parametrize("task,kw", [("standing", {}), ("locomotion", {"velocity_filter_seconds": 0.2}),
+                                     ("rollout", {})])
+def test_observations_from_state_equal_the_kernel(model_dir, task, kw):
+    """`observations(state())` (torch, tensor_env.py:238-258) and
+    `get_observations()` (the task kernel) give the same rows."""
+    env = TensorEnv(model_dir, 16, iterations=ITER, dt=DT, substeps=4, seed=3, task=task,
+                    auto_reset=False, **kw)
+    rng = np.random.default_rng(6)
+    for _ in range(6):
+        env.step(torch.tensor(rng.uniform(-0.5, 0.5, (16, 14)), dtype=torch.float32, device=DEV))
+        torch_rows = env.observations(env.state())
+        kernel_rows, _ = env.get_observations()
+        assert torch_rows.shape == kernel_rows.shape
+        np.testing.assert_allclose(_np(torch_rows), _np(kernel_rows), rtol=1e-5, atol=2e-6)
