@@ -690,7 +690,7 @@ __global__ void framesKernel(const DeviceModel<R> *model, Frames<R, B, J> *out) 
   stageFrames<R, B, J>(*out, *model, threadIdx.x, blockDim.x);
 }
 
-template <class R, int B, int J, int CG, int CS, int L, int PL, bool Servo>
+template <class R, int B, int J, int CG, int CS, int L, int PL, bool Servo, bool Pairs>
 __device__ __forceinline__ void stepBody(const StepArgs &args, const ServoArgs<R> &sv) {
   constexpr int G = 64 / L;
   // Lanes per body-pair query, pairs per round and rounds (pairs <= CS).
@@ -709,7 +709,8 @@ __device__ __forceinline__ void stepBody(const StepArgs &args, const ServoArgs<R
   const int e = xcdBlock(blockIdx.x, gridDim.x) * G + g;
   const bool valid = e < args.count;
   Env &E = envs[g];
-  const int nb = args.nb, nj = args.nj, ns = args.ns, np = args.np;
+  // (a model without body pairs: none of their code is compiled)
+  const int nb = args.nb, nj = args.nj, ns = args.ns, np = Pairs ? args.np : 0;
 
   // Controls and the model's per-joint defaults, loaded first so that their
   // latency overlaps the model staging and the blob copy.
@@ -889,10 +890,10 @@ __device__ __forceinline__ void stepBody(const StepArgs &args, const ServoArgs<R
   }
   __syncthreads();
 
-  Stepper<R, B, J, CG, CS, L, PL> stp{M, points, F, E, lane};
+  Stepper<R, B, J, CG, CS, L, PL, Pairs> stp{M, points, F, E, lane};
   // Block-solve lanes: with P == 2, lanes l and l ^ 8 (same 16-lane DPP row)
   // share a body; `slot` numbers the bodies a colour pass runs at once.
-  constexpr int P = Stepper<R, B, J, CG, CS, L, PL>::P;
+  constexpr int P = Stepper<R, B, J, CG, CS, L, PL, Pairs>::P;
   static_assert(P == 1 || L % (8 * P) == 0, "split block solves need 8 P-lane groups");
   const int part = (lane >> 3) & (P - 1);
   const int slot = P == 1 ? lane : (lane & 7) + 8 * (lane / (8 * P));
@@ -1419,6 +1420,35 @@ __device__ __forceinline__ void stepBody(const StepArgs &args, const ServoArgs<R
       if (c1 + slot < c2)
         mine[1] = E.order[c1 + slot];
     }
+    // A third colour that holds one body (a body contact recoloured it) whose
+    // hinges all end at colour-0 or static bodies: none of its rows but the
+    // body contacts reads a pose that the colour-1 pass moves, so the free
+    // slot of colour 1 assembles them during that pass (bit 28 of its plan's
+    // first word), and the third pass adds the body-contact rows and solves.
+    // The sums and their order are those of one assembly in the third pass.
+    bool early = false, stageLane = false;
+    if constexpr (sizeof(R) == sizeof(float) && P == 2 && Pairs) {
+      if (active && twoColourSlots && E.s.colorCount == 3) {
+        const int c1 = E.colorStart[1], c2 = E.colorStart[2];
+        if (E.colorStart[3] - c2 == 1 && c2 - c1 < L / P) {
+          const int b3 = E.order[c2];
+          bool ok = true;
+          for (int a = F.adjStart[b3]; a < F.adjStart[b3 + 1]; ++a) {
+            const int packed = F.adj[a], ja = (packed >> 8) & 255, jb = (packed >> 16) & 255;
+            const int other = ja == b3 ? jb : ja;
+            ok = ok && (E.s.mass[other] <= 0 || E.s.colors[other] == 0);
+          }
+          early = ok;
+          stageLane = ok && slot == c2 - c1;
+          if (stageLane)
+            mine[1] = b3;
+          if (ok && lane == 0) {
+            E.earlyMask = E.smask[b3];
+            E.smask[b3] = 0;
+          }
+        }
+      }
+    }
     if constexpr (P == 2) {
       // A colour with a free slot lends it to its body with the most hinges
       // or ground contacts (three or more: two lanes would need two rounds);
@@ -1427,7 +1457,7 @@ __device__ __forceinline__ void stepBody(const StepArgs &args, const ServoArgs<R
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
           const int cs = E.colorStart[c], n = E.colorStart[c + 1] - cs;
-          if (n >= L / P)
+          if (n >= L / P || (c == 1 && early))
             continue;
           int best = -1, bestUnits = 2;
           for (int k = 0; k < n; ++k) {
@@ -1464,13 +1494,15 @@ __device__ __forceinline__ void stepBody(const StepArgs &args, const ServoArgs<R
       }
     }
     // The lane's assembly plans for its bodies of the first two colours.
-    typename Stepper<R, B, J, CG, CS, L, PL>::SlotPlan plans[2] = {{0, 0}, {0, 0}};
+    typename Stepper<R, B, J, CG, CS, L, PL, Pairs>::SlotPlan plans[2] = {{0, 0}, {0, 0}};
     if constexpr (sizeof(R) == sizeof(float)) {
 #pragma unroll
       for (int c = 0; c < 2; ++c)
         if (active && twoColourSlots && mine[c] >= 0)
           plans[c] = stp.plan(mine[c], partOf[c], partsOf[c]);
+      plans[1].w0 |= stageLane ? 1 << 28 : 0;
     }
+    E.early = early ? 1 : 0;
     // Which hinge's dual update a lane makes first.  A hinge's dual update
     // and the next iteration's first-colour block solve of its colour-0 body
     // evaluate it at the same poses (nothing moves in between), so when every
@@ -1488,7 +1520,7 @@ __device__ __forceinline__ void stepBody(const StepArgs &args, const ServoArgs<R
     // The ends of that hinge and the owner of the lane's first ground
     // contact (the list is fixed until the next detection).
     const int ends0 = dualJoint >= 0 ? F.a[dualJoint] | F.b[dualJoint] << 8 : F.a[0] | F.b[0] << 8;
-    typename Stepper<R, B, J, CG, CS, L, PL>::JointEval lastEval{};
+    typename Stepper<R, B, J, CG, CS, L, PL, Pairs>::JointEval lastEval{};
     int owner0 = 0;
     if (active && lane < E.s.ngc) {
       const int id = E.s.gc[lane].id;
@@ -1497,7 +1529,7 @@ __device__ __forceinline__ void stepBody(const StepArgs &args, const ServoArgs<R
     // Contact rounds of the dual update for the whole wave (scalars; the
     // lists are fixed until the next detection).
     const int groundRounds = __builtin_amdgcn_readfirstlane(waveMaxInt(active ? E.s.ngc : 0));
-    const int selfRounds = __builtin_amdgcn_readfirstlane(waveMaxInt(active ? E.s.nsc : 0));
+    const int selfRounds = Pairs ? __builtin_amdgcn_readfirstlane(waveMaxInt(active ? E.s.nsc : 0)) : 0;
     // ---------------- AVBD iterations (kernel.cuh:979-1063) ---------------
     bool dualRan = false;
     R dJoint = 0, dAxis = 0, dDepth = 0;
@@ -1528,9 +1560,11 @@ __device__ __forceinline__ void stepBody(const StepArgs &args, const ServoArgs<R
                                                        c0 ? partsOf[0] : partsOf[1], quadPass,
                                                        c0 ? plans[0] : plans[1]));
           } else {
+            // (an early-assembled third colour is its one body: slot 0)
             for (int k = E.colorStart[c] + slot; k < E.colorStart[c + 1]; k += L / P) {
               const int bi = E.order[k];
-              maxUpdate = mx(maxUpdate, stp.updateBody(bi, true, part, P, false, stp.plan(bi, part, P)));
+              maxUpdate = mx(maxUpdate, stp.updateBody(bi, true, part, P, false, stp.plan(bi, part, P),
+                                                       nullptr, c == 2 && E.early != 0));
             }
           }
         }
@@ -1548,7 +1582,7 @@ __device__ __forceinline__ void stepBody(const StepArgs &args, const ServoArgs<R
         R errC0 = 0;
         dualRan = true;
         dJoint = dAxis = dDepth = 0;
-        auto foldJoint = [&](const typename Stepper<R, B, J, CG, CS, L, PL>::JointDual &jd) {
+        auto foldJoint = [&](const typename Stepper<R, B, J, CG, CS, L, PL, Pairs>::JointDual &jd) {
 #pragma unroll
           for (int k = 0; k < 3; ++k)
             dJoint = mx(dJoint, mabs(jd.C[k]));
@@ -1710,16 +1744,17 @@ __device__ __forceinline__ void stepBody(const StepArgs &args, const ServoArgs<R
     storeEnv<State>(gs, E.s, lane, L, plan >> 8, (plan >> 1) & 3, writeColours);
 }
 
-template <class R, int B, int J, int CG, int CS, int L, int PL = defaultSolveLanes(L)>
+// Pairs false: for a model without body pairs.
+template <class R, int B, int J, int CG, int CS, int L, int PL = defaultSolveLanes(L), bool Pairs = true>
 __global__ __launch_bounds__(64) void advanceKernel(StepArgs args) {
   const ServoArgs<R> none{};
-  stepBody<R, B, J, CG, CS, L, PL, false>(args, none);
+  stepBody<R, B, J, CG, CS, L, PL, false, Pairs>(args, none);
 }
 
 // One servo substep per launch (bam_env.py:307-337 with refresh()).
-template <class R, int B, int J, int CG, int CS, int L, int PL = defaultSolveLanes(L)>
+template <class R, int B, int J, int CG, int CS, int L, int PL = defaultSolveLanes(L), bool Pairs = true>
 __global__ __launch_bounds__(64) void servoStepKernel(StepArgs args, ServoArgs<R> servo) {
-  stepBody<R, B, J, CG, CS, L, PL, true>(args, servo);
+  stepBody<R, B, J, CG, CS, L, PL, true, Pairs>(args, servo);
 }
 
 } // namespace duckhip

@@ -195,10 +195,17 @@ template <class R, int B, int J, int CG, int CS> struct EnvLdsCore {
   int order[B], colorStart[CS + 3];
   // what the write-back copies, decided with the controls: the first word
   // (bits 8-), the drive parameters (bits 1-2), and whether the blob held the
-  // model's colours (bit 0)
-  int writeback, pad0, pad1, pad2;
+  // model's colours (bit 0); whether this step's third colour is assembled a
+  // pass ahead of its solve, and then its body's body-contact mask (its
+  // smask word is zero while the other rows are assembled)
+  int writeback, early;
+  uint32_t earlyMask;
+  int pad2;
   int shapeCount[B]; // shapes <= B
   int pairHit[CS];   // body-contact pairs <= CS
+  // a two-part body system assembled a pass ahead of its solve (21 Hessian
+  // entries and 6 gradient entries per part; float batches only)
+  R staged[sizeof(R) == sizeof(float) ? 2 : 1][28];
 };
 
 // One environment's LDS record.  A wave holds 64 / L environments and their

@@ -341,7 +341,9 @@ template <int N> __device__ __forceinline__ double rowRotate(double v) {
 // environment, two with 16, four with 32.
 constexpr int defaultSolveLanes(int L) { return L >= 32 ? 4 : (L >= 16 ? 2 : 1); }
 
-template <class R, int B, int J, int CG, int CS, int L, int PL = defaultSolveLanes(L)>
+// Pairs: the model may have body-body contacts (without them, the rows and
+// the two-pass assembly of body contacts are left out).
+template <class R, int B, int J, int CG, int CS, int L, int PL = defaultSolveLanes(L), bool Pairs = true>
 struct Stepper {
   using Env = EnvLds<R, B, J, CG, CS, L>;
   using Fr = Frames<R, B, J>;
@@ -910,7 +912,7 @@ struct Stepper {
         if ((nth + 1) % nParts == part % nParts)
           groundRows(H, bi, 64 * w + __builtin_ctzll(m), true);
     nth = 0;
-    for (uint32_t m = E.smask[bi]; m; m &= m - 1, ++nth)
+    for (uint32_t m = Pairs ? E.smask[bi] : 0u; m; m &= m - 1, ++nth)
       if ((nth + 1) % nParts == part % nParts)
         selfRows(H, bi, __builtin_ctz(m));
   }
@@ -930,7 +932,7 @@ struct Stepper {
   // registers, and the assembly starts on the hinge data without the
   // dependent adjacency loads.
   struct SlotPlan {
-    int w0; // first hinge (hinge | a << 8 | b << 16) | h0 << 24 | v0 << 25 | v1 << 26 | any contact << 27
+    int w0; // first hinge (hinge | a << 8 | b << 16) | h0 << 24 | v0 << 25 | v1 << 26 | any contact << 27 | staged << 28
     int w1; // c0 | c1 << 8 | next hinge slot << 16 | end of the body's hinges << 24
   };
   __device__ SlotPlan plan(int bi, int part, int nParts) const {
@@ -996,7 +998,7 @@ struct Stepper {
         if ((!Ground || nth >= 2 * nParts) && nth % nParts == p0)
           groundRows(H, bi, 64 * w + __builtin_ctzll(g), true);
     nth = 0;
-    for (uint32_t g = E.smask[bi]; g; g &= g - 1, ++nth)
+    for (uint32_t g = Pairs ? E.smask[bi] : 0u; g; g &= g - 1, ++nth)
       if (nth % nParts == p0)
         selfRows(H, bi, __builtin_ctz(g));
     return !slow;
@@ -1012,24 +1014,55 @@ struct Stepper {
   // `quad` tells every lane of the wave that such a group exists in this pass.
   // `sp` is plan(bi, part, nParts) (float only).  Given: `given` is the
   // evaluation of the lane's first hinge at the current poses (float only).
+  // A body solved alone in a later colour may be assembled in two passes:
+  // a lane whose plan has bit 28 of its first word set (float only; the
+  // body's smask word is zero then) assembles its share of every row but the
+  // body contacts into E.staged[part] and leaves the pose alone (returning
+  // 0); a lane with `finish` set starts from that share and adds the
+  // body-contact rows of E.earlyMask -- the same sums in the same order as
+  // one assembly.
   template <bool Given = false>
   __device__ R updateBody(int bi, bool implicitDrive, int part, int nParts, bool quad, SlotPlan sp,
-                          const JointEval *given = nullptr) {
+                          const JointEval *given = nullptr, bool finish = false) {
+    const bool stage = Pairs && sizeof(R) == sizeof(float) && ((sp.w0 >> 28) & 1);
     const V3<R> x = X(bi);
     const Q4<R> q = Q(bi);
     Hess<R> H;
-    bool done = false;
-    if constexpr (sizeof(R) == sizeof(float)) {
-      // Wave-uniform choices: with or without the straight-line contacts,
-      // and the generic assembly for every lane when any lane fell outside
-      // the fast forms.
-      const bool fast = __any((sp.w0 >> 27) & 1)
-                            ? assembleFast<true, Given>(H, bi, implicitDrive, part, nParts, sp, given)
-                            : assembleFast<false, Given>(H, bi, implicitDrive, part, nParts, sp, given);
-      done = !__any(!fast);
+    if (Pairs && finish) {
+#pragma unroll
+      for (int k = 0; k < 21; ++k)
+        H.h[k] = E.staged[part][k];
+#pragma unroll
+      for (int k = 0; k < 6; ++k)
+        H.g[k] = E.staged[part][21 + k];
+      const int p0 = (part + nParts - 1) % nParts;
+      int nth = 0;
+      for (uint32_t g = E.earlyMask; g; g &= g - 1, ++nth)
+        if (nth % nParts == p0)
+          selfRows(H, bi, __builtin_ctz(g));
+    } else {
+      bool done = false;
+      if constexpr (sizeof(R) == sizeof(float)) {
+        // Wave-uniform choices: with or without the straight-line contacts,
+        // and the generic assembly for every lane when any lane fell outside
+        // the fast forms.
+        const bool fast =
+            __any((sp.w0 >> 27) & 1)
+                ? assembleFast<true, Given>(H, bi, implicitDrive, part, nParts, sp, given)
+                : assembleFast<false, Given>(H, bi, implicitDrive, part, nParts, sp, given);
+        done = !__any(!fast);
+      }
+      if (!done)
+        assembleGeneric(H, bi, implicitDrive, part, nParts);
+      if (stage) {
+#pragma unroll
+        for (int k = 0; k < 21; ++k)
+          E.staged[part][k] = H.h[k];
+#pragma unroll
+        for (int k = 0; k < 6; ++k)
+          E.staged[part][21 + k] = H.g[k];
+      }
     }
-    if (!done)
-      assembleGeneric(H, bi, implicitDrive, part, nParts);
     if constexpr (P >= 2) {
 #pragma unroll
       for (int k = 0; k < 21; ++k)
@@ -1069,11 +1102,11 @@ struct Stepper {
     V3<R> tx{st[0], st[1], st[2]}, rx{st[3], st[4], st[5]};
     const R ntx = fnorm(tx), nrx = fnorm(rx);
     R scale = mn(R(1), mn(fdiv(R(.1), mx(ntx, R(1e-30))), fdiv(R(.25), mx(nrx, R(1e-30)))));
-    if (part == 0) {
+    if (part == 0 && !stage) {
       setX(bi, faxpy(scale, tx, x));
       setQ(bi, fnormalized(fqmul(fexpmap(scale * rx), q)));
     }
-    return mx(ntx, nrx) * scale;
+    return stage ? R(0) : mx(ntx, nrx) * scale;
   }
 };
 

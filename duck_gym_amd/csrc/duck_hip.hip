@@ -238,6 +238,9 @@ class Batch final : public BatchBase {
   void record(hipStream_t s) { hipCheck(hipEventRecord(ready, s), "hipEventRecord"); }
   void launched(const char *what) { hipCheck(hipGetLastError(), what); }
   static int blocks64(int n) { return (n + 63) / 64; }
+  // The float MicroDuck-sized batch has a step compiled without body-pair
+  // code, launched for models that have none.
+  static constexpr bool kPairless = sizeof(R) == sizeof(float) && L == 16;
 
   void advance(unsigned char *states, int n, const void *targets, const void *forces,
                const void *motor, int substeps, double kp, double limit, hipStream_t s,
@@ -248,7 +251,14 @@ class Batch final : public BatchBase {
                   substeps, mode, kp, limit,
                   int(host.bodies.size()), int(host.joints.size()), int(host.shapes.size()),
                   int(host.pairs.size()), states == dStates && customBodies ? 1 : 0};
-    advanceKernel<R, B, J, CG, CS, L, PL><<<(n + G - 1) / G, 64, 0, s>>>(args);
+    if constexpr (kPairless) {
+      if (host.pairs.empty())
+        advanceKernel<R, B, J, CG, CS, L, PL, false><<<(n + G - 1) / G, 64, 0, s>>>(args);
+      else
+        advanceKernel<R, B, J, CG, CS, L, PL><<<(n + G - 1) / G, 64, 0, s>>>(args);
+    } else {
+      advanceKernel<R, B, J, CG, CS, L, PL><<<(n + G - 1) / G, 64, 0, s>>>(args);
+    }
     launched("advanceKernel");
   }
 
@@ -532,7 +542,14 @@ public:
                   nb, int(host.joints.size()), int(host.shapes.size()), int(host.pairs.size()),
                   customBodies ? 1 : 0};
     wait(s);
-    servoStepKernel<R, B, J, CG, CS, L, PL><<<(count + G - 1) / G, 64, 0, s>>>(args, sv);
+    if constexpr (kPairless) {
+      if (host.pairs.empty())
+        servoStepKernel<R, B, J, CG, CS, L, PL, false><<<(count + G - 1) / G, 64, 0, s>>>(args, sv);
+      else
+        servoStepKernel<R, B, J, CG, CS, L, PL><<<(count + G - 1) / G, 64, 0, s>>>(args, sv);
+    } else {
+      servoStepKernel<R, B, J, CG, CS, L, PL><<<(count + G - 1) / G, 64, 0, s>>>(args, sv);
+    }
     launched("servoStepKernel");
     record(s);
   }

@@ -110,6 +110,39 @@ def test_fp64_self_contact_single_iteration_matches_oracle(models, home):
     print(f"self contact: {contacts} body-body contacts, worst pose difference {worst:.3e}")
 
 
+def test_fp32_self_contact_third_colour_matches_oracle(models, home):
+    """float32 steps with body-body contacts, re-seeded from the float32 oracle
+    before every step (10 iterations): contact sets and colours exact, the
+    rest within the float32 gates.  Covers the third colour that a body
+    contact gives one foot, whose rows other than the body contact's are
+    assembled during the colour-1 pass and finished in its own pass."""
+    rng = np.random.default_rng(11)
+    E = 16
+    targets = _legs_together(home, rng, E)
+    batch = CudaBatch(models["selfc"], E, DT, ITER, 0, False)
+    oracles = oracle_envs(models["selfc"], E, DT, ITER, False)
+    for o, q in zip(oracles, targets):
+        o.reset(q)
+    codec = batch.codec()
+    tg = torch.tensor(targets, dtype=torch.float32, device=DEV)
+    fg = torch.zeros(E, 3, device=DEV)
+    third = 0
+    for step in range(30):
+        seed_batch(batch, oracles)
+        batch.step(tg, fg, 1, KP, 0.5)
+        for o, t in zip(oracles, targets):
+            o.step(t, None, 1, KP, 0.5)
+        raw = batch.export_state().cpu().numpy()
+        for e, o in enumerate(oracles):
+            gpu, ref = codec.decode(raw[e]), oracle_state(o)
+            compare_env(gpu, ref, 1e-5, f"fp32 step {step + 1} env {e}")
+            colours = np.asarray(ref["colors"])
+            # the right foot (body 15, hinged to the colour-0 shin) alone in colour 2
+            third += int(ref["colorCount"]) == 3 and int((colours == 2).sum()) == 1 and colours[15] == 2
+    assert third > 0, "no step gave the right foot alone a third colour"
+    print(f"{third} env-steps with the right foot alone in a third colour")
+
+
 def torque_gate(gpu, ref, floor, what):
     """Applied joint torque (generalized_loads column 2, kernel.cuh:546-548):
     within 1e-4 relative on every hinge with |tau| >= 1e-3 N m, and within
