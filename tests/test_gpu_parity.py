@@ -126,7 +126,7 @@ def test_fp32_self_contact_third_colour_matches_oracle(models, home):
     codec = batch.codec()
     tg = torch.tensor(targets, dtype=torch.float32, device=DEV)
     fg = torch.zeros(E, 3, device=DEV)
-    third = 0
+    third = other = 0
     for step in range(30):
         seed_batch(batch, oracles)
         batch.step(tg, fg, 1, KP, 0.5)
@@ -138,9 +138,13 @@ def test_fp32_self_contact_third_colour_matches_oracle(models, home):
             compare_env(gpu, ref, 1e-5, f"fp32 step {step + 1} env {e}")
             colours = np.asarray(ref["colors"])
             # the right foot (body 15, hinged to the colour-0 shin) alone in colour 2
-            third += int(ref["colorCount"]) == 3 and int((colours == 2).sum()) == 1 and colours[15] == 2
+            # (assembled early), or another third colour (assembled in its own pass)
+            alone = int((colours == 2).sum()) == 1 and colours[15] == 2
+            third += int(ref["colorCount"]) == 3 and alone
+            other += int(ref["colorCount"]) >= 3 and not alone
     assert third > 0, "no step gave the right foot alone a third colour"
-    print(f"{third} env-steps with the right foot alone in a third colour")
+    assert other > 0, "no step had a third colour assembled in its own pass"
+    print(f"{third} env-steps with the right foot alone in a third colour, {other} with another")
 
 
 def torque_gate(gpu, ref, floor, what):
