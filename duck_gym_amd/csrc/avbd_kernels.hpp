@@ -1593,8 +1593,37 @@ __device__ __forceinline__ void stepBody(const StepArgs &args, const ServoArgs<R
         static_assert(L <= CG, "a lane's first contact slot exists");
         // a lane without a hinge evaluates an existing slot and stores nothing
         const bool hasJoint = dualJoint >= 0;
+        // New force, penalties and stick flag of body contact i (kernel.cuh:
+        // 1029-1052), stored when v; returns its depth and its term of the
+        // error (folded by the caller).
+        const int nsc = E.s.nsc;
+        auto selfDual = [&](int i, bool v) __attribute__((always_inline)) {
+          SelfContact<R> &c = E.s.sc[v ? i : 0];
+          V3<R> ra, rb;
+          V3<R> C = stp.selfC(c, ra, rb);
+          const R depth = mx(R(0), -(C.z + alpha * c.c0));
+          V3<R> f = contactForce(C, c.lambda, c.penalty, c.friction);
+          R trial = fhypot(fmad(c.penalty[0], C.x, c.lambda[0]), fmad(c.penalty[1], C.y, c.lambda[1]));
+          bool stick = trial <= -c.friction * f.z && double(fhypot(C.x, C.y)) < 1e-5;
+          R fk[3] = {f.x, f.y, f.z}, Ck[3] = {C.x, C.y, C.z};
+          if (v) {
+            c.id = (c.id & 0x7fffffff) | (stick ? int(0x80000000u) : 0);
+#pragma unroll
+            for (int k = 0; k < 3; ++k) {
+              c.lambda[k] = fk[k];
+              if (f.z < 0 && (k == 2 || trial <= -c.friction * f.z))
+                c.penalty[k] = mn(fmad(M.betaLinear, mabs(Ck[k]), c.penalty[k]), R(1e9));
+            }
+          }
+          return V3<R>{depth, mx(R(0), -C.z), R(0)};
+        };
         auto j0 = stp.jointDual(hasJoint ? dualJoint : (lane < J ? lane : 0), hasJoint, error, ends0);
         const auto g0 = stp.groundDual(lane, lane < ngc, errC0, owner0);
+        // with body pairs, the lane's first body contact in the same block
+        // (its terms are folded after the ground contacts', as the rounds do)
+        V3<R> s0{0, 0, 0};
+        if constexpr (Pairs)
+          s0 = selfDual(lane, lane < nsc);
         if (__any(j0.wide) && j0.wide)
           error = stp.frictionDual(j0, wrapAngle(j0.angle));
         lastEval = j0.je;
@@ -1635,29 +1664,17 @@ __device__ __forceinline__ void stepBody(const StepArgs &args, const ServoArgs<R
           stp.storeGroundDual(k, gd);
           dDepth = v ? mx(dDepth, gd.depth) : dDepth;
         }
-        const int nsc = E.s.nsc;
-        for (int i0 = 0; i0 < selfRounds; i0 += L) {
+        if constexpr (Pairs) {
+          const bool v = lane < nsc;
+          dDepth = v ? mx(dDepth, s0.x) : dDepth;
+          error = v ? mx(error, s0.y) : error;
+        }
+        for (int i0 = Pairs ? L : 0; i0 < selfRounds; i0 += L) {
           const int i = i0 + lane;
           const bool v = i < nsc;
-          SelfContact<R> &c = E.s.sc[v ? i : 0];
-          V3<R> ra, rb;
-          V3<R> C = stp.selfC(c, ra, rb);
-          const R depth = mx(R(0), -(C.z + alpha * c.c0));
-          V3<R> f = contactForce(C, c.lambda, c.penalty, c.friction);
-          R trial = fhypot(fmad(c.penalty[0], C.x, c.lambda[0]), fmad(c.penalty[1], C.y, c.lambda[1]));
-          bool stick = trial <= -c.friction * f.z && double(fhypot(C.x, C.y)) < 1e-5;
-          R fk[3] = {f.x, f.y, f.z}, Ck[3] = {C.x, C.y, C.z};
-          if (v) {
-            c.id = (c.id & 0x7fffffff) | (stick ? int(0x80000000u) : 0);
-#pragma unroll
-            for (int k = 0; k < 3; ++k) {
-              c.lambda[k] = fk[k];
-              if (f.z < 0 && (k == 2 || trial <= -c.friction * f.z))
-                c.penalty[k] = mn(fmad(M.betaLinear, mabs(Ck[k]), c.penalty[k]), R(1e9));
-            }
-          }
-          dDepth = v ? mx(dDepth, depth) : dDepth;
-          error = v ? mx(error, mx(R(0), -C.z)) : error;
+          const V3<R> sd = selfDual(i, v);
+          dDepth = v ? mx(dDepth, sd.x) : dDepth;
+          error = v ? mx(error, sd.y) : error;
         }
       }
       error = groupMax<L>(error);
