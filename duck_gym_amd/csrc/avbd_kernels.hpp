@@ -1425,7 +1425,10 @@ __device__ __forceinline__ void stepBody(const StepArgs &args, const ServoArgs<R
     // body contacts reads a pose that the colour-1 pass moves, so the free
     // slot of colour 1 assembles them during that pass (bit 28 of its plan's
     // first word), and the third pass adds the body-contact rows and solves.
-    // The sums and their order are those of one assembly in the third pass.
+    // The sums and their order are those of one assembly in the third pass,
+    // unless a lane of the wave leaves the fast forms in one of the two passes
+    // and not the other (the generic assembly orders a body's rows otherwise;
+    // float only, within rounding).
     bool early = false, stageLane = false;
     if constexpr (sizeof(R) == sizeof(float) && P == 2 && Pairs) {
       if (active && twoColourSlots && E.s.colorCount == 3) {
