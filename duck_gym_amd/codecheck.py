@@ -86,10 +86,16 @@ def exec_zero_writes(text: str):
         if op == "s_getpc_b64":
             n = int(re.match(r"s\[(\d+):", regs[0]).group(1))
             pc[n] = [address + 4, 0, 0]
-        elif op == "s_add_u32" and regs[0] == regs[1] and int(regs[0][1:]) in pc:
-            _offset(pc, int(regs[0][1:]), 1, regs[2])
-        elif op == "s_addc_u32" and regs[0] == regs[1] and int(regs[0][1:]) - 1 in pc:
-            _offset(pc, int(regs[0][1:]) - 1, 2, regs[2])
+        elif op in ("s_add_u32", "s_addc_u32") and len(regs) == 3 and regs[0] == regs[1]:
+            # only an SGPR destination sn can be half of an s_getpc pair
+            # (vcc_lo, ttmp or m0 destinations are skipped)
+            sgpr = re.fullmatch(r"s(\d+)", regs[0])
+            if sgpr:
+                n = int(sgpr.group(1))
+                if op == "s_add_u32" and n in pc:
+                    _offset(pc, n, 1, regs[2])
+                elif op == "s_addc_u32" and n - 1 in pc:
+                    _offset(pc, n - 1, 2, regs[2])
         elif op == "s_setpc_b64":
             n = int(re.match(r"s\[(\d+):", regs[0]).group(1))
             if n in pc:

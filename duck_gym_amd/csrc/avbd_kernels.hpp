@@ -592,7 +592,8 @@ template <class R> struct ServoArgs {
   int feet[DUCK_MAX_FEET];
   R sites[DUCK_MAX_FEET][3];
   R *gravity, *angularVelocity, *linearVelocity, *originVelocity, *footForces, *sitePositions,
-      *siteVelocities, *airTime, *contactTime;
+      *siteVelocities, *airTime, *contactTime, *meanVelocity;
+  R meanAlpha;
 };
 
 // The servo substep's prologue (the motor channels of this substep into

@@ -199,7 +199,8 @@ template <class R> DUCK_HD R maximumNan(R a, R b) { return a != a || b != b ? R(
 // the running maxima (bam_env.py:333-335), then refresh() (bam_env.py:128-
 // 155) on the new state: gravity and velocities in the root frame, the
 // ground contact force on each foot (contactForcesKernel's sums), the foot
-// sites and the air/contact timers.
+// sites, the mean-velocity filter (bam_env.py:343-345) and the air/contact
+// timers.
 template <class R, int B, int J, int CG, int CS, class Env>
 __device__ __forceinline__ void servoEpilogue(const ServoArgs<R> &sv, const DeviceModel<R> &M, Env &E,
                                               int e) {
@@ -238,6 +239,14 @@ __device__ __forceinline__ void servoEpilogue(const ServoArgs<R> &sv, const Devi
   const V3<R> origin = v1 + cross(w1, rootR);
   put(sv.originVelocity, e, origin);
   put(sv.linearVelocity, e, rotate(conj(root), origin));
+  if (sv.meanVelocity) {
+    // mean_velocity_world.lerp_(origin, alpha) (bam_env.py:343-345) as
+    // mean + alpha (origin - mean)
+    R *m = sv.meanVelocity + size_t(e) * 3;
+    m[0] = m[0] + sv.meanAlpha * (origin.x - m[0]);
+    m[1] = m[1] + sv.meanAlpha * (origin.y - m[1]);
+    m[2] = m[2] + sv.meanAlpha * (origin.z - m[2]);
+  }
   const R h = M.dt;
   for (int f = 0; f < sv.numFeet; ++f) {
     const int body = sv.feet[f];

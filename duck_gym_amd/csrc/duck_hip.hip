@@ -55,6 +55,20 @@ void *referenceScratch(int device) {
   return address[device];
 }
 
+// The host lock of a device's `scratch`: duck_reference_noalloc holds it for
+// the whole call, so calls from several host threads on one device take turns
+// instead of overwriting each other's blob and outputs.  A plain static
+// mutex per device (no device memory).
+constexpr int kMaxScratchDevices = 64;
+std::mutex &referenceScratchLock(int device) {
+  static std::mutex locks[kMaxScratchDevices];
+  if (device < 0 || device >= kMaxScratchDevices)
+    throw DuckError(DUCK_ERR_ARGUMENT, "reference scratch: device index " +
+                                           std::to_string(device) + " beyond the library's " +
+                                           std::to_string(kMaxScratchDevices));
+  return locks[device];
+}
+
 // Clears `words` 32-bit words (a fill kernel rather than hipMemset, so that
 // the sequence stays capturable).
 __global__ void zeroWordsKernel(unsigned *p, long long words) {
@@ -217,6 +231,7 @@ struct BatchBase {
   virtual void task(const DuckTask &, int, const TaskBuffers &, hipStream_t) = 0;
   virtual void servo(const DuckServo &, const ServoBuffers &, hipStream_t) = 0;
   virtual void servoSubstep(const DuckServo &, const DuckServoSubstep &, hipStream_t) = 0;
+  virtual void kernelInfo(int which, long long *out) = 0;
 };
 
 template <class R, int B, int J, int CG, int CS, int L, int PL = defaultSolveLanes(L)>
@@ -477,6 +492,7 @@ public:
                       "reference scratch: this model needs " + std::to_string(need) +
                           " bytes of the library's " + std::to_string(kReferenceScratchBytes));
     require(dScratch != nullptr, "reference scratch: no device address");
+    std::lock_guard<std::mutex> lock(referenceScratchLock(device));
     unsigned char *base = static_cast<unsigned char *>(dScratch);
     referenceIn(base, reinterpret_cast<R *>(base + blobBytes), target, force, substeps, kp, limit,
                 bodies, joints, diag);
@@ -537,6 +553,10 @@ public:
     sv.siteVelocities = static_cast<R *>(io.site_velocities);
     sv.airTime = static_cast<R *>(io.air_time);
     sv.contactTime = static_cast<R *>(io.contact_time);
+    sv.meanVelocity = static_cast<R *>(io.mean_velocity);
+    require(!io.mean_velocity || (io.mean_velocity_alpha >= 0 && io.mean_velocity_alpha <= 1),
+            "servo substep: mean_velocity_alpha outside [0, 1]");
+    sv.meanAlpha = R(io.mean_velocity_alpha);
     StepArgs args{dModel, dFrames, dPoints, dStates, blobBytes, count, nullptr, nullptr, nullptr,
                   1, kMotorControls, 0, 0,
                   nb, int(host.joints.size()), int(host.shapes.size()), int(host.pairs.size()),
@@ -562,6 +582,39 @@ public:
     record(s);
   }
   void layout(long long *out) const override;
+  // Resources of the kernel this batch's duck_step (which = DUCK_KERNEL_STEP)
+  // or duck_servo_substep (DUCK_KERNEL_SERVO_SUBSTEP) launches -- the build
+  // without body-pair code for a model without pairs: VGPRs, static LDS and
+  // scratch per lane from the code object, resident workgroups per CU from
+  // the runtime's occupancy calculator, lanes and environments per
+  // workgroup, and workgroups per launch.
+  void kernelInfo(int which, long long *out) override {
+    DeviceGuard guard(device);
+    require(which == DUCK_KERNEL_STEP || which == DUCK_KERNEL_SERVO_SUBSTEP,
+            "kernel_info: unknown kernel");
+    const bool pairless = kPairless && host.pairs.empty();
+    const void *fn = nullptr;
+    if (which == DUCK_KERNEL_STEP)
+      fn = reinterpret_cast<const void *>(&advanceKernel<R, B, J, CG, CS, L, PL>);
+    else
+      fn = reinterpret_cast<const void *>(&servoStepKernel<R, B, J, CG, CS, L, PL>);
+    if constexpr (kPairless) {
+      if (pairless && which == DUCK_KERNEL_STEP)
+        fn = reinterpret_cast<const void *>(&advanceKernel<R, B, J, CG, CS, L, PL, false>);
+      if (pairless && which == DUCK_KERNEL_SERVO_SUBSTEP)
+        fn = reinterpret_cast<const void *>(&servoStepKernel<R, B, J, CG, CS, L, PL, false>);
+    }
+    hipFuncAttributes a{};
+    hipCheck(hipFuncGetAttributes(&a, fn), "hipFuncGetAttributes");
+    int perCu = 0;
+    hipCheck(hipOccupancyMaxActiveBlocksPerMultiprocessor(&perCu, fn, 64, 0),
+             "hipOccupancyMaxActiveBlocksPerMultiprocessor");
+    const long long v[7] = {a.numRegs, static_cast<long long>(a.sharedSizeBytes),
+                            static_cast<long long>(a.localSizeBytes), perCu, 64, G,
+                            (count + G - 1) / G};
+    for (int i = 0; i < 7; ++i)
+      out[i] = v[i];
+  }
   void exportState(void *dst, hipStream_t s) override {
     DeviceGuard guard(device);
     require(dst, "export_state: null buffer");
@@ -796,6 +849,13 @@ int duck_contact_counts(void *handle, void *out, void *hip_stream) {
 int duck_generalized_loads(void *handle, const void *offset, void *out, void *hip_stream) {
   return guarded([&] { as(handle)->generalizedLoads(offset, out, st(hip_stream)); });
 }
+int duck_kernel_info(void *handle, int which, long long *out) {
+  return guarded([&] {
+    require(handle != nullptr && out != nullptr, "null argument");
+    as(handle)->kernelInfo(which, out);
+  });
+}
+
 int duck_state_layout(void *handle, long long *out) {
   return guarded([&] {
     require(out != nullptr, "null argument");

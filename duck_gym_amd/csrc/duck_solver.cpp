@@ -195,7 +195,7 @@ void Solver::evaluateJoint(const Joint &j, std::array<double, 7> &C, std::array<
                            std::array<V6, 7> &JB) const {
   const Body &a = bodies.at(j.a), &b = bodies.at(j.b);
   const Vec3 ra = rotate(a.q, j.ra), rb = rotate(b.q, j.rb);
-  const Vec3 gap = (a.x + ra) - (b.x + rb);
+  const Vec3 gap = a.x + ra - b.x - rb; // left to right, as solver.cpp:192
   // anchors coincide: one row per world axis e, C = gap . e, with
   // d(gap)/d(x_a, theta_a) = (e, ra x e) and the opposite on b
   for (int k = 0; k < 3; ++k) {

@@ -39,6 +39,7 @@ def library():
             "duck_num_envs": (ip, [vp]),
             "duck_fp_bits": (ip, [vp]),
             "duck_state_bytes": (ctypes.c_longlong, [vp]),
+            "duck_kernel_info": (ip, [vp, ip, ctypes.POINTER(ctypes.c_longlong)]),
             "duck_joint_name": (cp, [vp, ip]),
             "duck_reset": (ip, [vp, vp, vp, vp, vp, vp]),
             "duck_step": (ip, [vp, vp, vp, ip, dbl, dbl, vp]),
@@ -73,7 +74,8 @@ def library():
 
 EXPORTED = (
     "duck_create", "duck_destroy", "duck_model_info", "duck_dims", "duck_num_envs", "duck_fp_bits",
-    "duck_state_bytes", "duck_joint_name", "duck_reset", "duck_step", "duck_step_motor", "duck_advance",
+    "duck_state_bytes", "duck_kernel_info", "duck_joint_name", "duck_reset", "duck_step",
+    "duck_step_motor", "duck_advance",
     "duck_state", "duck_contact_forces", "duck_self_contact_stats", "duck_contact_counts",
     "duck_generalized_loads", "duck_reference", "duck_reference_noalloc", "duck_state_layout",
     "duck_export_state",
@@ -113,7 +115,8 @@ class DuckServoSubstep(ctypes.Structure):
         ("linear_velocity", ctypes.c_void_p), ("origin_velocity", ctypes.c_void_p),
         ("foot_forces", ctypes.c_void_p), ("site_positions", ctypes.c_void_p),
         ("site_velocities", ctypes.c_void_p), ("air_time", ctypes.c_void_p),
-        ("contact_time", ctypes.c_void_p)]
+        ("contact_time", ctypes.c_void_p), ("mean_velocity", ctypes.c_void_p),
+        ("mean_velocity_alpha", ctypes.c_double)]
 
 
 TASK_STANDING, TASK_LOCOMOTION, TASK_ROLLOUT = 0, 1, 2
@@ -206,6 +209,24 @@ class CudaBatch:
     @property
     def state_bytes(self):
         return int(library().duck_state_bytes(self._h))
+
+    def kernel_info(self, kernel="step"):
+        """Resources of the kernel `step` ("step") or `servo_substep`
+        ("servo_substep") launches (duck_kernel_info): VGPRs, static LDS bytes
+        per workgroup, scratch bytes per lane, resident workgroups per CU,
+        lanes and environments per workgroup, workgroups per launch, and the
+        waves per SIMD they give."""
+        which = {"step": 0, "servo_substep": 1}[kernel]
+        out = (ctypes.c_longlong * 7)()
+        code = library().duck_kernel_info(self._h, which, out)
+        if code:
+            _raise(code, "kernel_info")
+        keys = ("vgprs", "lds_bytes_per_workgroup", "scratch_bytes_per_lane",
+                "workgroups_per_cu", "lanes_per_workgroup", "envs_per_workgroup",
+                "workgroups_per_launch")
+        info = dict(zip(keys, (int(v) for v in out)))
+        info["waves_per_simd"] = info["workgroups_per_cu"] * info["lanes_per_workgroup"] / 64 / 4
+        return info
 
     # --------------------------------------------------------------- checks
     def _stream(self):
@@ -361,10 +382,12 @@ class CudaBatch:
                       self_penetration=None, gravity=None, angular_velocity=None,
                       linear_velocity=None, origin_velocity=None, foot_forces=None,
                       site_positions=None, site_velocities=None, air_time=None,
-                      contact_time=None):
+                      contact_time=None, mean_velocity=None, mean_velocity_alpha=0.0):
         """One fused BAM substep (include/duck_hip.h duck_servo_substep): the
-        servo, the motor step with zero root force, the self-contact maxima and
-        the refresh() quantities, in one launch.  Outputs are written into the
+        servo, the motor step with zero root force, the self-contact maxima,
+        the refresh() quantities and, with `mean_velocity` [E,3], the
+        mean-velocity filter mean += alpha (origin velocity - mean)
+        (bam_env.py:343-345), in one launch.  Outputs are written into the
         tensors given (any may be None); in/out tensors are updated in place."""
         E, J = self.num_envs, self.num_joints
         F = len(feet)
@@ -388,9 +411,11 @@ class CudaBatch:
                                ("foot_forces", foot_forces, [E, F, 3]),
                                ("site_positions", site_positions, [E, F, 3]),
                                ("site_velocities", site_velocities, [E, F, 3]),
-                               ("air_time", air_time, [E, F]), ("contact_time", contact_time, [E, F])):
+                               ("air_time", air_time, [E, F]), ("contact_time", contact_time, [E, F]),
+                               ("mean_velocity", mean_velocity, [E, 3])):
             ptr = self._ptr(t, shape)
             setattr(io, name, None if ptr is None else ptr.value)
+        io.mean_velocity_alpha = float(mean_velocity_alpha)
         for k in range(4):
             io.root_principal_quat[k] = float(root_principal_quat[k])
         io.num_feet = F

@@ -20,6 +20,8 @@ physically plausible set for tests and benchmarks -- not BAM's fitted values.
 
 from __future__ import annotations
 
+import math
+
 import torch
 
 from .native import DuckServo
@@ -77,7 +79,10 @@ class ServoLoop:
     `BamEnv.refresh` derives (bam_env.py:128-155): `gravity`, `ang_vel`,
     `lin_vel` and `origin_velocity` of the root, the ground `contact_force`
     on each foot and its `contact` flag, foot `site_pos` / `site_vel`, and
-    the `air_time` / `contact_time` timers (bam_env.py:336-337).
+    the `air_time` / `contact_time` timers (bam_env.py:336-337).  With
+    `mean_velocity_tau` > 0, `mean_velocity` [E,3] low-passes the root-origin
+    world velocity every substep (bam_env.py:343-345, weight
+    -expm1(-dt / tau)); `reset` clears it.
 
     `fused` (default) runs a substep as one launch (`CudaBatch.servo_substep`);
     otherwise as the reference loop does: the servo kernel, the motor step,
@@ -87,7 +92,9 @@ class ServoLoop:
     body frames."""
 
     def __init__(self, batch, params, home, root_offset, *, root_principal_quat=(1.0, 0.0, 0.0, 0.0),
-                 feet=(), foot_sites=None, fused=True):
+                 feet=(), foot_sites=None, fused=True, mean_velocity_tau=0.0):
+        if mean_velocity_tau < 0:
+            raise ValueError("mean_velocity_tau must be non-negative")
         self.batch = batch
         self.params = params
         self.fused = fused
@@ -116,6 +123,10 @@ class ServoLoop:
         self.gravity, self.ang_vel, self.lin_vel, self.origin_velocity = (z3(E, 3) for _ in range(4))
         self.contact_force, self.site_pos, self.site_vel = (z3(E, F, 3) for _ in range(3))
         self.air_time, self.contact_time = z3(E, F), z3(E, F)
+        self.mean_velocity_tau = float(mean_velocity_tau)
+        self.mean_alpha = -math.expm1(-batch.dt / self.mean_velocity_tau) \
+            if self.mean_velocity_tau else 0.0
+        self.mean_velocity = z3(E, 3)
 
     @property
     def contact(self):
@@ -131,6 +142,7 @@ class ServoLoop:
         self.self_penetration[mask] = 0
         self.air_time[mask] = 0
         self.contact_time[mask] = 0
+        self.mean_velocity[mask] = 0
 
     def _refresh(self):
         """bam_env.py:128-155 and 336-337 in torch (the unfused path)."""
@@ -150,6 +162,17 @@ class ServoLoop:
             r = _inverse_rotate(foot[:, :, 3:7] * conj, sites[None].expand(b.shape[0], -1, -1))
             self.site_pos.copy_(foot[:, :, :3] + r)
             self.site_vel.copy_(foot[:, :, 7:10] + torch.linalg.cross(foot[:, :, 10:13], r))
+
+    def _after_callback(self):
+        """bam_env.py:341-347 in torch (the unfused path): the self-contact
+        maxima, the mean-velocity filter, then the air/contact timers."""
+        stats = self.batch.self_contact_stats()
+        torch.maximum(self.self_contacts, stats[:, 0], out=self.self_contacts)
+        torch.maximum(self.self_penetration, stats[:, 1], out=self.self_penetration)
+        if self.mean_velocity_tau:
+            # mean + alpha (origin - mean), the operations of the fused epilogue
+            self.mean_velocity.add_(self.mean_alpha * (self.origin_velocity - self.mean_velocity))
+        if self.feet:
             contact = self.contact
             dt = self.batch.dt
             self.air_time.copy_(torch.where(contact, 0.0, self.air_time + dt))
@@ -157,8 +180,11 @@ class ServoLoop:
 
     def substeps(self, target, count, substep_callback=None):
         """`count` physics substeps toward `target` [E,J] (bam_env.py:307-337).
-        The callback sees the state and refresh quantities of each substep
-        (in the fused path the self-contact maxima already include it)."""
+        The callback sees the state and refresh quantities of each substep.
+        The unfused path calls it where the reference does, before the
+        self-contact maxima, the mean-velocity filter and the timers take
+        this substep in; in the fused path, one launch per substep, they
+        already include it when the callback runs."""
         target = target.contiguous()
         self.self_contacts.zero_()
         self.self_penetration.zero_()
@@ -173,7 +199,9 @@ class ServoLoop:
                     angular_velocity=self.ang_vel, linear_velocity=self.lin_vel,
                     origin_velocity=self.origin_velocity, foot_forces=self.contact_force,
                     site_positions=self.site_pos, site_velocities=self.site_vel,
-                    air_time=self.air_time, contact_time=self.contact_time)
+                    air_time=self.air_time, contact_time=self.contact_time,
+                    mean_velocity=self.mean_velocity if self.mean_velocity_tau else None,
+                    mean_velocity_alpha=self.mean_alpha)
                 self.cursor = (self.cursor + 1) % (self.params.lag + 1)
                 if substep_callback is not None:
                     substep_callback(self)
@@ -187,6 +215,4 @@ class ServoLoop:
             self._refresh()
             if substep_callback is not None:
                 substep_callback(self)
-            stats = self.batch.self_contact_stats()
-            torch.maximum(self.self_contacts, stats[:, 0], out=self.self_contacts)
-            torch.maximum(self.self_penetration, stats[:, 1], out=self.self_penetration)
+            self._after_callback()

@@ -114,10 +114,21 @@ int duck_reference(void *handle, const void *target, const void *force, int subs
  * static device scratch, 64 KiB per device (held until the process ends);
  * a model whose blob plus 6 + 3 J + 13 B reals exceeds it is rejected with
  * DUCK_ERR_ARGUMENT.  Results are those of duck_reference.  The scratch is
- * shared by every call on a device and keeps the last call's contents:
- * calls that overlap on one device (from several host threads) race. */
+ * shared by every call on a device and keeps the last call's contents;
+ * calls on one device are serialised by a host lock held for the whole call
+ * (calls from several host threads take turns). */
 int duck_reference_noalloc(void *handle, const void *target, const void *force, int substeps,
                            double kp, double limit, void *bodies, void *joints, void *diag);
+
+/* Resources of the kernel that duck_step (which = DUCK_KERNEL_STEP) or
+ * duck_servo_substep (DUCK_KERNEL_SERVO_SUBSTEP) launches for this batch (no
+ * reference counterpart: for measurement).  out[7] = VGPRs per lane, static
+ * LDS bytes per workgroup, scratch bytes per lane, resident workgroups per CU
+ * (the runtime's occupancy calculator), lanes per workgroup, environments per
+ * workgroup, workgroups per launch.  Waves per SIMD = workgroups per CU x
+ * lanes per workgroup / 64 / 4. */
+enum { DUCK_KERNEL_STEP = 0, DUCK_KERNEL_SERVO_SUBSTEP = 1 };
+int duck_kernel_info(void *handle, int which, long long *out);
 
 /* Size in bytes of one environment's HBM state blob. */
 long long duck_state_bytes(void *handle);
@@ -243,6 +254,9 @@ typedef struct DuckServoSubstep {
   void *site_velocities;        /* [E,F,3] foot site velocities, out */
   void *air_time;               /* [E,F] seconds since the foot last touched, in/out */
   void *contact_time;           /* [E,F] seconds the foot has touched, in/out */
+  void *mean_velocity;          /* [E,3] low-passed root-origin world velocity, in/out
+                                   (NULL = no filter; bam_env.py:343-345) */
+  double mean_velocity_alpha;   /* filter weight per substep, -expm1(-dt / tau) */
 } DuckServoSubstep;
 
 /* One substep of the BAM-actuated environment in one launch
@@ -253,7 +267,9 @@ typedef struct DuckServoSubstep {
  * from the new state: gravity and velocities in the root frame, the ground
  * contact force on each foot (duck_contact_forces with ground_only), foot
  * site positions and velocities, and the air/contact timers (a foot touches
- * when its force exceeds 1e-5 N).  The caller advances `cursor` per
+ * when its force exceeds 1e-5 N).  With `mean_velocity`, the filter of
+ * bam_env.py:343-345 follows: mean += alpha (origin_velocity - mean), in
+ * that operation order.  The caller advances `cursor` per
  * substep as for duck_servo.  No reference counterpart as one call: it
  * replaces the reference loop's five calls and torch arithmetic. */
 int duck_servo_substep(void *handle, const DuckServo *servo, const DuckServoSubstep *io,

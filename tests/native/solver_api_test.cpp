@@ -121,6 +121,30 @@ static int math() {
   std::array<V6, 7> JA{}, JB{};
   sim.evaluateJoint(j, C, JA, JB);
   check(std::abs(C[5] - 0.8) < 1e-14 && std::abs(C[6] - 0.4) < 1e-14, "limit rows");
+  // The anchor rows bit for bit: solver.cpp:192 evaluates a.x + ra - b.x - rb
+  // left to right.  Over random poses, the grouping (a.x + ra) - (b.x + rb)
+  // rounds differently in some component, so this check tells them apart.
+  bool groupingDiffers = false;
+  unsigned seed = 12345;
+  auto uniform = [&seed]() {
+    seed = seed * 1664525u + 1013904223u;
+    return (seed >> 8) * (1.0 / 16777216.0) - 0.5;
+  };
+  for (int trial = 0; trial < 200; ++trial) {
+    sim.bodies[0].x = {uniform(), uniform(), uniform()};
+    sim.bodies[1].x = {uniform(), uniform(), uniform()};
+    sim.bodies[0].q = exp({uniform(), uniform(), uniform()});
+    sim.bodies[1].q = exp({uniform(), uniform(), uniform()});
+    sim.evaluateJoint(j, C, JA, JB);
+    const Vec3 ra = rotate(sim.bodies[0].q, j.ra), rb = rotate(sim.bodies[1].q, j.rb);
+    for (int k = 0; k < 3; ++k) {
+      const double ordered = sim.bodies[0].x[k] + ra[k] - sim.bodies[1].x[k] - rb[k];
+      const double grouped = (sim.bodies[0].x[k] + ra[k]) - (sim.bodies[1].x[k] + rb[k]);
+      check(C[k] == ordered, "anchor rows in solver.cpp's operation order");
+      groupingDiffers = groupingDiffers || grouped != ordered;
+    }
+  }
+  check(groupingDiffers, "the anchor-row check distinguishes the two groupings");
   std::printf("math checks passed\n");
   return 0;
 }

@@ -79,3 +79,19 @@ def test_built_library_has_no_vector_writes_with_exec_zero():
     text = C.disassemble(library)
     assert "advanceKernel" in text
     assert C.exec_zero_writes(text) == []
+
+
+def test_scalar_adds_to_non_sgpr_destinations_are_skipped():
+    # s_add_u32 / s_addc_u32 on vcc_lo, ttmp or m0 are no half of a far jump:
+    # the tracker skips them instead of misreading or failing on them
+    lines = LOOP + ["s_add_u32 vcc_lo, vcc_lo, 4", "s_addc_u32 vcc_hi, vcc_hi, 0",
+                    "s_add_u32 ttmp4, ttmp4, 8", "s_add_u32 m0, m0, 16",
+                    "v_accvgpr_write_b32 a0, v1", "s_or_b64 exec, exec, s[4:5]", "s_endpgm"]
+    assert [f[2] for f in C.exec_zero_writes(_asm(lines))] == ["v_accvgpr_write_b32 a0, v1"]
+    # an m0 add after s_getpc of s[0:1] does not move the s0 pair's offset
+    far = _asm(LOOP + ["v_cndmask_b32_e64 v2, 0, 1, s[4:5]",
+                       "s_getpc_b64 s[0:1]", "s_add_u32 m0, m0, 0x100",
+                       "s_add_u32 s0, s0, 0xfffffff8", "s_addc_u32 s1, s1, -1",
+                       "s_setpc_b64 s[0:1]", "s_endpgm"])
+    # s_getpc at 0x1014 yields 0x1018; -8 lands on the v_cndmask at 0x1010
+    assert C.exec_zero_writes(far) == []

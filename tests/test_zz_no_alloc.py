@@ -67,3 +67,34 @@ def test_noalloc_reference_rejects_invalid_inputs(models):
     assert "Invalid CPU reference inputs" in lib.duck_last_error().decode()
     assert lib.duck_reference_noalloc(batch._h, ptr(t), None, 1, 8.0, 0.0, ptr(out), ptr(out),
                                       ptr(out)) != 0
+
+
+def test_noalloc_largest_model_fits_and_allocates_nothing(tmp_path):
+    """The largest state the loader admits -- 32 bodies, 30 hinges and 31
+    ground shapes in float64, which runs the generic instance's blob (the
+    largest blob) -- together with its inputs and outputs needs less than the
+    64 KiB scratch, so no loadable model reaches the size rejection (it guards
+    a future growth of the blob).  The call equals duck_reference bit for bit,
+    and a warm call leaves the device's free memory unchanged."""
+    lib = library()
+    model = tmp_path / "chain32.duck"
+    model.write_text(chain(bodies=32, ground_flags=[1] * 31))
+    batch = CudaBatch(model, 1, 0.005, 10, 0, True)
+    nb, nj = batch.num_bodies, batch.num_joints
+    assert (nb, nj) == (32, 30)
+    need = lib.duck_state_bytes(batch._h) + 8 * (6 + 3 * nj + 13 * nb)
+    assert need <= 64 * 1024, need
+    target = np.random.default_rng(9).uniform(-0.2, 0.2, nj)
+    force = np.array([0.0, 0.1, 0.0])
+    torch.cuda.synchronize()
+    want = _call(lib.duck_reference, batch, target, force, 3, 8.0, 0.0)
+    got = _call(lib.duck_reference_noalloc, batch, target, force, 3, 8.0, 0.0)
+    for w, g in zip(want, got):
+        np.testing.assert_array_equal(g, w)
+    torch.cuda.synchronize()
+    free_before = torch.cuda.mem_get_info()[0]
+    again = _call(lib.duck_reference_noalloc, batch, target, force, 3, 8.0, 0.0)
+    free_after = torch.cuda.mem_get_info()[0]
+    assert free_after == free_before, (free_before, free_after)
+    for w, g in zip(want, again):
+        np.testing.assert_array_equal(g, w)
