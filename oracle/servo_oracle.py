@@ -50,30 +50,35 @@ def xl330_m6(target, position, velocity, previous_motor, previous_applied, exter
 
 
 class ServoOracle:
-    """One environment's servo loop on an oracle.Oracle."""
+    """One environment's servo loop on an oracle.Oracle.  `dtype` is the
+    actuator's arithmetic: float64, or float32 as the reference's float32
+    BamEnv evaluates actuator.py (float32 torch tensors, Python scalars
+    rounded to float32); the history, torques and the state read from the
+    oracle are held in it."""
 
-    def __init__(self, oracle, home, root_offset, lag, **supply):
+    def __init__(self, oracle, home, root_offset, lag, dtype=np.float64, **supply):
         self.o = oracle
         self.lag = lag
+        self.dtype = dtype
         self.root_offset = np.asarray(root_offset, float)
-        self.history = np.tile(np.asarray(home, float), (lag + 1, 1))
+        self.history = np.tile(np.asarray(home, dtype), (lag + 1, 1))
         self.initialized = False
         self.cursor = 0
         J = len(home)
-        self.previous_motor = np.zeros(J)
-        self.previous_applied = np.zeros(J)
+        self.previous_motor = np.zeros(J, dtype)
+        self.previous_applied = np.zeros(J, dtype)
         self.supply = supply
 
     def substep(self, target):
-        target = np.asarray(target, float)
+        target = np.asarray(target, self.dtype)
         self.history[self.cursor] = target
         if not self.initialized:
             self.history[:] = target
             self.initialized = True
         delayed = self.history[(self.cursor - self.lag) % (self.lag + 1)]
         self.cursor = (self.cursor + 1) % (self.lag + 1)
-        loads = self.o.generalized_loads(self.root_offset)
-        joints = self.o.snapshot()[1]
+        loads = self.o.generalized_loads(self.root_offset).astype(self.dtype)
+        joints = self.o.snapshot()[1].astype(self.dtype)
         motor, raw, _ = xl330_m6(delayed, joints[:, 0], joints[:, 1], self.previous_motor,
                                  self.previous_applied, -loads[:, 0] + loads[:, 1],
                                  **self.supply)

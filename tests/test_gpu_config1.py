@@ -84,11 +84,14 @@ def test_fp32_pose_tolerances_against_reference_kernel_output(tmp_path):
     rotation angles within 1e-5 m / 1e-5 rad over the first three steps and
     within 1e-3 at steps 10-200; hinge angles likewise; the compacted contact
     list (bodies, shapes, features, order, stick flags) identical after one
-    step from the common reset state, the contact count and colours at every
-    checkpoint.  Later lists may differ: the four lowest corners of a foot
-    resting flat lie within float rounding of each other, and the reference
-    takes them lowest first (kernel.cuh:338-364), so two float builds that
-    round a height differently list the same corners in another order."""
+    step from the common reset state; at every checkpoint the contact count,
+    the colours and the contact SET -- the (body, shape, feature) of every
+    ground contact, in any order -- equal the reference's.  Later lists may
+    differ in order only: the four lowest corners of a foot resting flat lie
+    within float rounding of each other, and the reference takes them lowest
+    first (kernel.cuh:338-364), so two float builds that round a height
+    differently list the same corners in another order; the test counts the
+    checkpoints where that happens."""
     worst = {}
     for f, i, step, batch in _run(32, tmp_path):
         what = f"HOME fp32 step {step}"
@@ -103,8 +106,13 @@ def test_fp32_pose_tolerances_against_reference_kernel_output(tmp_path):
         same = contact_keys(gpu["gc"]) == contact_keys(ref["gc"])
         if step == 1:
             assert same, what
+        corners = lambda entries: sorted(k[:3] for k in contact_keys(entries))  # noqa: E731
+        assert corners(gpu["gc"]) == corners(ref["gc"]), (what, corners(gpu["gc"]),
+                                                          corners(ref["gc"]))
         assert list(gpu["colors"]) == list(ref["colors"]) and gpu["colorCount"] == ref["colorCount"]
         assert diag[2] == ref["diag"][2] and diag[5] == 0
         worst[step] = (dx, rot, dj, same)
-    print("fp32 HOME (x, rotation, hinge angle, same contact list) by step:",
+    print("fp32 HOME (x, rotation, hinge angle, same contact list in order) by step:",
           {s: tuple(f"{v:.2e}" for v in w[:3]) + (w[3],) for s, w in worst.items()})
+    print("checkpoints with the same contact set in another order:",
+          [s for s, w in worst.items() if not w[3]])

@@ -75,39 +75,81 @@ def test_actuator_channels_match_oracle_fp64(models, home):
 @pytest.mark.parametrize("fused", [False, True], ids=["unfused", "fused"])
 @pytest.mark.parametrize("fp64", [True, False])
 def test_servo_loop_matches_oracle(models, home, fp64, fused):
-    n, lag, steps = 6, 2, 40
+    """40 substeps (4 per control step, a 2-substep lag) against the servo
+    oracle.  float64: poses and applied torques within 1e-9 of the float64
+    oracle.  float32: poses within 1e-3 m / 1e-3 rad (measured 1.2e-5 m,
+    4.4e-4 rad), and at substeps 4, 20 and 40 the applied torques within
+    the reference's own float32 spread on the same inputs:
+        max_{e,h} |tau_gpu32 - tau_oracle64| <= 2 max_{e,h} |tau_oracle32 - tau_oracle64| + 1e-6 N m
+    over the 12 environments and 14 hinges, where the float32 oracle is the
+    reference's float32 build (its physics bit-exact with kernel.cuh's
+    float32 CPU build, the actuator evaluated in float32 as bam_env.py does on
+    a float32 batch).  The actuator's position loop (kp_fw) turns pose
+    rounding into torque, so a fixed relative gate is not a float32 property
+    of this loop; this one ties the GPU to the reference's own float behaviour.
+    The bound does not hold hinge by hinge or environment by environment for
+    the reference against itself: its float32 spread ranges over
+    1e-9 .. 8e-5 N m across the hinges of one env and 2e-6 .. 8e-5 N m
+    across the envs at substep 40 (two float32 computations of this loop
+    round differently and the loop amplifies it), so the test prints the
+    envs and hinges beyond their own spread instead."""
+    n, lag, steps = 6 if fp64 else 12, 2, 40
     b = _batch(models["standing"], home, n, fp64)
     dt = torch.float64 if fp64 else torch.float32
     params = servo_params(**SYNTHETIC_SUPPLY, lag=lag)
     loop = ServoLoop(b, params, home, OFFSET, fused=fused)
-    oracles = []
-    for e in range(n):
-        o = Oracle(models["standing"], DT, ITER, fp64)
-        o.reset(home)
-        oracles.append(ServoOracle(o, home, OFFSET, lag, parameters=SYNTHETIC_XL330,
-                                   **SYNTHETIC_SUPPLY))
+
+    def servo_oracles(bits64):
+        out = []
+        for _ in range(n):
+            o = Oracle(models["standing"], DT, ITER, bits64)
+            o.reset(home)
+            out.append(ServoOracle(o, home, OFFSET, lag, np.float64 if bits64 else np.float32,
+                                   parameters=SYNTHETIC_XL330, **SYNTHETIC_SUPPLY))
+        return out
+
+    oracles = servo_oracles(True)
+    oracles32 = [] if fp64 else servo_oracles(False)
     plan = [_targets(home, n, 100 + k) for k in range(steps // 4)]
+    worst, hinges, envs_beyond = {}, [], {}
     for k in range(steps // 4):  # 4 substeps per control step
         loop.substeps(torch.tensor(plan[k], dtype=dt, device=DEV), 4)
-        for e, so in enumerate(oracles):
-            for _ in range(4):
-                so.substep(plan[k][e])
+        for group in (oracles, oracles32):
+            for e, so in enumerate(group):
+                for _ in range(4):
+                    so.substep(plan[k][e])
+        substep = 4 * (k + 1)
+        if not fp64 and substep in (4, 20, 40):
+            gpu = loop.previous_applied.cpu().double().numpy()
+            t64 = np.stack([so.previous_applied for so in oracles])
+            t32 = np.stack([so.previous_applied for so in oracles32]).astype(np.float64)
+            mine, spread = np.abs(gpu - t64), np.abs(t32 - t64)
+            assert mine.max() <= 2 * spread.max() + 1e-6, (
+                f"substep {substep}: applied torques differ from float64 by up to "
+                f"{mine.max():.3e} N m against the reference float32 spread {spread.max():.3e}")
+            worst[substep] = (float(mine.max()), float(spread.max()))
+            envs_beyond[substep] = int((mine.max(1) > 2 * spread.max(1) + 1e-6).sum())
+            for e, h in zip(*np.nonzero(mine > 2 * spread + 1e-6)):
+                hinges.append((substep, int(e), int(h), float(mine[e, h]), float(spread[e, h])))
     bodies = b.state()[0].cpu().double().numpy()
-    # float32: poses within 1e-3 m / 1e-3 rad after 40 substeps (measured
-    # 1.2e-5 m, 4.4e-4 rad); applied torque within 2e-3 N m (measured
-    # 6.3e-4).  The actuator's position loop (kp_fw) turns pose rounding into
-    # torque: the reference's own float32 build differs from its float64 build
-    # by the same 6.2e-4 N m / 6.4e-3 relative here, so a 1e-4 relative torque
-    # gate is not a float32 property of this loop.
     tol = 1e-9 if fp64 else 1e-3
     for e, so in enumerate(oracles):
         ref = so.o.snapshot()[0]
         np.testing.assert_allclose(bodies[e, :, :3], ref[:, :3], rtol=0, atol=tol)
         assert rotation_angle(bodies[e, :, 3:7], ref[:, 3:7]).max() <= tol
-        np.testing.assert_allclose(loop.previous_applied[e].cpu().double().numpy(),
-                                   so.previous_applied, rtol=0, atol=1e-9 if fp64 else 2e-3)
+        if fp64:
+            np.testing.assert_allclose(loop.previous_applied[e].cpu().numpy(),
+                                       so.previous_applied, rtol=0, atol=1e-9)
     assert loop.cursor == steps % (lag + 1)
     assert not bool(b.state()[2][:, 5].any())
+    if worst:
+        print("float32 applied torque vs float64, worst by substep (N m), GPU / reference:",
+              {s: f"{v[0]:.2e} / {v[1]:.2e}" for s, v in worst.items()})
+        print("envs beyond 2x their own reference spread + 1e-6 N m, by substep:", envs_beyond,
+              f"of {n}")
+        print(f"hinges beyond 2x their own reference spread + 1e-6 N m: {len(hinges)} of "
+              f"{3 * n * 14}:", [f"substep {a} env {b} hinge {c}: {d:.2e} vs {e:.2e}"
+                                 for a, b, c, d, e in hinges])
 
 
 def test_servo_reset_refills_the_ring(models, home):
@@ -147,11 +189,12 @@ def test_fused_substep_equals_unfused(models, home, fp64):
     torch arithmetic, on the biped with body contacts: states, actuator
     history, motor channels, self-contact maxima, foot forces and the
     air/contact timers bit for bit; the root-frame and site quantities to
-    rounding (torch evaluates the same formulas in another order)."""
+    rounding (torch evaluates the same formulas in another order), and so
+    the mean-velocity filter fed by the origin velocity."""
     n, lag = 8, 2
     dt = torch.float64 if fp64 else torch.float32
     principal, feet = _frame()
-    kw = dict(root_principal_quat=principal, feet=feet, foot_sites=SITES)
+    kw = dict(root_principal_quat=principal, feet=feet, foot_sites=SITES, mean_velocity_tau=0.02)
     params = servo_params(**SYNTHETIC_SUPPLY, lag=lag)
     a, b = _batch(models["selfc"], home, n, fp64), _batch(models["selfc"], home, n, fp64)
     # reach states with body-body contacts first (as the channel test does)
@@ -176,7 +219,8 @@ def test_fused_substep_equals_unfused(models, home, fp64):
                      "self_contacts", "self_penetration", "contact_force", "air_time",
                      "contact_time"):
             assert torch.equal(getattr(fused, name), getattr(plain, name)), (name, k)
-        for name in ("gravity", "ang_vel", "lin_vel", "origin_velocity", "site_pos", "site_vel"):
+        for name in ("gravity", "ang_vel", "lin_vel", "origin_velocity", "site_pos", "site_vel",
+                     "mean_velocity"):
             diff = float((getattr(fused, name) - getattr(plain, name)).abs().max())
             assert diff <= tol, (name, k, diff)
         touched += int((b.contact_counts()[:, 1] > 0).sum())
@@ -195,11 +239,28 @@ def test_fused_refresh_quantities(models, home, fp64):
     principal, feet = _frame()
     params = servo_params(**SYNTHETIC_SUPPLY, lag=1)
     a = _batch(models["selfc"], home, n, fp64)
+    tau = 0.02
     loop = ServoLoop(a, params, home, OFFSET, root_principal_quat=principal, feet=feet,
-                     foot_sites=SITES)
+                     foot_sites=SITES, mean_velocity_tau=tau)
     tol = 1e-12 if fp64 else 3e-6
+    # bam_env.py:343-345 in float64: lerp_ with weight -expm1(-dt / tau) < 0.5,
+    # i.e. mean + w (origin - mean), fed by the origin velocity of each substep
+    weight = -np.expm1(-DT / tau)
+    mean = np.zeros((n, 3))
+    seen = []
+
+    def callback(lp):
+        nonlocal mean
+        body = a.state()[0].cpu().double().numpy()[:, 1]
+        r = -T.inverse_rotate(body[:, 3:7] * np.array([1, -1, -1, -1]),
+                              np.broadcast_to(OFFSET, (n, 3)))
+        origin = body[:, 7:10] + np.cross(body[:, 10:13], r)
+        mean = mean + weight * (origin - mean)
+        seen.append(float(np.abs(lp.mean_velocity.cpu().double().numpy() - mean).max()))
+
     for k in range(6):
-        loop.substeps(torch.tensor(_targets(home, n, 300 + k), dtype=dt, device=DEV), 4)
+        loop.substeps(torch.tensor(_targets(home, n, 300 + k), dtype=dt, device=DEV), 4,
+                      substep_callback=callback)
         bodies = a.state()[0].cpu().double().numpy()
         q1 = bodies[:, 1, 3:7]
         root = T.quat_multiply(q1, np.asarray(principal) * np.array([1, -1, -1, -1]))
@@ -219,3 +280,7 @@ def test_fused_refresh_quantities(models, home, fp64):
             np.testing.assert_allclose(got, ref, rtol=0, atol=tol, err_msg=f"{name} step {k}")
         assert torch.equal(loop.contact_force, a.contact_forces(ground_only=True)[:, feet])
     assert bool(loop.contact.any())
+    assert len(seen) == 24 and max(seen) <= tol, seen
+    assert float(np.abs(mean).max()) > 1e-3  # the filter saw motion
+    loop.reset(torch.tensor([True] + [False] * (n - 1), device=DEV))
+    assert float(loop.mean_velocity[0].abs().max()) == 0.0
