@@ -14,7 +14,17 @@ The JSON line also carries
                 persistent state read and written once per step plus the
                 controls read) over its measured duration, against 8 TB/s;
                 `traffic` is the measured HBM bytes per launch from
-                rocprofv3 FETCH_SIZE/WRITE_SIZE when recorded in profiles/
+                rocprofv3 FETCH_SIZE/WRITE_SIZE when recorded in profiles/.
+                `bound` says what limits the kernel: neither HBM nor MFMA,
+                but the latency of one wave's dependent FP32 VALU chain (one
+                wave per SIMD, fixed by the LDS each workgroup stages);
+                `valu` gives the exact floating-point work per env-step of
+                the reference algorithm (oracle/op_count over the timed
+                window, recorded in profiles/flop_counts.md) over the kernel
+                time against the FP32 vector peak (157.3 TFLOP/s) and against
+                the 78.6 TFLOP/s reachable without packed FP32; `occupancy`
+                the step kernel's registers, LDS, scratch and resident waves
+                as the runtime reports them
   cpu_baseline  the reference's own CPU build of the same solver core
                 (src/cuda/kernel.cuh via src/cuda/cpu_bindings.cpp, compiled
                 in place into oracle/_ref) on a bounded sample of the
@@ -38,7 +48,12 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "physics env-steps/s at 4096 envs on 1 MI355X; achieved HBM GB/s vs peak"
 HBM_PEAK_GBS = 8000.0
+FP32_PEAK_TFLOPS = 157.3          # MI355X dense FP32 vector, packed FP32 included
+FP32_NONPACKED_PEAK_TFLOPS = 78.6  # one wave64 FMA per SIMD per quad-cycle
 ENVS, DT, ITERATIONS, KP = 4096, 0.005, 10, 8.0
+BOUND = ("latency: one wave per SIMD (the LDS each workgroup stages allows no second), "
+         "whose dependent FP32 VALU chain and LDS round trips set the step time; neither "
+         "HBM- nor MFMA-bound (profiles/advance_kernel_microduck_4096_counters.md)")
 
 
 def state_bytes_per_env(contacts, bodies=15, joints=14):
@@ -50,10 +65,29 @@ def state_bytes_per_env(contacts, bodies=15, joints=14):
     return bodies * 13 * 4 + joints * 16 * 4 + 52 * contacts + 8
 
 
-def algorithmic_bytes_per_launch(envs, contacts, model_bytes):
-    """State read + written once, targets [J] + forces [3] read, model once."""
-    per_env = 2 * state_bytes_per_env(contacts) + (14 + 3) * 4
+SELF_CONTACT_BYTES = 68  # normal, two local points, lambda 3, penalty 3, c0, ids
+
+
+def algorithmic_bytes_per_launch(envs, contacts, model_bytes, self_contacts=0.0):
+    """State read + written once (with `self_contacts` live body-contact cache
+    entries per env), targets [J] + forces [3] read, model once."""
+    per_env = 2 * (state_bytes_per_env(contacts) + SELF_CONTACT_BYTES * self_contacts) + \
+        (14 + 3) * 4
     return envs * per_env + model_bytes
+
+
+def servo_bytes_per_env(contacts, self_contacts, joints=14, feet=2):
+    """One fused servo substep of one env: the persistent state read and
+    written once, plus the actuator's buffers -- the ring slot written and the
+    delayed one read, the targets and root offset read, previous raw/applied
+    torques read and written, the motor channels and supply written, the
+    self-contact maxima read and written, the refresh outputs written (root
+    gravity, angular, linear and origin velocity; per foot the force, site
+    position and velocity) and the air/contact timers read and written."""
+    state = 2 * (state_bytes_per_env(contacts) + SELF_CONTACT_BYTES * self_contacts)
+    actuator = (2 * joints + joints + 3 + 2 * 2 * joints + 3 * joints + 1 + 2 * 2
+                + 4 * 3 + feet * 9 + 2 * 2 * feet) * 4 + 2  # + the initialized flag R/W
+    return state + actuator
 
 
 def measured_traffic():
@@ -63,6 +97,68 @@ def measured_traffic():
         return None
     m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", path.read_text())
     return float(m.group(1)) if m else None
+
+
+def measured_valu():
+    """The step kernel's VALU counters recorded from rocprofv3 in profiles/
+    (fixed HOME, 4096 envs): the fraction of the wave's life issuing VALU
+    instructions, the active lanes per VALU instruction, and the FP32 lane
+    operations it executes per env-step."""
+    path = ROOT / "profiles" / "advance_kernel_microduck_4096_counters.md"
+    if not path.exists():
+        return None
+    text, out = path.read_text(), {}
+    for key in ("valu_busy_fraction", "valu_lanes_active", "executed_fp32_lane_flop_per_env_step"):
+        m = re.search(rf"^{key}:\s*([0-9.eE+]+)", text, re.M)
+        if m:
+            out[key] = float(m.group(1))
+    return out or None
+
+
+def flop_per_env_step(workload):
+    """Exact floating-point operations per env-step of the reference
+    algorithm on `workload` (oracle/op_count over the timed window, recorded
+    in profiles/flop_counts.md by oracle/flop_counts.py), or None."""
+    path = ROOT / "profiles" / "flop_counts.md"
+    if not path.exists():
+        return None
+    m = re.search(rf"flop_per_env_step\.{workload}:\s*([0-9.]+)", path.read_text())
+    return float(m.group(1)) if m else None
+
+
+def roofline(kernel_s, algo_bytes, env_steps_per_launch, flop_workload, occupancy,
+             traffic=None, kernel="advanceKernel"):
+    """The roofline object of a bench line for the dominant kernel: HBM
+    (the metric's figures), the FP32-VALU fraction and the occupancy."""
+    achieved = algo_bytes / kernel_s / 1e9
+    out = {
+        "bound": "latency",
+        "bound_detail": BOUND,
+        "achieved": achieved,
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": achieved / HBM_PEAK_GBS,
+        "traffic": traffic,
+        "kernel": kernel,
+        "kernel_ms": kernel_s * 1e3,
+        "algorithmic_bytes_per_launch": algo_bytes,
+        "valu": None,
+        "occupancy": occupancy,
+    }
+    flop = flop_per_env_step(flop_workload)
+    if flop is not None:
+        tflops = flop * env_steps_per_launch / kernel_s / 1e12
+        out["valu"] = {
+            "flop_per_env_step": flop,
+            "flop_source": f"oracle/op_count on the {flop_workload} workload "
+                           "(profiles/flop_counts.md)",
+            "achieved_tflops": tflops,
+            "peak_tflops": FP32_PEAK_TFLOPS,
+            "frac": tflops / FP32_PEAK_TFLOPS,
+            "peak_nonpacked_tflops": FP32_NONPACKED_PEAK_TFLOPS,
+            "frac_nonpacked": tflops / FP32_NONPACKED_PEAK_TFLOPS,
+        }
+    return out
 
 
 def host_facts():
@@ -215,18 +311,27 @@ def other_workload(args):
         for s in range(args.warmup):
             batch.step(blocks[s // 4], forces, 1, kp, 0.0)
         torch.cuda.synchronize()
+        stream = torch.cuda.current_stream()
+        begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         t0 = time.perf_counter()
+        begin.record(stream)
         for s in range(args.warmup, args.warmup + args.steps):
             batch.step(blocks[s // 4], forces, 1, kp, 0.0)
+        end.record(stream)
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
+        kernel_s = begin.elapsed_time(end) / 1000.0 / args.steps
         failed = int((batch.state()[2][:, 5] != 0).sum())
         value = E * args.steps / wall
+        counts = batch.contact_counts().float().mean(0)
+        algo = algorithmic_bytes_per_launch(E, float(counts[0]), 4 * 4096, float(counts[1]))
+        line_roofline = roofline(kernel_s, algo, E, args.workload, batch.kernel_info())
         config = {"workload": "servo-target sweep, HOME + U(-0.3, 0.3) every 4 steps, body "
                               "contacts between the leg chains, friction U(0.5, 1.2)" if sweep
                   else "drop/jump stress: base height U(0.15, 0.35) m, rotation +-0.5 rad, "
                        "velocity N(0, 0.5), masses x U(0.9, 1.1)",
-                  "envs": E, "iterations": iterations, "dt_s": DT, "failed_envs": failed}
+                  "envs": E, "iterations": iterations, "dt_s": DT, "failed_envs": failed,
+                  "live_contacts_per_env_at_end": [float(counts[0]), float(counts[1])]}
         ms = wall / args.steps * 1e3
     elif args.workload == "rollout":
         from duck_gym_amd.tensor_env import TensorEnv
@@ -240,17 +345,36 @@ def other_workload(args):
             torch.nn.Linear(48, 256), torch.nn.ELU(), torch.nn.Linear(256, 128), torch.nn.ELU(),
             torch.nn.Linear(128, 14)).to(dev)
         obs, _ = env.get_observations()
+        stream = torch.cuda.current_stream()
+        begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         with torch.no_grad():
             for _ in range(args.warmup):
                 obs, _, _, _ = env.step(policy(obs))
             torch.cuda.synchronize()
             t0 = time.perf_counter()
+            begin.record(stream)
             for _ in range(args.steps):
                 obs, _, _, _ = env.step(policy(obs))
+            end.record(stream)
             torch.cuda.synchronize()
         wall = time.perf_counter() - t0
         value = E * args.steps * substeps / wall
         ms = wall / args.steps * 1e3
+        # the whole control step (policy, task kernels and the 4-substep step
+        # launch) on the stream, per physics step; the step kernel alone is in
+        # the rocprofv3 trace (profiles/rollout_32768.md)
+        control_s = begin.elapsed_time(end) / 1000.0 / args.steps
+        counts = env.native.contact_counts().float().mean(0)
+        # one step launch of `substeps` physics steps moves the state once;
+        # the task kernels add the observation, the actions and last action,
+        # reward and done flags
+        algo = algorithmic_bytes_per_launch(E, float(counts[0]), 4 * 4096) + \
+            E * (48 * 4 + 2 * 14 * 4 + 4 * 4)
+        line_roofline = roofline(control_s, algo, E * substeps, "home",
+                                 env.native.kernel_info(), kernel="control step (all kernels)")
+        line_roofline["valu"] and line_roofline["valu"].update(
+            flop_source="oracle/op_count on the HOME workload (the rollout's targets stay "
+                        "near HOME; its trajectory is not counted separately)")
         config = {"workload": "tensor-env rollout: 48-wide observation, locomotion reward, reset "
                               "below 0.08 m, random-init 48-256-128-14 ELU policy",
                   "envs": E, "iterations": ITERATIONS, "dt_s": DT,
@@ -279,11 +403,23 @@ def other_workload(args):
             for k in range(args.warmup):
                 loop.substeps(targets[k], substeps)
             torch.cuda.synchronize()
+            stream = torch.cuda.current_stream()
+            begin = torch.cuda.Event(enable_timing=True)
+            end = torch.cuda.Event(enable_timing=True)
             t0 = time.perf_counter()
+            begin.record(stream)
             for k in range(args.warmup, args.warmup + args.steps):
                 loop.substeps(targets[k], substeps)
+            end.record(stream)
             torch.cuda.synchronize()
             timing[fused] = time.perf_counter() - t0
+            if fused:
+                kernel_s = begin.elapsed_time(end) / 1000.0 / (args.steps * substeps)
+                counts = batch.contact_counts().float().mean(0)
+                algo = E * servo_bytes_per_env(float(counts[0]), float(counts[1])) + 4 * 4096
+                line_roofline = roofline(kernel_s, algo, E, "servo",
+                                         batch.kernel_info("servo_substep"),
+                                         kernel="servoStepKernel")
         wall = timing[True]
         value = E * args.steps * substeps / wall
         ms = wall / args.steps * 1e3
@@ -298,6 +434,7 @@ def other_workload(args):
                   "unfused": "servo kernel, motor step, state/contact-force/self-contact "
                              "queries and torch refresh arithmetic per substep"}
     elif args.workload == "train":
+        line_roofline = None
         from duck_gym_amd.on_policy import STANDING, OnPolicyRunner
         from duck_gym_amd.tensor_env import TensorEnv
 
@@ -327,7 +464,7 @@ def other_workload(args):
     return {"metric": f"physics env-steps/s ({args.workload} workload)", "value": value,
             "unit": "env-steps/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
             "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-            "dtype": "fp32", "data": "synthetic", "config": config}
+            "dtype": "fp32", "data": "synthetic", "config": config, "roofline": line_roofline}
 
 
 def main():
@@ -421,7 +558,6 @@ def main():
     value = E * args.steps / wall
     model_bytes = 4 * 4096  # read-only model tables streamed per launch (upper bound)
     algo = algorithmic_bytes_per_launch(E, round(contacts), model_bytes)  # one state round trip
-    achieved = algo / kernel_s / 1e9
     traffic = measured_traffic() if E == ENVS and K == 1 else None
     line = {
         "metric": METRIC,
@@ -447,18 +583,18 @@ def main():
                       f"{K} physics steps per kernel launch",
             "live_ground_contacts_per_env": contacts,
         },
-        "roofline": {
-            "bound": "hbm",
-            "achieved": achieved,
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": achieved / HBM_PEAK_GBS,
-            "traffic": traffic,
-            "kernel_ms": kernel_s * 1e3,
-            "algorithmic_bytes_per_launch": algo,
-        },
+        "roofline": roofline(kernel_s, algo, E * K, "home", batch.kernel_info(), traffic),
         "cpu_baseline": None,
     }
+    valu = line["roofline"]["valu"]
+    counters = measured_valu() if E == ENVS and K == 1 else None
+    if valu is not None and counters is not None:
+        # the rocprofv3 counters of the same kernel and workload: the executed
+        # FP32 lane operations at this run's kernel time
+        counters["executed_tflops"] = \
+            counters["executed_fp32_lane_flop_per_env_step"] * E / kernel_s / 1e12
+        counters["source"] = "profiles/advance_kernel_microduck_4096_counters.md"
+        valu["counters"] = counters
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(model, home)
     print(json.dumps(line), flush=True)

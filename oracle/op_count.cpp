@@ -8,9 +8,19 @@
 // resets one environment to the joint angles q, holds them as targets with
 // gain kp, runs `steps` physics steps and prints the per-step averages of the
 // last half of the steps (after the contacts have settled).
+//
+//   op_count <model.duck> <steps> <iterations> <dt> <kp> - [first]  < script
+//
+// reads the environment's start and controls from standard input instead:
+// q_0 .. q_{J-1}, root (xyz offset, rotation vector), ground friction (< 0:
+// the shapes'), mass scale, root linear velocity xyz; then per step a letter
+// and its controls: `T` and J targets held with gain kp, or `M` and 3 J motor
+// channels (torque, friction budget, damping per hinge).  The averages cover
+// steps first .. steps - 1 (default: the last half).
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
+#include <string>
 #include <vector>
 
 namespace opcount {
@@ -81,29 +91,90 @@ int main(int argc, char **argv) {
   h.model = flatten<Counted>(file, dt, iterations, 0);
   h.env.initialize(h.model);
   const int nj = int(file.joints.size());
-  if (argc != 6 + nj) {
+  const bool script = argc >= 7 && std::string(argv[6]) == "-";
+  if (!script && argc != 6 + nj) {
     std::fprintf(stderr, "expected %d joint angles\n", nj);
     return 2;
   }
+  const int first = script && argc > 7 ? std::atoi(argv[7]) : steps / 2;
+  auto read = [](double &v) {
+    if (std::scanf("%lf", &v) != 1) {
+      std::fprintf(stderr, "op_count: truncated script\n");
+      std::exit(2);
+    }
+  };
   std::vector<Counted> q(nj), root(6, Counted(0.0));
-  for (int j = 0; j < nj; ++j)
-    q[j] = std::atof(argv[6 + j]);
-  h.env.resetPose(q.data(), root.data());
+  double friction = -1, massScale = 1, velocity[3] = {0, 0, 0};
   for (int j = 0; j < nj; ++j) {
-    auto &jt = h.env.joints[j];
-    jt.target = q[j];
-    jt.kp = Counted(kp);
-    jt.maxTorque = Counted(0.0);
-    jt.torque = h.model.joints[j].torque;
-    jt.frictionloss = h.model.joints[j].frictionloss;
-    jt.damping = h.model.joints[j].damping;
+    double v = script ? 0 : std::atof(argv[6 + j]);
+    if (script)
+      read(v);
+    q[j] = v;
   }
+  if (script) {
+    for (auto &r : root) {
+      double v;
+      read(v);
+      r = v;
+    }
+    read(friction);
+    read(massScale);
+    for (double &v : velocity)
+      read(v);
+  }
+  h.env.resetPose(q.data(), root.data());
+  // the batch extensions of duck_reset (per-env friction, mass/inertia scale
+  // of every dynamic body, root linear velocity), as the oracle applies them
+  h.env.frictionOverride = Counted(friction);
+  for (auto &b : h.env.bodies)
+    if (b.mass > 0) {
+      b.mass = b.mass * Counted(massScale);
+      b.inertia = scale(Counted(massScale), b.inertia);
+      b.v = {Counted(velocity[0]), Counted(velocity[1]), Counted(velocity[2])};
+    }
+  auto setTargets = [&](const std::vector<Counted> &target) {
+    for (int j = 0; j < nj; ++j) {
+      auto &jt = h.env.joints[j];
+      jt.target = target[j];
+      jt.kp = Counted(kp);
+      jt.maxTorque = Counted(0.0);
+      jt.torque = h.model.joints[j].torque;
+      jt.frictionloss = h.model.joints[j].frictionloss;
+      jt.damping = h.model.joints[j].damping;
+    }
+  };
+  setTargets(q);
   opcount::Counts total;
   int counted = 0;
   for (int s = 0; s < steps; ++s) {
+    if (script) {
+      char kind = 0;
+      if (std::scanf(" %c", &kind) != 1 || (kind != 'T' && kind != 'M')) {
+        std::fprintf(stderr, "op_count: step %d needs T or M\n", s);
+        return 2;
+      }
+      if (kind == 'T') {
+        std::vector<Counted> target(nj);
+        for (auto &t : target) {
+          double v;
+          read(v);
+          t = v;
+        }
+        setTargets(target);
+      } else {
+        std::vector<Counted> motor(3 * nj);
+        for (auto &m : motor) {
+          double v;
+          read(v);
+          m = v;
+        }
+        Counted force[3] = {Counted(0.0), Counted(0.0), Counted(0.0)};
+        h.env.setMotor(motor.data(), force);
+      }
+    }
     opcount::g = {};
     h.env.advance(1);
-    if (s >= steps / 2) {
+    if (s >= first) {
       total.add += opcount::g.add, total.mul += opcount::g.mul, total.div += opcount::g.div;
       total.sqrt += opcount::g.sqrt, total.trig += opcount::g.trig;
       ++counted;
