@@ -1,10 +1,13 @@
 // C ABI of the gfx950 AVBD batch (include/duck_hip.h): model upload, state
 // ownership, stream ordering and kernel dispatch.
 #include "../../include/duck_hip.h"
+#include "avbd_sequential.hpp"
+#include "avbd_sequential_pack.hpp"
 #include "avbd_servo.hpp"
 #include "avbd_task.hpp"
 #include "duck_model.hpp"
 
+#include <algorithm>
 #include <cstring>
 #include <memory>
 #include <mutex>
@@ -747,6 +750,84 @@ BatchBase *as(void *h) {
 }
 hipStream_t st(void *s) { return static_cast<hipStream_t>(s); }
 
+// ---- explicit-sequential step (duck_sequential_step) ----
+
+// `steps` steps of environment i, whose record starts at records + offset[i];
+// an environment stops at its first fault.
+__global__ __launch_bounds__(64) void sequentialStepKernel(unsigned char *records,
+                                                           const long long *offset, int n,
+                                                           int steps) {
+  const int i = blockIdx.x * 64 + threadIdx.x;
+  if (i >= n)
+    return;
+  seq::Env e(records + offset[i]);
+  for (int s = 0; s < steps && e.r->status == DUCK_SEQ_OK; ++s)
+    e.step();
+}
+
+// The device buffers of one device, reused and grown across calls; calls on
+// one device take turns on them.
+struct SequentialBuffers {
+  std::mutex lock;
+  unsigned char *records = nullptr;
+  long long *offsets = nullptr;
+  size_t recordBytes = 0, offsetCount = 0;
+};
+SequentialBuffers &sequentialBuffers(int device) {
+  static std::mutex guard;
+  static std::vector<std::unique_ptr<SequentialBuffers>> all;
+  std::lock_guard<std::mutex> lock(guard);
+  require(device >= 0 && device < 1024, "sequential step: invalid device");
+  if (device >= int(all.size()))
+    all.resize(device + 1);
+  if (!all[device])
+    all[device] = std::make_unique<SequentialBuffers>();
+  return *all[device];
+}
+
+void sequentialStep(DuckSeqEnv *envs, int n, int steps, int device) {
+  require(envs != nullptr && n > 0 && steps > 0, "sequential step: no environments or steps");
+  int devices = 0;
+  hipCheck(hipGetDeviceCount(&devices), "hipGetDeviceCount");
+  require(device >= 0 && device < devices, "sequential step: invalid device");
+  std::vector<unsigned char> image;
+  std::vector<long long> offsets;
+  try {
+    for (int i = 0; i < n; ++i)
+      seq::checkSequential(envs[i], steps);
+    seq::packSequential(envs, n, image, offsets);
+  } catch (const seq::SeqError &e) {
+    throw DuckError(DUCK_ERR_ARGUMENT, e.what());
+  }
+  const size_t total = image.size();
+  DeviceGuard guard(device);
+  SequentialBuffers &buf = sequentialBuffers(device);
+  std::lock_guard<std::mutex> lock(buf.lock);
+  if (total > buf.recordBytes) {
+    if (buf.records)
+      hipCheck(hipFree(buf.records), "hipFree(sequential records)");
+    buf.records = nullptr;
+    buf.recordBytes = 0;
+    hipCheck(hipMalloc(&buf.records, total), "hipMalloc(sequential records)");
+    buf.recordBytes = total;
+  }
+  if (size_t(n) > buf.offsetCount) {
+    if (buf.offsets)
+      hipCheck(hipFree(buf.offsets), "hipFree(sequential offsets)");
+    buf.offsets = nullptr;
+    buf.offsetCount = 0;
+    hipCheck(hipMalloc(&buf.offsets, sizeof(long long) * n), "hipMalloc(sequential offsets)");
+    buf.offsetCount = n;
+  }
+  hipCheck(hipMemcpy(buf.records, image.data(), total, hipMemcpyHostToDevice), "upload");
+  hipCheck(hipMemcpy(buf.offsets, offsets.data(), sizeof(long long) * n, hipMemcpyHostToDevice),
+           "upload");
+  sequentialStepKernel<<<(n + 63) / 64, 64, 0, 0>>>(buf.records, buf.offsets, n, steps);
+  hipCheck(hipGetLastError(), "sequentialStepKernel");
+  hipCheck(hipMemcpy(image.data(), buf.records, total, hipMemcpyDeviceToHost), "download");
+  seq::unpackSequential(envs, n, image, offsets);
+}
+
 } // namespace
 } // namespace duckhip
 
@@ -849,6 +930,10 @@ int duck_contact_counts(void *handle, void *out, void *hip_stream) {
 int duck_generalized_loads(void *handle, const void *offset, void *out, void *hip_stream) {
   return guarded([&] { as(handle)->generalizedLoads(offset, out, st(hip_stream)); });
 }
+int duck_sequential_step(DuckSeqEnv *envs, int num_envs, int steps, int device) {
+  return guarded([&] { sequentialStep(envs, num_envs, steps, device); });
+}
+
 int duck_kernel_info(void *handle, int which, long long *out) {
   return guarded([&] {
     require(handle != nullptr && out != nullptr, "null argument");

@@ -1,13 +1,18 @@
-// duck::Solver (include/duck/solver.hpp) over the C ABI of this library: a
-// one-environment float64 device batch per Solver, written from and read
-// back into the public members around each step.
+// duck::Solver (include/duck/solver.hpp) over the C ABI of this library.
+// step() and stepAll() hand the public members to duck_sequential_step (the
+// explicit-sequential step of src/solver.cpp, one GPU thread per
+// environment) and read them back; stepImplicit() writes them into a
+// one-environment float64 device batch of the CudaBatch step and reads it
+// back.
 #include "../../include/duck/solver.hpp"
 #include "../../include/duck_hip.h"
 #include "duck_model.hpp"
 
 #include <hip/hip_runtime_api.h>
 
+#include <algorithm>
 #include <cctype>
+#include <exception>
 #include <cstdio>
 #include <cstring>
 #include <fstream>
@@ -284,7 +289,277 @@ std::string modelText(const Solver &s, bool state) {
 
 } // namespace
 
+namespace {
+
+// One Solver's structs for duck_sequential_step.
+struct SequentialStage {
+  std::vector<DuckSeqBody> bodies;
+  std::vector<DuckSeqJoint> joints;
+  std::vector<DuckSeqShape> shapes;
+  std::vector<double> points;
+  std::vector<DuckSeqContact> contacts;
+  DuckSeqEnv env{};
+};
+
+void put3(double *d, Vec3 v) {
+  d[0] = v.x;
+  d[1] = v.y;
+  d[2] = v.z;
+}
+void put4(double *d, Quat q) {
+  d[0] = q.w;
+  d[1] = q.x;
+  d[2] = q.y;
+  d[3] = q.z;
+}
+Vec3 get3(const double *d) { return {d[0], d[1], d[2]}; }
+Quat get4(const double *d) { return {d[0], d[1], d[2], d[3]}; }
+
+void stage(const Solver &s, SequentialStage &st) {
+  const Options &o = s.options;
+  DuckSeqOptions &so = st.env.options;
+  so.dt = o.dt;
+  so.alpha = o.alpha;
+  so.gamma = o.gamma;
+  so.beta_linear = o.betaLinear;
+  so.beta_angular = o.betaAngular;
+  so.tolerance = o.tolerance;
+  put3(so.gravity, o.gravity);
+  so.iterations = o.iterations;
+  so.ground = o.ground ? 1 : 0;
+  st.bodies.assign(s.bodies.size(), DuckSeqBody{});
+  for (size_t i = 0; i < s.bodies.size(); ++i) {
+    const Body &b = s.bodies[i];
+    DuckSeqBody &d = st.bodies[i];
+    d.mass = b.mass;
+    put3(d.inertia, b.inertia);
+    put3(d.x, b.x);
+    put3(d.v, b.v);
+    put3(d.w, b.w);
+    put3(d.x0, b.x0);
+    put3(d.xp, b.xp);
+    put3(d.force, b.force);
+    put4(d.q, b.q);
+    put4(d.q0, b.q0);
+    put4(d.qp, b.qp);
+  }
+  st.joints.assign(s.joints.size(), DuckSeqJoint{});
+  for (size_t i = 0; i < s.joints.size(); ++i) {
+    const Joint &j = s.joints[i];
+    DuckSeqJoint &d = st.joints[i];
+    d.a = j.a;
+    d.b = j.b;
+    d.limited = j.limited ? 1 : 0;
+    put3(d.ra, j.ra);
+    put3(d.rb, j.rb);
+    put3(d.axis_a, j.axisA);
+    put3(d.axis_b, j.axisB);
+    put3(d.tangent_a, j.tangentA);
+    put3(d.tangent_b, j.tangentB);
+    d.lo = j.lo;
+    d.hi = j.hi;
+    d.damping = j.damping;
+    d.armature = j.armature;
+    d.frictionloss = j.frictionloss;
+    d.lambda_f = j.lambdaF;
+    d.penalty_f = j.penaltyF;
+    d.torque = j.torque;
+    d.kp = j.kp;
+    d.target = j.target;
+    d.max_torque = j.maxTorque;
+    d.angle0 = j.angle0;
+    d.velocity0 = j.velocity0;
+    for (int k = 0; k < 7; ++k) {
+      d.lambda[k] = j.lambda[k];
+      d.penalty[k] = j.penalty[k];
+      d.c0[k] = j.c0[k];
+    }
+  }
+  st.shapes.assign(s.shapes.size(), DuckSeqShape{});
+  st.points.clear();
+  for (size_t i = 0; i < s.shapes.size(); ++i) {
+    const Shape &sh = s.shapes[i];
+    DuckSeqShape &d = st.shapes[i];
+    d.body = sh.body;
+    d.type = sh.type;
+    d.ground = sh.ground ? 1 : 0;
+    d.first_point = int(st.points.size() / 3);
+    d.num_points = int(sh.localPoints.size());
+    for (Vec3 p : sh.localPoints) {
+      st.points.push_back(p.x);
+      st.points.push_back(p.y);
+      st.points.push_back(p.z);
+    }
+    put3(d.center, sh.center);
+    put3(d.size, sh.size);
+    put4(d.q, sh.q);
+    d.friction = sh.friction;
+    d.bounding_radius = sh.boundingRadius;
+  }
+  const size_t capacity = std::max(s.contacts.size(), 4 * s.shapes.size());
+  st.contacts.assign(capacity, DuckSeqContact{});
+  for (size_t i = 0; i < s.contacts.size(); ++i) {
+    const Contact &c = s.contacts[i];
+    DuckSeqContact &d = st.contacts[i];
+    d.body = c.body;
+    d.shape = c.shape;
+    d.feature = c.feature;
+    d.stick = c.stick ? 1 : 0;
+    put3(d.local, c.local);
+    put3(d.anchor, c.anchor);
+    d.radius = c.radius;
+    d.friction = c.friction;
+    d.c0 = c.c0;
+    for (int k = 0; k < 3; ++k) {
+      d.lambda[k] = c.lambda[k];
+      d.penalty[k] = c.penalty[k];
+    }
+  }
+  DuckSeqEnv &e = st.env;
+  e.num_bodies = int(st.bodies.size());
+  e.num_joints = int(st.joints.size());
+  e.num_shapes = int(st.shapes.size());
+  e.num_points = int(st.points.size() / 3);
+  e.num_contacts = int(s.contacts.size());
+  e.contact_capacity = int(capacity);
+  e.bodies = st.bodies.data();
+  e.joints = st.joints.data();
+  e.shapes = st.shapes.data();
+  e.points = st.points.data();
+  e.contacts = st.contacts.data();
+}
+
+void unstage(const SequentialStage &st, Solver &s) {
+  for (size_t i = 0; i < s.bodies.size(); ++i) {
+    Body &b = s.bodies[i];
+    const DuckSeqBody &d = st.bodies[i];
+    b.x = get3(d.x);
+    b.v = get3(d.v);
+    b.w = get3(d.w);
+    b.x0 = get3(d.x0);
+    b.xp = get3(d.xp);
+    b.q = get4(d.q);
+    b.q0 = get4(d.q0);
+    b.qp = get4(d.qp);
+  }
+  for (size_t i = 0; i < s.joints.size(); ++i) {
+    Joint &j = s.joints[i];
+    const DuckSeqJoint &d = st.joints[i];
+    j.lambdaF = d.lambda_f;
+    j.penaltyF = d.penalty_f;
+    j.angle0 = d.angle0;
+    j.velocity0 = d.velocity0;
+    for (int k = 0; k < 7; ++k) {
+      j.lambda[k] = d.lambda[k];
+      j.penalty[k] = d.penalty[k];
+      j.c0[k] = d.c0[k];
+    }
+  }
+  s.contacts.assign(st.env.num_contacts, Contact{});
+  for (int i = 0; i < st.env.num_contacts; ++i) {
+    const DuckSeqContact &d = st.contacts[i];
+    Contact &c = s.contacts[i];
+    c.body = d.body;
+    c.shape = d.shape;
+    c.feature = d.feature;
+    c.stick = d.stick != 0;
+    c.local = get3(d.local);
+    c.anchor = get3(d.anchor);
+    c.radius = d.radius;
+    c.friction = d.friction;
+    c.c0 = d.c0;
+    for (int k = 0; k < 3; ++k) {
+      c.lambda[k] = d.lambda[k];
+      c.penalty[k] = d.penalty[k];
+    }
+  }
+  const DuckSeqDiagnostics &g = st.env.diagnostics;
+  s.diagnostics.jointError = g.joint_error;
+  s.diagnostics.axisError = g.axis_error;
+  s.diagnostics.penetration = g.penetration;
+  s.diagnostics.update = g.update;
+  s.diagnostics.contacts = g.contacts;
+  s.diagnostics.iterations = g.iterations;
+  s.diagnostics.converged = g.converged != 0;
+}
+
+// What the reference's step throws before it changes anything
+// (solver.cpp:316-320).
+void checkSequential(const Solver &s) {
+  if (!s.collisionPairs.empty())
+    throw std::runtime_error("Body contacts require the shared CpuBatch/CUDA solver");
+  const Options &o = s.options;
+  if (!(o.dt > 0) || o.iterations < 1 || o.alpha < 0 || o.alpha >= 1 || o.gamma <= 0 ||
+      o.gamma >= 1)
+    throw std::runtime_error("Invalid solver options");
+}
+
+// The exception the reference's step throws where the device step stopped.
+void throwFault(int status) {
+  switch (status) {
+  case DUCK_SEQ_HESSIAN:
+    throw std::runtime_error("Non-positive local Hessian");
+  case DUCK_SEQ_NONFINITE:
+    throw std::runtime_error("Non-finite state");
+  case DUCK_SEQ_QUATERNION:
+    throw std::runtime_error("Zero quaternion");
+  default:
+    throw std::runtime_error("sequential step: unknown fault " + std::to_string(status));
+  }
+}
+
+// Solver::step of solvers[0..n) in one launch, with the outcome of stepping
+// them in order: an environment the reference would reject stops the list
+// there, and the first environment that faults is written back and thrown.
+void stepSolvers(Solver *const *solvers, int n) {
+  int stepped = n;
+  std::exception_ptr rejected;
+  for (int i = 0; i < n; ++i) {
+    try {
+      checkSequential(*solvers[i]);
+    } catch (...) {
+      rejected = std::current_exception();
+      stepped = i;
+      break;
+    }
+  }
+  if (stepped > 0) {
+    std::vector<SequentialStage> stages(stepped);
+    std::vector<DuckSeqEnv> envs(stepped);
+    for (int i = 0; i < stepped; ++i) {
+      stage(*solvers[i], stages[i]);
+      envs[i] = stages[i].env;
+    }
+    int gpu = 0;
+    hip(hipGetDevice(&gpu), "hipGetDevice");
+    if (int code = duck_sequential_step(envs.data(), stepped, 1, gpu))
+      throw std::runtime_error(duck_last_error());
+    for (int i = 0; i < stepped; ++i) {
+      stages[i].env = envs[i];
+      unstage(stages[i], *solvers[i]);
+      if (envs[i].status != DUCK_SEQ_OK)
+        throwFault(envs[i].status);
+    }
+  }
+  if (rejected)
+    std::rethrow_exception(rejected);
+}
+
+} // namespace
+
 void Solver::step() {
+  Solver *self = this;
+  stepSolvers(&self, 1);
+}
+
+void stepAll(std::vector<Solver> &environments) {
+  std::vector<Solver *> all(environments.size());
+  for (size_t i = 0; i < environments.size(); ++i)
+    all[i] = &environments[i];
+  stepSolvers(all.data(), int(all.size()));
+}
+
+void Solver::stepImplicit() {
   const Options defaults;
   if (options.alpha != defaults.alpha || options.gamma != defaults.gamma ||
       options.betaLinear != defaults.betaLinear || options.betaAngular != defaults.betaAngular ||

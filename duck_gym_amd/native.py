@@ -40,6 +40,7 @@ def library():
             "duck_fp_bits": (ip, [vp]),
             "duck_state_bytes": (ctypes.c_longlong, [vp]),
             "duck_kernel_info": (ip, [vp, ip, ctypes.POINTER(ctypes.c_longlong)]),
+            "duck_sequential_step": (ip, [vp, ip, ip, ip]),
             "duck_joint_name": (cp, [vp, ip]),
             "duck_reset": (ip, [vp, vp, vp, vp, vp, vp]),
             "duck_step": (ip, [vp, vp, vp, ip, dbl, dbl, vp]),
@@ -81,6 +82,7 @@ EXPORTED = (
     "duck_export_state",
     "duck_import_state", "duck_last_error", "duck_task_obs_dim", "duck_task_targets",
     "duck_task_step", "duck_task_observe", "duck_servo", "duck_servo_substep",
+    "duck_sequential_step",
 )
 
 MAX_JOINTS = 32

@@ -3,26 +3,31 @@
 //
 // A Solver holds one environment's model and state in its public members, as
 // the reference's does; callers may read and change them between steps.
-// step() runs one physics step of that state on the MI355X with the batched
-// HIP step of libduck_hip.so (float64, one environment): the public state is
-// written into a one-environment device batch, advanced once with the
-// per-hinge controls it holds (target, kp, maxTorque, torque, frictionloss,
-// damping) and the root body's force, and read back.  The step has the
-// semantics of the reference's CUDA batch (src/cuda/kernel.cuh: the PD drive
-// stamped implicitly into each body's Hessian, graph-coloured block descent,
-// body-body contacts) rather than src/solver.cpp's explicit PD torque and
-// body-order sweeps; on the MicroDuck biped at kp = 8 and dt = 5 ms the
-// latter diverges.  Consequences for callers of the reference:
-//  * Body::force is applied to the root body (body 1) only; step() throws
+// step() is the reference's Solver::step (src/solver.cpp:315-537): the PD
+// drive as an explicit torque in the predictor, block Gauss-Seidel over the
+// bodies in index order, ground contacts, the warm-start fields angle0 /
+// velocity0 / c0 kept on the hinges and every Diagnostics field.  It runs on
+// the MI355X through duck_sequential_step (libduck_hip.so, one GPU thread per
+// environment, float64): the public state goes to the device, is stepped and
+// comes back, and the same errors are thrown as std::runtime_error ("Body
+// contacts require the shared CpuBatch/CUDA solver", "Invalid solver
+// options", "Non-positive local Hessian", "Non-finite state", "Zero
+// quaternion").  Batch::step steps all its environments in one launch.
+//
+// stepImplicit() is the reference's CUDA batch step instead (src/cuda/
+// kernel.cuh: the PD drive stamped implicitly into each body's Hessian,
+// graph-coloured block descent, body-body contacts), which stays stable where
+// the explicit drive diverges (the MicroDuck biped at kp = 8 and dt = 5 ms):
+//  * Body::force is applied to the root body (body 1) only; it throws
 //    std::invalid_argument for a non-zero force on any other body;
 //  * Options::alpha, gamma, betaLinear, betaAngular and tolerance keep their
-//    defaults (0.9, 0.99, 1e7, 1e5, 1e-7): step() throws for other values;
+//    defaults (0.9, 0.99, 1e7, 1e5, 1e-7): it throws for other values;
 //  * Diagnostics::update is not computed (0); Joint::angle0, velocity0 and
 //    c0 are not written back; contacts are the ground contacts (body-body
 //    contacts of two-way pairs are kept internally between steps).
 // load() parses a `.duck` file with Solver::load's checks (solver.cpp:67-174,
-// std::runtime_error); the first step() also applies the batch's flattening
-// checks (model.hpp: std::invalid_argument), e.g. at most 32 bodies.
+// std::runtime_error); the first stepImplicit() also applies the batch's
+// flattening checks (model.hpp: std::invalid_argument), e.g. at most 32 bodies.
 #pragma once
 #include "math.hpp"
 
@@ -100,6 +105,8 @@ public:
 
   void load(const std::string &path);
   void step();
+  // One step with the reference's CUDA-batch semantics (see above).
+  void stepImplicit();
   void reset();
   // Hinge angle of b relative to a about the axis (solver.cpp:181-187).
   double angle(const Joint &j) const;
@@ -116,6 +123,12 @@ private:
   std::vector<unsigned char> bodyContacts; // body-body contacts between steps
 };
 
+// Solver::step of every environment in one GPU launch, with the outcome of
+// stepping them one after the other: when an environment throws, those
+// before it have stepped, it is left as its step left it, and those after it
+// are untouched.
+void stepAll(std::vector<Solver> &environments);
+
 // Independent environments copied from a prototype; step() advances each.
 class Batch {
 public:
@@ -125,10 +138,7 @@ public:
       throw std::invalid_argument("num_envs must be positive");
     environments.assign(num_envs, prototype);
   }
-  void step() {
-    for (auto &env : environments)
-      env.step();
-  }
+  void step() { stepAll(environments); }
   void reset(int id) { environments.at(id).reset(); }
 };
 

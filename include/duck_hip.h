@@ -275,6 +275,74 @@ typedef struct DuckServoSubstep {
 int duck_servo_substep(void *handle, const DuckServo *servo, const DuckServoSubstep *io,
                        void *hip_stream);
 
+/* ---- Explicit-sequential step (src/solver.cpp:315-537) ----
+ * The step of the reference's independent float64 solver, duck::Solver::step
+ * (include/duck/solver.hpp:56-80): the PD drive as an explicit torque in the
+ * predictor (solver.cpp:339-347), block Gauss-Seidel over the bodies in index
+ * order (solver.cpp:363), ground contacts only (solver.cpp:216-302), the
+ * hinges' angle0 / velocity0 / c0 kept, and the diagnostics including the
+ * largest block update.  The structs mirror duck::Options, Body, Joint,
+ * Shape, Contact and Diagnostics field for field (vectors as [3], quaternions
+ * as w x y z); duck::Solver::step and duck::Batch::step fill them. */
+typedef struct DuckSeqOptions {
+  double dt, alpha, gamma, beta_linear, beta_angular, tolerance, gravity[3];
+  int iterations, ground;
+} DuckSeqOptions;
+typedef struct DuckSeqBody {
+  double mass, inertia[3], x[3], v[3], w[3], x0[3], xp[3], force[3], q[4], q0[4], qp[4];
+} DuckSeqBody;
+typedef struct DuckSeqJoint {
+  int a, b, limited, reserved;
+  double ra[3], rb[3], axis_a[3], axis_b[3], tangent_a[3], tangent_b[3];
+  double lo, hi, damping, armature, frictionloss, lambda_f, penalty_f, torque, kp, target,
+      max_torque, angle0, velocity0, lambda[7], penalty[7], c0[7];
+} DuckSeqJoint;
+typedef struct DuckSeqShape {
+  int body, type, ground;
+  int first_point, num_points; /* its body-frame candidate points (Shape::localPoints) in
+                                  DuckSeqEnv.points */
+  double center[3], size[3], q[4], friction, bounding_radius;
+} DuckSeqShape;
+typedef struct DuckSeqContact {
+  int body, shape, feature, stick;
+  double local[3], anchor[3], radius, friction, c0, lambda[3], penalty[3];
+} DuckSeqContact;
+typedef struct DuckSeqDiagnostics {
+  double joint_error, axis_error, penetration, update;
+  int contacts, iterations, converged, reserved;
+} DuckSeqDiagnostics;
+enum {
+  DUCK_SEQ_OK = 0,
+  DUCK_SEQ_HESSIAN = 1,    /* "Non-positive local Hessian" (math.hpp:91) */
+  DUCK_SEQ_NONFINITE = 2,  /* "Non-finite state" (solver.cpp:521) */
+  DUCK_SEQ_QUATERNION = 3  /* "Zero quaternion" (math.hpp:53) */
+};
+typedef struct DuckSeqEnv {
+  DuckSeqOptions options;
+  int num_bodies, num_joints, num_shapes, num_points;
+  int num_contacts;     /* in: the contacts of the last step; out: this step's */
+  int contact_capacity; /* entries of `contacts`: at least num_contacts and 4 per shape */
+  DuckSeqBody *bodies;
+  DuckSeqJoint *joints;
+  const DuckSeqShape *shapes;
+  const double *points; /* [num_points][3] */
+  DuckSeqContact *contacts;
+  DuckSeqDiagnostics diagnostics; /* out */
+  int status;                     /* out: DUCK_SEQ_*; the environment stops at a fault */
+} DuckSeqEnv;
+
+/* `steps` steps of each of `num_envs` independent environments (host
+ * structs, updated in place), one GPU thread per environment on `device`;
+ * synchronous.  Argument errors return DUCK_ERR_ARGUMENT and change nothing:
+ * the reference's "Invalid solver options" (solver.cpp:318-320), an index out
+ * of range, a capacity below the step's needs, or more than 2e5 iterations x
+ * steps in one call (a bound on the kernel's running time: one thread runs an
+ * environment's iterations serially).
+ * A numerical fault of one environment is its `status`, where the reference
+ * throws, and leaves that environment as the reference's step leaves it when
+ * it throws. */
+int duck_sequential_step(DuckSeqEnv *envs, int num_envs, int steps, int device);
+
 const char *duck_last_error(void);
 
 #ifdef __cplusplus

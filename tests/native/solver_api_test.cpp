@@ -6,14 +6,24 @@
 //   solver_api_test gpu MODEL     environments of a duck::Batch stepped on the
 //                                 GPU: independence, reset, replay and reload
 //                                 (tests/state_test.cpp's invariants)
-//   solver_api_test trace MODEL N body poses after each of N steps
+//   solver_api_test batch MODEL   Batch::step (one launch) against each
+//                                 environment stepped alone, and its outcome
+//                                 when an environment throws
+//   solver_api_test seqtrace MODEL N DT ITER [CONTROLS]
+//                                 Solver::step (solver.cpp's explicit-
+//                                 sequential step): body states and
+//                                 diagnostics after each of N steps
+//   solver_api_test trace MODEL N body poses after each of N steps of
+//                                 Solver::stepImplicit
 // Prints one line per passed check; exits non-zero on the first failure.
 #include "duck/solver.hpp"
 
 #include <algorithm>
+#include <cmath>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <fstream>
 #include <string>
 
 using namespace duck;
@@ -157,6 +167,7 @@ static int gpu(const char *model) {
   original.options.dt = 0.005;
   original.options.iterations = 10;
   check(original.bodies.size() >= 2 && original.joints.size() >= 1, "model loaded");
+  original.options.dt = 0.001; // the explicit drive is stable at 1 ms
   Batch batch(original, 3);
   batch.environments[1].bodies[1].v.x = 0.1;
   for (int i = 0; i < 50; ++i)
@@ -189,30 +200,188 @@ static int gpu(const char *model) {
     rejected = true;
   }
   check(rejected, "an empty batch is rejected");
-  // options the device step does not run are refused, not ignored
+  // options the implicit step does not run are refused, not ignored
   Solver changed = original;
   changed.options.alpha = 0.5;
   rejected = false;
   try {
-    changed.step();
+    changed.stepImplicit();
   } catch (const std::invalid_argument &) {
     rejected = true;
   }
-  check(rejected, "unsupported options rejected");
+  check(rejected, "options the implicit step does not run are rejected");
+  changed.step();
+  check(changed.diagnostics.iterations > 0, "the sequential step runs other AL constants");
+  changed.options.alpha = 1.5;
+  rejected = false;
+  try {
+    changed.step();
+  } catch (const std::runtime_error &e) {
+    rejected = std::string(e.what()) == "Invalid solver options";
+  }
+  check(rejected, "invalid options rejected as solver.cpp rejects them");
   std::printf("gpu checks passed: %s\n", model);
   return 0;
 }
 
-// One environment stepped STEPS times (dt 5 ms, 10 iterations, the file's
-// controls); prints "step body x y z qw qx qy qz" for every body after every
-// step, full precision.
+// Bitwise equality (a NaN equals its own bits).
+static bool eq(double a, double b) { return std::memcmp(&a, &b, sizeof a) == 0; }
+static bool eq(Vec3 a, Vec3 b) { return eq(a.x, b.x) && eq(a.y, b.y) && eq(a.z, b.z); }
+static bool eq(Quat a, Quat b) { return eq(a.w, b.w) && eq(a.x, b.x) && eq(a.y, b.y) && eq(a.z, b.z); }
+template <size_t N> static bool eq(const std::array<double, N> &a, const std::array<double, N> &b) {
+  for (size_t i = 0; i < N; ++i)
+    if (!eq(a[i], b[i]))
+      return false;
+  return true;
+}
+
+// Every field a step writes, bit for bit.
+static bool same(const Solver &a, const Solver &b) {
+  for (size_t i = 0; i < a.bodies.size(); ++i) {
+    const Body &x = a.bodies[i], &y = b.bodies[i];
+    if (!eq(x.x, y.x) || !eq(x.v, y.v) || !eq(x.w, y.w) || !eq(x.q, y.q) || !eq(x.x0, y.x0) ||
+        !eq(x.xp, y.xp) || !eq(x.q0, y.q0) || !eq(x.qp, y.qp))
+      return false;
+  }
+  for (size_t i = 0; i < a.joints.size(); ++i) {
+    const Joint &x = a.joints[i], &y = b.joints[i];
+    if (!eq(x.lambda, y.lambda) || !eq(x.penalty, y.penalty) || !eq(x.c0, y.c0) ||
+        !eq(x.angle0, y.angle0) || !eq(x.velocity0, y.velocity0) || !eq(x.lambdaF, y.lambdaF) ||
+        !eq(x.penaltyF, y.penaltyF))
+      return false;
+  }
+  if (a.contacts.size() != b.contacts.size())
+    return false;
+  for (size_t i = 0; i < a.contacts.size(); ++i) {
+    const Contact &x = a.contacts[i], &y = b.contacts[i];
+    if (x.body != y.body || x.shape != y.shape || x.feature != y.feature || x.stick != y.stick ||
+        !eq(x.lambda, y.lambda) || !eq(x.penalty, y.penalty) || !eq(x.c0, y.c0) ||
+        !eq(x.local, y.local) || !eq(x.anchor, y.anchor))
+      return false;
+  }
+  const Diagnostics &p = a.diagnostics, &q = b.diagnostics;
+  return eq(p.jointError, q.jointError) && eq(p.axisError, q.axisError) &&
+         eq(p.penetration, q.penetration) && eq(p.update, q.update) && p.contacts == q.contacts &&
+         p.iterations == q.iterations && p.converged == q.converged;
+}
+
+// Batch::step runs every environment in one launch: each ends as it would
+// stepped alone, and when one throws the outcome is that of stepping them in
+// order (the reference's loop): those before it stepped, it left as its step
+// left it, those after it untouched.
+static int batch(const char *model) {
+  Solver proto;
+  proto.load(model);
+  proto.options.dt = 0.001;
+  proto.options.iterations = 10;
+  Batch all(proto, 5);
+  for (int i = 0; i < 5; ++i) {
+    all.environments[i].bodies[1].v.y = 0.02 * i;
+    for (auto &j : all.environments[i].joints)
+      j.target += 0.01 * i;
+  }
+  std::vector<Solver> alone = all.environments;
+  for (int s = 0; s < 20; ++s) {
+    all.step();
+    for (auto &env : alone)
+      env.step();
+  }
+  bool equal = true;
+  for (int i = 0; i < 5; ++i)
+    equal = equal && same(all.environments[i], alone[i]);
+  check(equal, "Batch::step equals each environment stepped alone, bit for bit");
+  check(!same(all.environments[0], all.environments[1]), "the environments differ");
+
+  auto outcome = [&](const char *what, auto &&spoil) {
+    std::vector<Solver> before = all.environments;
+    spoil(all.environments[2]);
+    std::vector<Solver> spoiled = all.environments;
+    std::string message;
+    try {
+      all.step();
+    } catch (const std::runtime_error &e) {
+      message = e.what();
+    }
+    std::vector<Solver> expect = spoiled;
+    std::string expected;
+    for (int i = 0; i < 5; ++i) {
+      try {
+        expect[i].step();
+      } catch (const std::runtime_error &e) {
+        expected = e.what();
+        break;
+      }
+    }
+    bool ok = !message.empty() && message == expected;
+    for (int i = 0; i < 5; ++i)
+      ok = ok && same(all.environments[i], expect[i]);
+    ok = ok && same(all.environments[3], spoiled[3]) && same(all.environments[4], spoiled[4]);
+    std::printf("%s: %s\n", what, message.c_str());
+    check(ok, what);
+    all.environments = before;
+  };
+  outcome("a body-contact pair in environment 2 stops the batch there", [](Solver &s) {
+    s.collisionPairs.push_back(CollisionPair{0, 1, 0.5});
+  });
+  outcome("invalid options in environment 2 stop the batch there",
+          [](Solver &s) { s.options.gamma = 1.0; });
+  outcome("a numerical fault in environment 2 is thrown after it, the rest untouched",
+          [](Solver &s) { s.bodies[1].v.x = std::nan(""); });
+  std::printf("batch checks passed: %s\n", model);
+  return 0;
+}
+
+// Solver::step of one environment: STEPS steps at DT and ITER iterations,
+// with the file's controls or, from CONTROLS, J hinge targets, kp, the torque
+// limit and the root force (x, y, z).  Prints after every step one line per
+// body, "s b x y z qw qx qy qz vx vy vz wx wy wz", and one diagnostics line,
+// "d s jointError axisError penetration update contacts iterations converged".
+static int seqtrace(const char *model, int steps, double dt, int iterations,
+                    const char *controls) {
+  Solver sim;
+  sim.load(model);
+  sim.options.dt = dt;
+  sim.options.iterations = iterations;
+  if (controls) {
+    std::ifstream in(controls);
+    for (auto &j : sim.joints)
+      in >> j.target;
+    double kp = 0, limit = 0;
+    in >> kp >> limit >> sim.bodies.at(1).force.x >> sim.bodies[1].force.y >>
+        sim.bodies[1].force.z;
+    if (!in)
+      throw std::runtime_error("truncated controls file");
+    for (auto &j : sim.joints) {
+      j.kp = kp;
+      j.maxTorque = limit;
+    }
+  }
+  for (int s = 1; s <= steps; ++s) {
+    sim.step();
+    for (size_t b = 0; b < sim.bodies.size(); ++b) {
+      const Body &x = sim.bodies[b];
+      std::printf("%d %zu %.17g %.17g %.17g %.17g %.17g %.17g %.17g %.17g %.17g %.17g %.17g "
+                  "%.17g %.17g\n",
+                  s, b, x.x.x, x.x.y, x.x.z, x.q.w, x.q.x, x.q.y, x.q.z, x.v.x, x.v.y, x.v.z, x.w.x,
+                  x.w.y, x.w.z);
+    }
+    const Diagnostics &d = sim.diagnostics;
+    std::printf("d %d %.17g %.17g %.17g %.17g %d %d %d\n", s, d.jointError, d.axisError,
+                d.penetration, d.update, d.contacts, d.iterations, d.converged ? 1 : 0);
+  }
+  return 0;
+}
+
+// One environment stepped STEPS times with Solver::stepImplicit (dt 5 ms, 10
+// iterations, the file's controls); prints "step body x y z qw qx qy qz" for
+// every body after every step, full precision.
 static int trace(const char *model, int steps) {
   Solver sim;
   sim.load(model);
   sim.options.dt = 0.005;
   sim.options.iterations = 10;
   for (int s = 1; s <= steps; ++s) {
-    sim.step();
+    sim.stepImplicit();
     for (size_t b = 0; b < sim.bodies.size(); ++b) {
       const Body &x = sim.bodies[b];
       std::printf("%d %zu %.17g %.17g %.17g %.17g %.17g %.17g %.17g\n", s, b, x.x.x, x.x.y,
@@ -230,7 +399,13 @@ int main(int argc, char **argv) {
       return gpu(argv[2]);
     if (argc >= 4 && std::strcmp(argv[1], "trace") == 0)
       return trace(argv[2], std::atoi(argv[3]));
-    std::fprintf(stderr, "usage: solver_api_test math | gpu MODEL | trace MODEL STEPS\n");
+    if (argc >= 3 && std::strcmp(argv[1], "batch") == 0)
+      return batch(argv[2]);
+    if (argc >= 6 && std::strcmp(argv[1], "seqtrace") == 0)
+      return seqtrace(argv[2], std::atoi(argv[3]), std::atof(argv[4]), std::atoi(argv[5]),
+                      argc >= 7 ? argv[6] : nullptr);
+    std::fprintf(stderr, "usage: solver_api_test math | gpu MODEL | batch MODEL | trace MODEL "
+                         "STEPS | seqtrace MODEL STEPS DT ITER [CONTROLS]\n");
     return 2;
   } catch (const std::exception &e) {
     std::fprintf(stderr, "FAILED: %s\n", e.what());

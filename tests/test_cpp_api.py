@@ -8,8 +8,17 @@
   environments agree bit for bit, a perturbed one differs, reset restores
   the file state and replays bit for bit, reload clears the multipliers, an
   empty batch is rejected) on the pendulum fixture and the MicroDuck-like
-  biped, and duck::Solver::step -- the CudaBatch step with the controls
-  held in the state -- against the oracle's kernel.cuh step in float64."""
+  biped;
+* duck::Solver::step -- src/solver.cpp's explicit-sequential step, run by
+  duck_sequential_step -- against the reference's own duck_sim trajectories
+  (tests/golden/solver_*.npz: the limp biped, the pendulum, the standing
+  biped with its explicit PD drive at dt 1 ms and 5 ms) at every recorded
+  step, with duck_sim's diagnostics summary, and against the oracle's
+  explicit-sequential mode on random targets, torque limits and root forces;
+* Batch::step (one launch for all environments) against each environment
+  stepped alone, and its outcome when one environment throws;
+* duck::Solver::stepImplicit -- the CudaBatch step with the controls held in
+  the state -- against the oracle's kernel.cuh step in float64."""
 
 import subprocess
 from pathlib import Path
@@ -45,11 +54,181 @@ def test_batch_invariants_on_the_gpu(models, which):
     assert "gpu checks passed" in out.stdout
 
 
+def _seqtrace(model, steps, dt, iterations=10, controls=None):
+    """(states [steps, B, 13], diagnostics [steps, 7]) of Solver::step."""
+    args = ["seqtrace", model, steps, dt, iterations] + ([controls] if controls else [])
+    out = _run(*args, timeout=600)
+    assert out.returncode == 0, out.stdout[-2000:] + out.stderr
+    rows, diag = [], []
+    for line in out.stdout.splitlines():
+        f = line.split()
+        if f[0] == "d":
+            diag.append([float(v) for v in f[2:]])
+        else:
+            rows.append([float(v) for v in f])
+    rows = np.array(rows)
+    nb = int(rows[:, 1].max()) + 1
+    return rows[:, 2:].reshape(steps, nb, 13), np.array(diag)
+
+
+def _golden_model(f, tmp_path):
+    path = tmp_path / "model.duck"
+    path.write_text(str(f["model"]))
+    return path
+
+
 @pytest.mark.gpu
-def test_solver_step_matches_the_oracle(models):
-    """duck::Solver on the biped from its file state with the file's hinge
-    controls (kp 8, HOME targets, uncapped): 40 steps within 1e-9 of the
-    oracle's kernel.cuh step (set_controls, then advance) in float64."""
+@pytest.mark.parametrize("name,steps", [("solver_limp_fp64", 150), ("solver_pendulum_fp64", 400)])
+def test_sequential_step_matches_duck_sim(name, steps, tmp_path):
+    """Solver::step against the reference's duck_sim (src/main.cpp over
+    src/solver.cpp, dt 5 ms, 10 iterations): every body's position,
+    orientation and velocities within 1e-9 at every one of the steps -- the
+    limp biped (kp 0, dry friction, ground contacts) and the pendulum."""
+    f = np.load(GOLDEN / f"{name}.npz")
+    states, diag = _seqtrace(_golden_model(f, tmp_path), steps, 0.005)
+    traj = f["trajectory"]
+    worst = float(np.abs(states[:, 1:] - traj[1:]).max())
+    assert worst < 1e-9, worst
+    assert diag[:, 5].min() >= 1  # iterations ran every step
+    print(f"{name}: worst |Solver::step - duck_sim| over {steps} steps = {worst:.2e}")
+
+
+def _oracle_explicit(model, dt, steps, target=None, force=None, kp=None, limit=None):
+    """The oracle's explicit-sequential mode (bit-exact with duck_sim): body
+    states [steps, B, 13] and (converged, contacts) per step."""
+    from oracle.oracle import EXPLICIT_SEQUENTIAL, Oracle
+
+    o = Oracle(model, dt, 10, True, EXPLICIT_SEQUENTIAL)
+    states, flags = [], []
+    for _ in range(steps):
+        if target is None:
+            o.advance(1)
+        else:
+            o.step(target, force, 1, kp, limit)
+        bodies, _, d = o.snapshot()
+        states.append(bodies)
+        flags.append((d[3], d[2]))
+    return np.array(states), np.array(flags)
+
+
+# Steps through which the device's last-bit differences in sin, cos and atan2
+# stay below 1e-9 on the explicit PD drive (measured: 43 at dt 1 ms); after
+# that solver.cpp's explicit drive amplifies them (its light bodies spin at up
+# to 15 rad/s), on the host as on the device (tests/test_sequential_host.py
+# holds the same code on the host to duck_sim bit for bit).
+EXACT_STEPS = 40
+
+
+@pytest.mark.gpu
+def test_sequential_step_matches_duck_sim_explicit_pd(tmp_path):
+    """The standing biped with solver.cpp's explicit PD drive (kp 8 from the
+    file, HOME targets) at dt 1 ms over duck_sim's 200 steps:
+    * every body state within 1e-9 at duck_sim's checkpoints 1, 2, 3 and 10,
+      and at every step through step 40 against the oracle's explicit mode
+      (bit-exact with duck_sim);
+    * the converged flag and the contact count at every one of the 200 steps
+      equal to the oracle's, and duck_sim's summary: its contact count, mean
+      iterations and unconverged steps exactly, its largest joint error to
+      1e-4 relative;
+    * the checkpoints after the chaotic separation (50-200): positions within
+      0.1 m of duck_sim's (measured 5e-2 m at step 200)."""
+    import json
+
+    f = np.load(GOLDEN / "solver_standing_kp8_dt1ms_fp64.npz")
+    steps = list(f["step"])
+    model = _golden_model(f, tmp_path)
+    states, diag = _seqtrace(model, steps[-1], float(f["dt"]))
+    late = 0.0
+    for i, s in enumerate(steps[1:], 1):
+        err = float(np.abs(states[s - 1, 1:] - f["trajectory"][i]).max())
+        if s <= 10:
+            assert err < 1e-9, (s, err)
+        else:
+            late = max(late, float(np.abs(states[s - 1, 1:, :3] - f["trajectory"][i][:, :3]).max()))
+    assert late < 0.1, late
+    ref, flags = _oracle_explicit(model, float(f["dt"]), steps[-1])
+    exact = float(np.abs(states[:EXACT_STEPS] - ref[:EXACT_STEPS]).max())
+    assert exact < 1e-9, exact
+    np.testing.assert_array_equal(diag[:, 6], flags[:, 0])
+    np.testing.assert_array_equal(diag[:, 4], flags[:, 1])
+    summary = json.loads(str(f["summary"]))
+    # the largest joint error falls in the chaotic part (measured 1.2e-6 relative)
+    np.testing.assert_allclose(diag[:, 0].max(), summary["joint_error_m"], rtol=1e-4)
+    assert int(diag[:, 4].max()) == summary["max_contacts"]
+    assert diag[:, 5].mean() == pytest.approx(summary["mean_iterations"], rel=1e-12)
+    assert int((diag[:, 6] == 0).sum()) == summary["unconverged_steps"]
+    print(f"explicit PD, dt 1 ms: steps 1-{EXACT_STEPS} within {exact:.2e} of the oracle; "
+          f"positions at steps 50-200 within {late:.2e} m of duck_sim")
+
+
+@pytest.mark.gpu
+def test_sequential_step_reproduces_the_explicit_pd_divergence(tmp_path):
+    """At the single-env workload's dt = 5 ms the explicit PD drive diverges
+    (duck_sim: the root tens of metres away, no step converged).  Solver::step
+    follows duck_sim's checkpoints 1, 2 and 3 within 1e-9 (measured 2.7e-12),
+    and, as the motion blows up within the first ten steps and amplifies the
+    device's last-bit differences in sin, cos and atan2, diverges the same
+    way: its root leaves by more than 10 m and none of its 200 steps
+    converges."""
+    import json
+
+    f = np.load(GOLDEN / "solver_standing_kp8_dt5ms_fp64.npz")
+    steps = list(f["step"])
+    states, diag = _seqtrace(_golden_model(f, tmp_path), steps[-1], float(f["dt"]))
+    errors = {s: float(np.abs(states[s - 1, 1:] - f["trajectory"][i]).max())
+              for i, s in enumerate(steps[1:], 1)}
+    print("explicit PD, dt 5 ms, worst difference by checkpoint:",
+          {s: f"{e:.2e}" for s, e in errors.items()})
+    assert max(e for s, e in errors.items() if s <= 3) < 1e-9, errors
+    root = states[:, 1, :3]
+    start = f["trajectory"][0][0, :3]
+    assert np.linalg.norm(root[-1] - start) > 10.0
+    summary = json.loads(str(f["summary"]))
+    assert int((diag[:, 6] == 0).sum()) == summary["unconverged_steps"] == 200
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("model_name", ["standing", "friction"])
+def test_sequential_step_matches_oracle_on_random_controls(models, home, model_name, tmp_path):
+    """Solver::step with random hinge targets (HOME + U(-0.3, 0.3)), kp 8, a
+    0.4 N m torque limit and a root force, at dt 1 ms, against the oracle's
+    explicit-sequential mode (bit-exact with duck_sim) with the same controls:
+    every body state within 1e-9 at every step through step 20 (the torque
+    limit and the random targets make the motion more violent than at HOME,
+    so the device's last-bit differences grow faster: 1.4e-9 by step 40 on
+    the standing model), and the converged flag and contact count at every
+    step through 100."""
+    rng = np.random.default_rng(77 if model_name == "standing" else 78)
+    target = home + rng.uniform(-0.3, 0.3, 14)
+    force = np.array([0.05, -0.03, 0.1])
+    controls = tmp_path / "controls.txt"
+    controls.write_text(" ".join(repr(float(v)) for v in (*target, 8.0, 0.4, *force)))
+    steps = 100
+    states, diag = _seqtrace(models[model_name], steps, 0.001, 10, controls)
+    ref, flags = _oracle_explicit(models[model_name], 0.001, steps, target, force, 8.0, 0.4)
+    errors = np.abs(states - ref).max(axis=(1, 2))
+    assert errors[:20].max() < 1e-9, errors[:20].max()
+    np.testing.assert_array_equal(diag[:, 6], flags[:, 0])
+    np.testing.assert_array_equal(diag[:, 4], flags[:, 1])
+    beyond = np.nonzero(errors > 1e-9)[0]
+    print(f"{model_name}: steps 1-20 within {errors[:20].max():.2e} of the oracle; first step "
+          f"beyond 1e-9: {beyond[0] + 1 if beyond.size else None}; step {steps}: {errors[-1]:.2e}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("which", ["pendulum", "standing"])
+def test_batch_steps_in_one_launch_with_the_reference_outcome(models, which):
+    model = GOLDEN / "pendulum.duck" if which == "pendulum" else models["standing"]
+    out = _run("batch", model)
+    assert out.returncode == 0, out.stdout + out.stderr
+    assert "batch checks passed" in out.stdout
+
+
+@pytest.mark.gpu
+def test_solver_step_implicit_matches_the_oracle(models):
+    """duck::Solver::stepImplicit on the biped from its file state with the
+    file's hinge controls (kp 8, HOME targets, uncapped): 40 steps within 1e-9
+    of the oracle's kernel.cuh step (set_controls, then advance) in float64."""
     from oracle.oracle import Oracle
 
     model = models["standing"]
