@@ -1,7 +1,8 @@
 """Checks on the gfx950 machine code of the built library.
 
-`exec_zero_writes` finds vector instructions placed where the exec mask is
-zero.  A loop that lanes leave after different trip counts ends with
+`scalar_writes` finds writes through the scalar data cache, which the
+library must not contain.  `exec_zero_writes` finds vector instructions
+placed where the exec mask is zero.  A loop that lanes leave after different trip counts ends with
 `s_cbranch_execnz` falling through once exec is zero, into a block that then
 restores exec; an instruction the compiler places in that block before the
 restore writes no lane.  ROCm 7.2's compiler has placed the copy of a
@@ -121,9 +122,27 @@ def exec_zero_writes(text: str):
     return found
 
 
+# Writes through the scalar data cache (scalar memory stores and atomics, its
+# write-back and discard): the library must contain none.
+_SCALAR_WRITES = re.compile(r"^\s+(s_store_\w+|s_buffer_store_\w+|s_scratch_store_\w+|"
+                            r"s_atomic_\w+|s_buffer_atomic_\w+|s_dcache_wb\w*|"
+                            r"s_dcache_discard\w*)\b", re.M)
+
+
+def scalar_writes(text: str):
+    """Every scalar-cache write instruction in a disassembly listing."""
+    return [m.group(1) for m in _SCALAR_WRITES.finditer(text)]
+
+
 def check(library: Path, arch: str = "gfx950") -> None:
-    """Raise if the library's code writes vector registers with exec zero."""
-    found = exec_zero_writes(disassemble(library, arch))
+    """Raise if the library's code writes vector registers with exec zero, or
+    writes through the scalar data cache."""
+    text = disassemble(library, arch)
+    scalar = scalar_writes(text)
+    if scalar:
+        raise RuntimeError(f"{library}: {len(scalar)} scalar-cache write instruction(s): "
+                           f"{sorted(set(scalar))}")
+    found = exec_zero_writes(text)
     if found:
         lines = "\n".join(f"  {f} +{a:#x}: {i}" for f, a, i in found[:20])
         raise RuntimeError(f"{library}: {len(found)} vector instruction(s) placed where exec "

@@ -95,3 +95,11 @@ def test_scalar_adds_to_non_sgpr_destinations_are_skipped():
                        "s_setpc_b64 s[0:1]", "s_endpgm"])
     # s_getpc at 0x1014 yields 0x1018; -8 lands on the v_cndmask at 0x1010
     assert C.exec_zero_writes(far) == []
+
+
+def test_scalar_cache_writes_are_found():
+    text = _asm(["s_load_dwordx2 s[0:1], s[4:5], 0x0", "s_store_dword s2, s[0:1], 0x10",
+                 "s_atomic_add s3, s[0:1], 0x0", "s_dcache_wb", "global_store_dword v0, v1, s[0:1]",
+                 "s_endpgm"])
+    assert C.scalar_writes(text) == ["s_store_dword", "s_atomic_add", "s_dcache_wb"]
+    assert C.scalar_writes(_asm(LOOP + ["s_endpgm"])) == []
