@@ -113,12 +113,165 @@ __global__ void servoKernel(DuckServo p, const DeviceModel<R> *model, unsigned c
     static_cast<R *>(io.supply)[e] = supply;
 }
 
+// rneaLoadsIn split over an environment's L lanes, for a model whose hinges
+// form a tree listed parent first (M.jointLevels > 0): the outward pass one
+// tree level at a time (a hinge reads only its parent body, final after the
+// level before), the per-body forces and the contact sums one body per lane
+// (a body's contacts in list order, ground then body contacts), the inward
+// pass from the deepest level: each hinge of the level writes its loads, then
+// each parent adds its children's terms in decreasing hinge order.  Every
+// quantity is formed by the operations of rneaLoadsIn in its order, so the
+// loads are bitwise those of the sequential pass.  Every lane of the
+// workgroup calls it (barriers); `valid` lanes work.
+template <class R, int B, int J, int CG, int CS, int L>
+__device__ __forceinline__ void rneaLoadsLanes(const DeviceModel<R> &M,
+                                               const EnvState<R, B, J, CG, CS> &s, const R *off,
+                                               R *o, RneaWork<R, B> &work, int lane, bool valid) {
+  constexpr int BPL = (B + L - 1) / L, JPL = (J + L - 1) / L;
+  StateView<R, B, J, CG, CS> v{M, const_cast<EnvState<R, B, J, CG, CS> &>(s)};
+  V3<R> *acc = work.acc, *alpha = work.alpha, *force = work.force, *moment = work.moment,
+        *contact = work.contact, *contactMoment = work.contactMoment;
+  const int nb = M.nb, nj = M.nj, levels = M.jointLevels;
+  // the lane's hinges and bodies: level, ends, child hinges (read once); a
+  // hinge's world axis and child arm, formed in the outward pass, serve the
+  // inward pass too (the poses do not move in between); its actuator column
+  // needs no tree quantity and is written first
+  int jLevel[JPL], jA[JPL], jB[JPL], bLevel[BPL];
+  unsigned children[BPL];
+  V3<R> jAxis[JPL], jRb[JPL];
+#pragma unroll
+  for (int r = 0; r < JPL; ++r) {
+    const int j = lane + r * L;
+    const bool in = valid && j < nj;
+    jLevel[r] = in ? M.jointLevel[j] : -1;
+    jA[r] = in ? M.ja[j] : 0;
+    jB[r] = in ? M.jb[j] : 0;
+    jAxis[r] = jRb[r] = V3<R>{0, 0, 0};
+    if (in) {
+      R motor = s.torque[j] - s.kp[j] * wrapAngle(v.angle(j) - s.target[j]);
+      o[3 * j + 2] = s.maxTorque[j] > 0 ? clampv(motor, -s.maxTorque[j], s.maxTorque[j]) : motor;
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < BPL; ++r) {
+    const int b = lane + r * L;
+    const bool in = valid && b < nb;
+    bLevel[r] = in ? M.bodyLevel[b] : -1;
+    children[r] = in ? M.childHinges[b] : 0u;
+    if (in)
+      acc[b] = alpha[b] = force[b] = moment[b] = contact[b] = contactMoment[b] = V3<R>{0, 0, 0};
+  }
+  __syncthreads();
+  if (valid && lane == 0)
+    acc[1] = cross(v.W(1), cross(v.W(1), rotate(v.Q(1), V3<R>{off[0], off[1], off[2]})));
+  __syncthreads();
+  for (int level = 1; level <= levels; ++level) {
+#pragma unroll
+    for (int r = 0; r < JPL; ++r) {
+      const int j = lane + r * L;
+      if (jLevel[r] != level)
+        continue;
+      const int a = jA[r], b = jB[r];
+      Q4<R> qa = v.Q(a), qb = v.Q(b);
+      V3<R> axis = rotate(qa, v.mv(M.axisA, j)), ra = rotate(qa, v.mv(M.ra, j)),
+            rb = rotate(qb, v.mv(M.rb, j));
+      V3<R> wa = v.W(a), wb = v.W(b);
+      R speed = dot(wb - wa, axis);
+      alpha[b] = alpha[a] + cross(wa, axis) * speed;
+      acc[b] = (((acc[a] + cross(alpha[a], ra)) + cross(wa, cross(wa, ra))) - cross(alpha[b], rb)) -
+               cross(wb, cross(wb, rb));
+      jAxis[r] = axis;
+      jRb[r] = rb;
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int r = 0; r < BPL; ++r) {
+    const int b = lane + r * L;
+    if (!valid || b < 1 || b >= nb)
+      continue;
+    Q4<R> q = v.Q(b);
+    V3<R> I{s.inertia[0][b], s.inertia[1][b], s.inertia[2][b]}, w = v.W(b);
+    auto inertia = [&](V3<R> u) {
+      V3<R> l = rotate(conj(q), u);
+      l.x *= I.x;
+      l.y *= I.y;
+      l.z *= I.z;
+      return rotate(q, l);
+    };
+    force[b] = (acc[b] - V3<R>{M.gravity[0], M.gravity[1], M.gravity[2]}) * s.mass[b];
+    moment[b] = inertia(alpha[b]) + cross(w, inertia(w));
+    V3<R> sum{0, 0, 0}, sumMoment{0, 0, 0};
+    for (int i = 0; i < s.ngc; ++i) {
+      const auto &c = s.gc[i];
+      if (gcBody(c.id) != b)
+        continue;
+      V3<R> f = -((V3<R>{1, 0, 0} * c.lambda[0] + V3<R>{0, 1, 0} * c.lambda[1]) +
+                  V3<R>{0, 0, 1} * c.lambda[2]);
+      sum = sum + f;
+      sumMoment = sumMoment + cross(rotate(q, V3<R>{c.local[0], c.local[1], c.local[2]}), f);
+    }
+    for (int i = 0; i < s.nsc; ++i) {
+      const auto &c = s.sc[i];
+      const int ca = scBody(c.id), cb = scOther(c.id);
+      if (ca != b && cb != b)
+        continue;
+      V3<R> f = -selfForceWorld(c);
+      if (ca == b) {
+        sum = sum + f;
+        sumMoment = sumMoment + cross(rotate(q, V3<R>{c.local[0], c.local[1], c.local[2]}), f);
+      }
+      if (cb == b) {
+        sum = sum + (-f);
+        sumMoment = sumMoment + cross(rotate(q, V3<R>{c.localB[0], c.localB[1], c.localB[2]}), -f);
+      }
+    }
+    contact[b] = sum;
+    contactMoment[b] = sumMoment;
+  }
+  __syncthreads();
+  for (int level = levels; level >= 1; --level) {
+#pragma unroll
+    for (int r = 0; r < JPL; ++r) {
+      const int k = lane + r * L;
+      if (jLevel[r] != level)
+        continue;
+      const int b = jB[r];
+      const V3<R> axis = jAxis[r], rb = jRb[r];
+      o[3 * k] = dot(axis, moment[b] - cross(rb, force[b]));
+      o[3 * k + 1] = dot(axis, contactMoment[b] - cross(rb, contact[b])) +
+                     (M.limited[k] ? -s.lambda[5][k] + s.lambda[6][k] : R(0));
+    }
+    if (level == 1)
+      break; // the roots' sums feed no hinge
+#pragma unroll
+    for (int r = 0; r < BPL; ++r) {
+      const int p = lane + r * L;
+      if (bLevel[r] != level - 1)
+        continue;
+      // the body's child hinges in decreasing order, as the sequential pass
+      for (unsigned m = children[r]; m; m &= ~(1u << (31 - __builtin_clz(m)))) {
+        const int k = 31 - __builtin_clz(m);
+        const int b = M.jb[k];
+        V3<R> shift = v.X(b) - v.X(p);
+        moment[p] = moment[p] + (moment[b] + cross(shift, force[b]));
+        force[p] = force[p] + force[b];
+        contactMoment[p] = contactMoment[p] + (contactMoment[b] + cross(shift, contact[b]));
+        contact[p] = contact[p] + contact[b];
+      }
+    }
+    __syncthreads();
+  }
+}
+
 // The servo substep inside the step launch (servoStepKernel): the operations
 // of servoKernel on the state the launch staged in LDS, before the motor
-// step.  Lanes take hinges; the environment's first lane runs the load pass
-// (its per-body quantities in the step's per-step scratch, which the step
-// fills later) and the supply sum, in servoKernel's order.  The channels go
-// into `ctl`, where the motor step takes them.
+// step.  Lanes take hinges; the environment's lanes run the load pass one
+// tree level at a time (rneaLoadsLanes; for a model whose hinges are no tree
+// listed parent first, the first lane runs it in hinge order), with its
+// per-body quantities in the step's per-step scratch, which the step fills
+// later; the first lane sums the supply in servoKernel's order.  The channels
+// go into `ctl`, where the motor step takes them.
 template <class R, int B, int J, int CG, int CS, int L, int JPL, class Env>
 __device__ __forceinline__ void servoPrologue(const ServoArgs<R> &sv, const DeviceModel<R> &M, Env &E,
                                               int e, int lane, bool valid, int count,
@@ -147,9 +300,15 @@ __device__ __forceinline__ void servoPrologue(const ServoArgs<R> &sv, const Devi
           sv.history[size_t(k) * plane + row + j] = t;
       delayed[r] = sv.history[size_t(delayedSlot) * plane + row + j];
     }
+  }
+  auto &work = *reinterpret_cast<RneaWork<R, B> *>(&E.x0[0][0]);
+  if (M.jointLevels > 0)
+    rneaLoadsLanes<R, B, J, CG, CS, L>(M, E.s, sv.rootOffset + size_t(e) * 3, loads, work, lane,
+                                       valid);
+  if (valid) {
     if (lane == 0) {
-      rneaLoadsIn<R, B, J, CG, CS>(M, E.s, sv.rootOffset + size_t(e) * 3, loads,
-                                   *reinterpret_cast<RneaWork<R, B> *>(&E.x0[0][0]));
+      if (M.jointLevels == 0)
+        rneaLoadsIn<R, B, J, CG, CS>(M, E.s, sv.rootOffset + size_t(e) * 3, loads, work);
       R total = 0;
       for (int j = 0; j < nj; ++j)
         total += mabs(sv.previousMotor[row + j]);

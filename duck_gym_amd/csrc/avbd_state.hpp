@@ -60,6 +60,12 @@ template <class R> struct DeviceModel {
   // body-contact pairs (shape indices)
   int pa[kMaxModelPairs], pb[kMaxModelPairs];
   R pfriction[kMaxModelPairs];
+  // tree levels of the Newton-Euler load pass: a hinge's level is the depth
+  // of its child body (a body that is no hinge's child has depth 0);
+  // jointLevels = the deepest level, or 0 when the hinges do not form a tree
+  // listed parent first (the pass then runs in hinge order on one lane)
+  int jointLevel[kMaxModelJoints], bodyLevel[kMaxModelBodies], jointLevels;
+  unsigned childHinges[kMaxModelBodies]; // bit j: hinge j has this body as parent
 };
 
 // Joint model used inside the solve, staged in LDS once per workgroup.

@@ -203,6 +203,31 @@ template <class R> DeviceModel<R> pack(const HostModel &h, double dt, int iterat
     m.pb[p] = h.pairs[p].b;
     m.pfriction[p] = R(h.pairs[p].friction);
   }
+  // Levels of the Newton-Euler tree: each body a child of at most one hinge,
+  // and no body used as a parent before the hinge that makes it a child.
+  {
+    std::vector<int> parentOf(m.nb, -1);
+    std::vector<char> usedAsParent(m.nb, 0);
+    bool tree = true;
+    int deepest = 0;
+    static_assert(kMaxModelJoints <= 32, "a body's child hinges fit one word");
+    for (int b = 0; b < m.nb; ++b) {
+      m.bodyLevel[b] = 0;
+      m.childHinges[b] = 0;
+    }
+    for (int j = 0; j < m.nj; ++j) {
+      const int a = m.ja[j], b = m.jb[j];
+      m.childHinges[a] |= 1u << j;
+      if (parentOf[b] >= 0 || usedAsParent[b])
+        tree = false;
+      parentOf[b] = j;
+      usedAsParent[a] = 1;
+      m.bodyLevel[b] = m.bodyLevel[a] + 1;
+      m.jointLevel[j] = m.bodyLevel[b];
+      deepest = std::max(deepest, m.bodyLevel[b]);
+    }
+    m.jointLevels = tree ? deepest : 0;
+  }
   return m;
 }
 

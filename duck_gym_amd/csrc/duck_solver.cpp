@@ -532,7 +532,7 @@ void stepSolvers(Solver *const *solvers, int n) {
     }
     int gpu = 0;
     hip(hipGetDevice(&gpu), "hipGetDevice");
-    if (int code = duck_sequential_step(envs.data(), stepped, 1, gpu))
+    if (duck_sequential_step(envs.data(), stepped, 1, gpu) != DUCK_OK)
       throw std::runtime_error(duck_last_error());
     for (int i = 0; i < stepped; ++i) {
       stages[i].env = envs[i];
