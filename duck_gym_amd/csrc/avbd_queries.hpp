@@ -225,6 +225,29 @@ template <class R> DUCK_HD V3<R> selfForceWorld(const SelfContact<R> &c) {
          (V3<R>{c.n[0], c.n[1], c.n[2]} * c.lambda[2]);
 }
 
+// The z component of contactForcesKernel's row for body b (ground and body
+// contacts): the same terms summed in the same order.
+template <class R, int B, int J, int CG, int CS>
+DUCK_HD R contactForceZ(const EnvState<R, B, J, CG, CS> &s, int b) {
+  R z = 0;
+  for (int i = 0; i < s.ngc; ++i) {
+    const auto &c = s.gc[i];
+    const V3<R> f = -((V3<R>{1, 0, 0} * c.lambda[0] + V3<R>{0, 1, 0} * c.lambda[1]) +
+                      V3<R>{0, 0, 1} * c.lambda[2]);
+    if (gcBody(c.id) == b)
+      z += f.z;
+  }
+  for (int i = 0; i < s.nsc; ++i) {
+    const auto &c = s.sc[i];
+    const V3<R> f = -selfForceWorld(c);
+    if (scBody(c.id) == b)
+      z += f.z;
+    if (scOther(c.id) == b)
+      z -= f.z;
+  }
+  return z;
+}
+
 // [E,B,3] contact force on each body (kernel.cuh:467-480).
 template <class R, int B, int J, int CG, int CS>
 __global__ void contactForcesKernel(const DeviceModel<R> *model, unsigned char *states,

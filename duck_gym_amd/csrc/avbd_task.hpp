@@ -14,6 +14,8 @@ enum TaskMode { kTaskStep = 0, kTaskReset = 1 };
 
 DUCK_HD float mexp(float x) { return expf(x); }
 DUCK_HD double mexp(double x) { return exp(x); }
+DUCK_HD float tsin(float x) { return sinf(x); }
+DUCK_HD double tsin(double x) { return sin(x); }
 
 // Observation widths (tensor_env.py:238-258 and the 48-wide rollout layout).
 DUCK_HD int taskObsDim(const DuckTask &t, int nj) {
@@ -24,11 +26,43 @@ DUCK_HD int taskObsDim(const DuckTask &t, int nj) {
   return 6 + 3 * nj;
 }
 
+// The gait reference of hinge j (tensor_env.py:263-277): the episode's
+// phase picks two neighbouring rows of the table of the command's direction
+// (the first of the largest of +x, -x, +y, -y) and blends them linearly;
+// HOME blends into that over the first second.  The operations and their
+// order are torch's, in the batch dtype.
+template <class R>
+DUCK_HD R gaitReference(const DuckTask &t, long long episode, const R *cmd, int j, int nj) {
+  const R *table = static_cast<const R *>(t.gait_table);
+  const int count = t.gait_phases;
+  const R ep = R(episode);
+  const R phase = ep * R(t.control_dt) / R(t.gait_period);
+  // torch.remainder of a non-negative phase by 1 is fmod; index < count
+  // (the clamp only guards the table)
+  const R index = fmod(phase, R(1)) * R(count);
+  long long lo = static_cast<long long>(index);
+  lo = lo < 0 ? 0 : (lo >= count ? count - 1 : lo);
+  const R fraction = index - R(lo);
+  const R score[4] = {cmd[0], -cmd[0], cmd[1], -cmd[1]};
+  int d = 0;
+  for (int k = 1; k < 4; ++k)
+    d = score[k] > score[d] ? k : d;
+  const R a = table[(size_t(d) * count + lo) * nj + j];
+  const R b = table[(size_t(d) * count + (lo + 1) % count) * nj + j];
+  const R ref = a * (R(1) - fraction) + b * fraction;
+  R blend = ep * R(t.control_dt);
+  blend = blend < R(0) ? R(0) : (blend > R(1) ? R(1) : blend);
+  const R home = R(t.home[j]);
+  return home + (ref - home) * blend;
+}
+
 // a = clamp(actions, -1, 1); target = clamp(ref + scale a, lower, upper)
-// with ref = HOME when `reference` is null (tensor_env.py:260-277, 279-285).
+// with ref = `reference`, else the gait reference (t.gait), else HOME
+// (tensor_env.py:263-283).
 template <class R>
 __global__ void taskTargetsKernel(DuckTask t, int count, int nj, const R *actions,
-                                  const R *reference, R *clamped, R *target) {
+                                  const R *reference, const long long *episode, const R *commands,
+                                  R *clamped, R *target) {
   int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= count * nj)
     return;
@@ -36,7 +70,10 @@ __global__ void taskTargetsKernel(DuckTask t, int count, int nj, const R *action
   R a = actions[i];
   // torch.clamp propagates NaN; so do these comparisons (NaN fails both).
   a = a < R(-1) ? R(-1) : (a > R(1) ? R(1) : a);
-  R ref = reference ? reference[i] : R(t.home[j]);
+  const int e = i / nj;
+  R ref = reference ? reference[i]
+                    : (t.gait ? gaitReference<R>(t, episode[e], commands + size_t(e) * 2, j, nj)
+                              : R(t.home[j]));
   R v = ref + R(t.action_scale) * a;
   R lo = R(t.lower[j]), hi = R(t.upper[j]);
   v = v < lo ? lo : (v > hi ? hi : v);
@@ -151,8 +188,54 @@ __global__ void taskKernel(DuckTask t, int mode, const DeviceModel<R> *model,
                R(t.tracking_weight) * mexp(-error / (sigma * sigma)) - R(0.1) * w2 -
                R(t.heading_weight) * (R(1) - yawC) - R(0.02) * act2 - R(0.03) * dact2;
     }
+    // Gait shaping (tensor_env.py:328-354), at the counter after this step.
+    const long long next = io.episode[e] + 1;
+    if (t.foot_clearance) {
+      // the feet's lowest collision points against a lift that peaks
+      // mid-swing; the phase is float32 (an int64 counter times a float)
+      const R *pts = static_cast<const R *>(t.foot_point);
+      R penalty = 0;
+      for (int f = 0; f < 2; ++f) {
+        const int fb = t.feet[f];
+        const V3<R> p{s.x[0][fb], s.x[1][fb], s.x[2][fb]};
+        const Q4<R> qf = view.Q(fb);
+        // inverse_rotate(q, up) (tensor_env.py:21-23)
+        const V3<R> up{R(0), R(0), R(1)}, u{-qf.x, -qf.y, -qf.z};
+        const V3<R> tt = cross(u, up) * R(2);
+        const V3<R> localUp = (up + tt * qf.w) + cross(u, tt);
+        R lowest = R(0);
+        for (int k = 0; k < t.foot_points; ++k) {
+          const R *v = pts + (size_t(f) * t.foot_points + k) * 3;
+          const R h = (v[0] * localUp.x + v[1] * localUp.y + v[2] * localUp.z) + p.z;
+          lowest = k == 0 || h < lowest ? h : lowest;
+        }
+        float phase = float(next) * float(t.control_dt) / float(t.gait_period) + (f ? 0.5f : 0.0f);
+        phase = fmodf(phase, 1.0f);
+        float swing = (phase - 0.6f) / 0.4f;
+        swing = swing < 0.0f ? 0.0f : (swing > 1.0f ? 1.0f : swing);
+        const float sw = sinf(float(3.14159265358979323846) * swing);
+        const R desired = R(float(t.gait_lift) * (sw * sw));
+        const R gap = (lowest < R(0) ? R(0) : lowest) - desired;
+        penalty += gap * gap;
+      }
+      reward -= R(20000) * penalty;
+    }
+    if (t.load_transfer) {
+      // vertical contact force of each foot, in body weights, against a
+      // sinusoidal left/right split
+      const R cycle = (R(io.episode[e]) + R(1)) * R(t.control_dt) / R(t.gait_period);
+      const R left = R(0.5) + R(0.5) * tsin(R(2 * 3.14159265358979323846) * (cycle - R(0.05)));
+      R penalty = 0;
+      for (int f = 0; f < 2; ++f) {
+        R force = contactForceZ(s, t.feet[f]) / R(t.weight);
+        force = force < R(0) ? R(0) : (force > R(3) ? R(3) : force);
+        const R d = force - (f ? R(1) - left : left);
+        penalty += d * d;
+      }
+      reward -= R(3) * penalty;
+    }
     reward = (failed ? R(-2) : reward) * R(t.control_dt);
-    long long ep = io.episode[e] + 1;
+    long long ep = next;
     io.episode[e] = ep;
     io.returns[e] += float(reward);
     timeout = ep >= t.max_episode_length && !failed;

@@ -254,8 +254,8 @@ struct BatchBase {
   virtual void layout(long long *out) const = 0;
   virtual void exportState(void *, hipStream_t) = 0;
   virtual void importState(const void *, hipStream_t) = 0;
-  virtual void taskTargets(const DuckTask &, const void *, const void *, void *, void *,
-                           hipStream_t) = 0;
+  virtual void taskTargets(const DuckTask &, const void *, const void *, const long long *,
+                           const void *, void *, void *, hipStream_t) = 0;
   virtual void task(const DuckTask &, int, const TaskBuffers &, hipStream_t) = 0;
   virtual void servo(const DuckServo &, const ServoBuffers &, hipStream_t) = 0;
   virtual void servoSubstep(const DuckServo &, const DuckServoSubstep &, hipStream_t) = 0;
@@ -525,14 +525,15 @@ public:
     referenceIn(base, reinterpret_cast<R *>(base + blobBytes), target, force, substeps, kp, limit,
                 bodies, joints, diag);
   }
-  void taskTargets(const DuckTask &t, const void *actions, const void *reference, void *clamped,
-                   void *target, hipStream_t s) override {
+  void taskTargets(const DuckTask &t, const void *actions, const void *reference,
+                   const long long *episode, const void *commands, void *clamped, void *target,
+                   hipStream_t s) override {
     DeviceGuard guard(device);
     require(actions && clamped && target, "task targets: null buffer");
     const int nj = host.joints.size();
     taskTargetsKernel<R><<<blocks64(count * nj), 64, 0, s>>>(
-        t, count, nj, static_cast<const R *>(actions), static_cast<const R *>(reference),
-        static_cast<R *>(clamped), static_cast<R *>(target));
+        t, count, nj, static_cast<const R *>(actions), static_cast<const R *>(reference), episode,
+        static_cast<const R *>(commands), static_cast<R *>(clamped), static_cast<R *>(target));
     launched("taskTargetsKernel");
   }
   void task(const DuckTask &t, int mode, const TaskBuffers &io, hipStream_t s) override {
@@ -990,6 +991,17 @@ static void checkTask(BatchBase *b, const DuckTask *t) {
   require(t->kind == DUCK_TASK_STANDING || (std::isfinite(t->tracking_sigma) && t->tracking_sigma > 0),
           "tracking sigma must be positive");
   require(b->host.bodies.size() >= 2, "task needs a root body (body 1)");
+  if (t->gait)
+    require(t->gait_table != nullptr && t->gait_phases >= 1, "gait: table required");
+  if (t->foot_clearance || t->load_transfer) {
+    const int nb = int(b->host.bodies.size());
+    require(t->feet[0] >= 0 && t->feet[0] < nb && t->feet[1] >= 0 && t->feet[1] < nb,
+            "gait shaping: foot body out of range");
+  }
+  if (t->foot_clearance)
+    require(t->foot_point != nullptr && t->foot_points >= 1, "foot clearance: points required");
+  if (t->load_transfer)
+    require(std::isfinite(t->weight) && t->weight > 0, "load transfer: weight must be positive");
 }
 int duck_task_obs_dim(const DuckTask *task, int joints) {
   if (!task || joints < 0 || joints > DUCK_MAX_JOINTS)
@@ -997,11 +1009,15 @@ int duck_task_obs_dim(const DuckTask *task, int joints) {
   return taskObsDim(*task, joints);
 }
 int duck_task_targets(void *handle, const DuckTask *task, const void *actions,
-                      const void *reference, void *clamped, void *target, void *hip_stream) {
+                      const void *reference, const long long *episode, const void *commands,
+                      void *clamped, void *target, void *hip_stream) {
   return guarded([&] {
     auto *b = as(handle);
     checkTask(b, task);
-    b->taskTargets(*task, actions, reference, clamped, target, st(hip_stream));
+    require(reference || !task->gait || (episode && commands),
+            "task targets: the gait reference needs the episode counters and commands");
+    b->taskTargets(*task, actions, reference, episode, commands, clamped, target,
+                   st(hip_stream));
   });
 }
 int duck_task_step(void *handle, const DuckTask *task, const void *action, void *last_action,

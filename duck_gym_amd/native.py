@@ -58,7 +58,7 @@ def library():
             "duck_import_state": (ip, [vp, vp, vp]),
             "duck_last_error": (cp, []),
             "duck_task_obs_dim": (ip, [ctypes.POINTER(DuckTask), ip]),
-            "duck_task_targets": (ip, [vp, ctypes.POINTER(DuckTask), vp, vp, vp, vp, vp]),
+            "duck_task_targets": (ip, [vp, ctypes.POINTER(DuckTask)] + [vp] * 7),
             "duck_task_step": (ip, [vp, ctypes.POINTER(DuckTask)] + [vp] * 13),
             "duck_task_observe": (ip, [vp, ctypes.POINTER(DuckTask)] + [vp] * 9),
             "duck_servo": (ip, [vp, ctypes.POINTER(DuckServo), vp, vp, ip] + [vp] * 7),
@@ -136,6 +136,11 @@ class DuckTask(ctypes.Structure):
         ("tracking_weight", ctypes.c_double), ("heading_weight", ctypes.c_double),
         ("tracking_sigma", ctypes.c_double), ("velocity_alpha", ctypes.c_double),
         ("fall_height", ctypes.c_double), ("max_episode_length", ctypes.c_longlong),
+        ("gait", ctypes.c_int), ("foot_clearance", ctypes.c_int),
+        ("load_transfer", ctypes.c_int), ("gait_phases", ctypes.c_int),
+        ("gait_table", ctypes.c_void_p), ("gait_lift", ctypes.c_double),
+        ("feet", ctypes.c_int * 2), ("foot_points", ctypes.c_int),
+        ("foot_point", ctypes.c_void_p), ("weight", ctypes.c_double),
     ]
 
 
@@ -435,10 +440,14 @@ class CudaBatch:
     def task_obs_dim(self, task):
         return int(library().duck_task_obs_dim(ctypes.byref(task), self.num_joints))
 
-    def task_targets(self, task, actions, reference, clamped, target):
-        """clamped <- clamp(actions, -1, 1); target <- clamp(ref + scale a, lower, upper)."""
+    def task_targets(self, task, actions, reference, clamped, target, episode=None,
+                     commands=None):
+        """clamped <- clamp(actions, -1, 1); target <- clamp(ref + scale a, lower, upper)
+        with ref = `reference`, else (task.gait) the gait reference of `episode`
+        [E] int64 and `commands` [E,2], else HOME."""
         E, J = self.num_envs, self.num_joints
         args = [self._check(actions, [E, J]), self._ptr(reference, [E, J]),
+                self._ptr(episode, [E], torch.int64), self._ptr(commands, [E, 2]),
                 self._check(clamped, [E, J]), self._check(target, [E, J])]
         with torch.cuda.device(self.device):
             code = library().duck_task_targets(self._h, ctypes.byref(task), *args, self._stream())

@@ -14,8 +14,10 @@ bookkeeping (tensor_env.py:178-219, 221-391).  Here the same step is
 
 The random draws (`torch.rand`/`torch.randint` on `self.generator`) are made
 exactly as the reference makes them, so a seed gives the same perturbations.
-Optional gait-table shaping (gait reference, foot clearance, load transfer)
-is computed with torch from the state snapshot, as in the reference.
+The gait-table options (tensor_env.py:151-170, 263-277, 328-354) run in the
+same launches: the gait reference in task_targets, the foot-clearance and
+load-transfer terms in task_step, which adds them to the reward before the
+failure and the control period apply, as the reference does.
 
 Extension: task="rollout" is the 48-wide observation (projected gravity,
 local angular velocity, q - HOME, 0.1 qdot, last action) with the locomotion
@@ -158,6 +160,26 @@ class TensorEnv:
         s.velocity_alpha = float(self.velocity_alpha)
         s.fall_height = float(fall_height)
         s.max_episode_length = int(self.max_episode_length)
+        if self.gait:
+            table = self.gait_table
+            if table.dim() != 3 or table.shape[0] != 4 or table.shape[2] != J:
+                raise ValueError("gait table must be [4, phases, joints]")
+            self.gait_table = table.contiguous()
+            s.gait, s.gait_phases = 1, int(table.shape[1])
+            s.gait_table = self.gait_table.data_ptr()
+        if self.foot_clearance or self.load_transfer:
+            if self.foot_bodies.numel() != 2:
+                raise ValueError("gait shaping needs two foot bodies")
+            s.feet[:] = [int(b) for b in self.foot_bodies.cpu()]
+            s.foot_clearance, s.load_transfer = int(self.foot_clearance), int(self.load_transfer)
+            s.gait_lift = float(self.gait_lift)
+            s.weight = float(self.meta["mass"] * 9.81)
+            points = self.foot_points
+            if points.dim() != 3 or points.shape[0] != 2 or points.shape[2] != 3:
+                raise ValueError("foot points must be [2, points, 3]")
+            self.foot_points = points.contiguous()
+            s.foot_points = int(points.shape[1])
+            s.foot_point = self.foot_points.data_ptr()
         return s
 
     @property
@@ -237,7 +259,9 @@ class TensorEnv:
         return obs, {"observations": {}}
 
     def reference(self):
-        """Servo reference: HOME, or the blended gait table (tensor_env.py:260-277)."""
+        """Servo reference: HOME (None), or the blended gait table in torch
+        (tensor_env.py:263-277); step() forms the same reference inside its
+        targets launch."""
         if not self.gait:
             return None
         phase = self.episode_length_buf.to(self.dtype) * self.control_dt / self.gait_period
@@ -252,41 +276,13 @@ class TensorEnv:
         return (self.home + (ref - self.home) * blend).contiguous()
 
     # ------------------------------------------------------------------- step
-    def _shaping(self, a):
-        """Gait-table reward terms of tensor_env.py:328-357 (torch, optional)."""
-        extra = None
-        if self.foot_clearance or self.load_transfer:
-            b = self.native.state()[0].to(self.dtype)
-            extra = torch.zeros(self.num_envs, device=self.device, dtype=self.dtype)
-        if self.foot_clearance:
-            poses = b[:, self.foot_bodies]
-            up = torch.tensor([0.0, 0, 1.0], device=self.device,
-                              dtype=self.dtype).expand(self.num_envs, 2, -1)
-            local_up = inverse_rotate(poses[:, :, 3:7], up)
-            heights = (local_up[:, :, None, :] * self.foot_points[None]).sum(-1) \
-                + poses[:, :, None, 2]
-            clearance = heights.amin(-1)
-            # The counter was already advanced by task_step: use it as is.
-            phase = (self.episode_length_buf[:, None] * self.control_dt / self.gait_period
-                     + torch.tensor([0.0, 0.5], device=self.device)) % 1
-            swing = ((phase - 0.6) / 0.4).clamp(0, 1)
-            desired = self.gait_lift * torch.sin(torch.pi * swing).square()
-            extra -= 20000 * (clearance.clamp_min(0) - desired).square().sum(-1)
-        if self.load_transfer:
-            forces = self.native.contact_forces()[:, self.foot_bodies, 2].to(self.dtype) / (
-                self.meta["mass"] * 9.81)
-            cycle = self.episode_length_buf.to(self.dtype) * self.control_dt / self.gait_period
-            left = 0.5 + 0.5 * torch.sin(2 * torch.pi * (cycle - 0.05))
-            wanted = torch.stack((left, 1 - left), dim=-1)
-            extra -= 3 * (forces.clamp(0, 3) - wanted).square().sum(-1)
-        return extra
-
     def step(self, actions):
         E, J = self.num_envs, self.num_actions
         raw = actions.to(dtype=self.dtype).contiguous()
         a = torch.empty(E, J, device=self.device, dtype=self.dtype)
         target = torch.empty_like(a)
-        self.native.task_targets(self.spec, raw, self.reference(), a, target)
+        self.native.task_targets(self.spec, raw, None, a, target, self.episode_length_buf,
+                                 self.commands)
         self.native.step(target, self.forces.contiguous(), self.substeps, self.meta["kp"],
                          self.meta["torque_limit"])
         obs = torch.empty(E, self.obs_dim, device=self.device)
@@ -298,11 +294,6 @@ class TensorEnv:
         self.native.task_step(self.spec, a, self.actions, self._commands,
                               self.episode_length_buf, self._filtered, self.returns, obs, reward,
                               failed, timeout, done, diag)
-        extra = self._shaping(a)
-        if extra is not None:
-            extra = torch.where(failed, 0.0, extra) * self.control_dt
-            reward += extra.float()
-            self.returns += extra.float()
         info = {
             "observations": {},
             "time_outs": timeout,

@@ -168,16 +168,31 @@ typedef struct DuckTask {
   double tracking_weight, heading_weight, tracking_sigma, velocity_alpha;
   double fall_height;
   long long max_episode_length;
+  /* Gait-table options (tensor_env.py:151-170, 263-277, 328-354), all zero when off.
+   * gait: the servo reference blends HOME into the table row of the command's
+   * direction (duck_task_targets); foot_clearance / load_transfer: the two
+   * shaping terms of the reward (duck_task_step). */
+  int gait, foot_clearance, load_transfer;
+  int gait_phases;         /* phases per direction in gait_table */
+  const void *gait_table;  /* [4, gait_phases, J] batch dtype, device (gait) */
+  double gait_lift;        /* foot_clearance: the swing foot's lift */
+  int feet[2];             /* the two foot bodies (foot_clearance, load_transfer) */
+  int foot_points;         /* body-frame collision points per foot */
+  const void *foot_point;  /* [2, foot_points, 3] batch dtype, device (foot_clearance) */
+  double weight;           /* load_transfer: metadata mass x 9.81 */
 } DuckTask;
 
 /* Observation width of `task` for a batch with `joints` hinges. */
 int duck_task_obs_dim(const DuckTask *task, int joints);
 
-/* TensorEnv.step head (tensor_env.py:331-335, 260-277): a = clamp(actions,-1,1),
- * target = clamp(ref + action_scale a, lower, upper); ref = HOME when
- * `reference` is NULL (the gait reference otherwise).  [E,J] batch dtype. */
+/* TensorEnv.step head (tensor_env.py:279-283, 263-277): a = clamp(actions,-1,1),
+ * target = clamp(ref + action_scale a, lower, upper).  ref: `reference` [E,J]
+ * when not NULL; else, with task->gait, the gait reference of the episode
+ * counters `episode` [E] int64 and `commands` [E,2]; else HOME.  [E,J] batch
+ * dtype. */
 int duck_task_targets(void *handle, const DuckTask *task, const void *actions,
-                      const void *reference, void *clamped, void *target, void *hip_stream);
+                      const void *reference, const long long *episode, const void *commands,
+                      void *clamped, void *target, void *hip_stream);
 
 /* TensorEnv.step tail after the physics (tensor_env.py:345-391): failure,
  * reward, returns, episode counters, timeouts, done, the observation of the
@@ -185,7 +200,9 @@ int duck_task_targets(void *handle, const DuckTask *task, const void *actions,
  * `last_action` [E,J] holds the previous one and is overwritten with `action`.
  * commands [E,2] (locomotion/rollout, else NULL), episode [E] int64, filtered
  * [E,2] (velocity filter, else NULL), returns/obs/reward float32, failed /
- * timeout / done [E] bytes. */
+ * timeout / done [E] bytes.  With task->foot_clearance / load_transfer the
+ * shaping terms join the reward before the failure and the control period
+ * apply (tensor_env.py:328-355). */
 int duck_task_step(void *handle, const DuckTask *task, const void *action, void *last_action,
                    const void *commands, long long *episode, void *filtered, float *returns,
                    float *obs, float *reward, unsigned char *failed, unsigned char *timeout,

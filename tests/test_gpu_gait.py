@@ -6,10 +6,13 @@ body-frame collision points.
 
 Two environments run in lockstep from the same seed and actions: one with
 the gait reference only, one with the reference and both shaping terms.  The
-applied targets of both equal the oracle's gait reference at the episode
-counters before the step; the difference of their rewards equals the
-oracle's shaping terms evaluated on the GPU state after the step, times the
-control period, wherever the env has not failed."""
+applied targets of both (formed inside the targets launch) equal the
+oracle's gait reference at the episode counters before the step, and equal
+bit for bit the reference's torch expressions on the same tensors; the
+difference of their rewards (the shaping terms join the reward inside the
+task launch, before the control period scales it, as in the reference)
+equals the oracle's shaping terms evaluated on the GPU state after the step,
+times the control period, wherever the env has not failed."""
 
 import json
 
@@ -67,11 +70,17 @@ def test_gait_reference_and_shaping_terms(gait_dir):
         ref = T.gait_reference(episode, commands, table, 0.8, home, dt)
         _, expected = T.targets(actions.cpu().double().numpy(), home, np.array(meta["lower"]),
                                 np.array(meta["upper"]), shaped.action_scale, ref)
+        # the reference's torch expressions of the targets (tensor_env.py:
+        # 263-283) on the same tensors: the targets launch repeats them bit
+        # for bit
+        torch_targets = [(env.reference() + env.action_scale * actions.clamp(-1, 1))
+                         .clamp(env.lower, env.upper) for env in (plain, shaped)]
         _, r1, _, info1 = shaped.step(actions)
         _, r0, _, info0 = plain.step(actions)
-        for info in (info0, info1):
+        for info, want in zip((info0, info1), torch_targets):
             np.testing.assert_allclose(info["applied_targets"].cpu().double().numpy(), expected,
                                        rtol=0, atol=2e-6)
+            assert torch.equal(info["applied_targets"], want), f"step {step}"
         bodies = shaped.native.state()[0].cpu().double().numpy()
         forces = shaped.native.contact_forces()[:, feet, 2].cpu().double().numpy()
         after = shaped.episode_length_buf.cpu().numpy()
