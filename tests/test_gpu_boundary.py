@@ -216,15 +216,27 @@ def test_checkpoint_replay_bit_exact(models, home, fp64):
 
 
 def test_reference_method_matches_fresh_batch(models, home):
-    """`reference()` advances one env from the model file's initial state."""
+    """`reference()` advances one env from the model file's initial state:
+    bit for bit a fresh one-env batch, and within 1e-9 the oracle's CPU batch
+    (CpuBatch64's semantics, oracle.OracleBatch) run from the same file state,
+    the host run the reference's `reference()` makes (extension.cu:385-415)."""
+    from oracle.oracle import OracleBatch
+
     b = _batch(models["standing"], 3, fp64=True)
     target = torch.tensor(home, dtype=torch.float64)
-    rb, rj, rd = b.reference(target, torch.zeros(3, dtype=torch.float64), 4, KP, 0.0)
+    # (a torque limit the CPU batch accepts: it refuses 0)
+    rb, rj, rd = b.reference(target, torch.zeros(3, dtype=torch.float64), 4, KP, 1e9)
     fresh = _batch(models["standing"], 1, fp64=True)  # initialised to the file state
-    fresh.step(target[None].to(DEV), torch.zeros(1, 3, dtype=torch.float64, device=DEV), 4, KP, 0.0)
+    fresh.step(target[None].to(DEV), torch.zeros(1, 3, dtype=torch.float64, device=DEV), 4, KP, 1e9)
     fb, fj, fd = (t[0].cpu() for t in fresh.state())
     torch.testing.assert_close(rb, fb, rtol=0, atol=0)
     torch.testing.assert_close(rj, fj, rtol=0, atol=0)
+    cpu = OracleBatch(models["standing"], 1, DT, ITER, fp64=True)
+    cpu.step(np.asarray(home)[None], np.zeros((1, 3)), 4, KP, 1e9)
+    ob, oj, od = cpu.state()
+    np.testing.assert_allclose(rb.numpy(), ob[0], rtol=0, atol=1e-9)
+    np.testing.assert_allclose(rj.numpy(), oj[0], rtol=0, atol=1e-9)
+    np.testing.assert_allclose(rd.numpy(), od[0], rtol=0, atol=1e-9)
     with pytest.raises(RuntimeError):
         b.reference(target.float(), torch.zeros(3, dtype=torch.float64), 1, KP, 0.0)
 
