@@ -1458,22 +1458,28 @@ __device__ __forceinline__ void stepBody(const StepArgs &args, const ServoArgs<R
       // or ground contacts (three or more: two lanes would need two rounds);
       // that body's group becomes four lanes (both slots, lane and lane ^ 8).
       if (active && twoColourSlots) {
+        // Each slot weighs its own body, and one reduction over the
+        // environment's lanes picks the first of the heaviest (the lanes of
+        // an environment are active together).
+        int bestOf[2];
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
           const int cs = E.colorStart[c], n = E.colorStart[c + 1] - cs;
-          if (n >= L / P || (c == 1 && early))
-            continue;
-          int best = -1, bestUnits = 2;
-          for (int k = 0; k < n; ++k) {
-            const int b = E.order[cs + k];
+          int key = 0;
+          if (slot < n && n < L / P && !(c == 1 && early)) {
+            const int b = E.order[cs + slot];
             const int hinges = F.adjStart[b + 1] - F.adjStart[b];
             const int ground = stp.groundCount(b);
             const int units = hinges > ground ? hinges : ground;
-            if (units > bestUnits) {
-              bestUnits = units;
-              best = k;
-            }
+            key = units > 2 ? (units << 8 | (255 - slot)) : 0;
           }
+          key = groupMax<L>(key);
+          bestOf[c] = key != 0 ? 255 - (key & 255) : -1;
+        }
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          const int cs = E.colorStart[c], n = E.colorStart[c + 1] - cs;
+          const int best = bestOf[c];
           if (best < 0)
             continue;
           // The busy body takes slots 0 and 4 (order within a colour is free:
