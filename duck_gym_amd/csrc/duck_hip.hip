@@ -791,6 +791,37 @@ __global__ __launch_bounds__(64) void sequentialStepKernel(unsigned char *record
     e.step();
 }
 
+// The same with one environment per workgroup and its record staged in LDS
+// (dynamic shared memory of the largest record's size): the workgroup copies
+// the record in, its first thread runs the steps on the LDS copy, and the
+// workgroup copies it back.  Records are whole 256-byte multiples.
+__global__ __launch_bounds__(64) void sequentialStepLdsKernel(unsigned char *records,
+                                                              const long long *offset, int n,
+                                                              long long total, int steps) {
+  extern __shared__ uint4 seqRecord[];
+  const int i = blockIdx.x;
+  const long long begin = offset[i], end = i + 1 < n ? offset[i + 1] : total;
+  const int chunks = int((end - begin) / 16);
+  uint4 *global = reinterpret_cast<uint4 *>(records + begin);
+  for (int k = threadIdx.x; k < chunks; k += 64)
+    seqRecord[k] = global[k];
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    seq::Env e(reinterpret_cast<unsigned char *>(seqRecord));
+    for (int s = 0; s < steps && e.r->status == DUCK_SEQ_OK; ++s)
+      e.step();
+  }
+  __syncthreads();
+  for (int k = threadIdx.x; k < chunks; k += 64)
+    global[k] = seqRecord[k];
+}
+// Records up to this size take the LDS kernel when the batch has at most
+// kSequentialLdsEnvs environments: one environment per workgroup measured
+// 12 % faster per step than the device-memory kernel for one environment,
+// and slower from a few hundred on (where 64 environments share a wave).
+constexpr long long kSequentialLdsBytes = 64 << 10;
+constexpr int kSequentialLdsEnvs = 64;
+
 // The device buffers of one device, reused and grown across calls; calls on
 // one device take turns on them.
 struct SequentialBuffers {
@@ -848,8 +879,17 @@ void sequentialStep(DuckSeqEnv *envs, int n, int steps, int device) {
   hipCheck(hipMemcpy(buf.records, image.data(), total, hipMemcpyHostToDevice), "upload");
   hipCheck(hipMemcpy(buf.offsets, offsets.data(), sizeof(long long) * n, hipMemcpyHostToDevice),
            "upload");
-  sequentialStepKernel<<<(n + 63) / 64, 64, 0, 0>>>(buf.records, buf.offsets, n, steps);
-  hipCheck(hipGetLastError(), "sequentialStepKernel");
+  long long largest = 0;
+  for (int i = 0; i < n; ++i)
+    largest = std::max(largest, (i + 1 < n ? offsets[i + 1] : (long long)total) - offsets[i]);
+  if (largest <= kSequentialLdsBytes && n <= kSequentialLdsEnvs) {
+    sequentialStepLdsKernel<<<n, 64, size_t(largest), 0>>>(buf.records, buf.offsets, n,
+                                                           (long long)total, steps);
+    hipCheck(hipGetLastError(), "sequentialStepLdsKernel");
+  } else {
+    sequentialStepKernel<<<(n + 63) / 64, 64, 0, 0>>>(buf.records, buf.offsets, n, steps);
+    hipCheck(hipGetLastError(), "sequentialStepKernel");
+  }
   hipCheck(hipMemcpy(image.data(), buf.records, total, hipMemcpyDeviceToHost), "download");
   seq::unpackSequential(envs, n, image, offsets);
 }

@@ -15,10 +15,14 @@
 //                                 diagnostics after each of N steps
 //   solver_api_test trace MODEL N body poses after each of N steps of
 //                                 Solver::stepImplicit
+//   solver_api_test throughput MODEL ENVS N DT ITER KP
+//                                 steps/s of Solver::step (one env) and of
+//                                 Batch::step (ENVS envs), N steps each
 // Prints one line per passed check; exits non-zero on the first failure.
 #include "duck/solver.hpp"
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -291,6 +295,22 @@ static int batch(const char *model) {
     equal = equal && same(all.environments[i], alone[i]);
   check(equal, "Batch::step equals each environment stepped alone, bit for bit");
   check(!same(all.environments[0], all.environments[1]), "the environments differ");
+  {
+    // a batch past the LDS-staged kernel's size takes the device-memory
+    // kernel: the same operations, so the same bits
+    Batch big(proto, 80);
+    for (int i = 0; i < 80; ++i) {
+      big.environments[i].bodies[1].v.y = 0.02 * (i % 5);
+      for (auto &j : big.environments[i].joints)
+        j.target += 0.01 * (i % 5);
+    }
+    for (int s = 0; s < 20; ++s)
+      big.step();
+    bool bigEqual = true;
+    for (int i = 0; i < 80; ++i)
+      bigEqual = bigEqual && same(big.environments[i], alone[i % 5]);
+    check(bigEqual, "an 80-environment Batch::step equals the 5-environment one, bit for bit");
+  }
 
   auto outcome = [&](const char *what, auto &&spoil) {
     std::vector<Solver> before = all.environments;
@@ -372,6 +392,49 @@ static int seqtrace(const char *model, int steps, double dt, int iterations,
   return 0;
 }
 
+// Throughput of Solver::step and duck::Batch::step (solver.cpp's step on the
+// GPU): the file's pose held by PD targets at its own hinge angles (gain KP,
+// uncapped), ground on; one environment stepped STEPS times, then a Batch of
+// ENVS copies stepped STEPS times, after two untimed steps each.
+static int throughput(const char *model, int envs, int steps, double dt, int iterations,
+                      double kp) {
+  Solver sim;
+  sim.load(model);
+  sim.options.dt = dt;
+  sim.options.iterations = iterations;
+  sim.options.ground = true;
+  for (auto &j : sim.joints) {
+    j.kp = kp;
+    j.target = sim.angle(j);
+  }
+  using clock = std::chrono::steady_clock;
+  auto seconds = [](clock::time_point a, clock::time_point b) {
+    return std::chrono::duration<double>(b - a).count();
+  };
+  Solver one = sim;
+  one.step();
+  one.step();
+  auto t0 = clock::now();
+  for (int s = 0; s < steps; ++s)
+    one.step();
+  const double single = seconds(t0, clock::now());
+  Batch batch(sim, envs);
+  batch.step();
+  batch.step();
+  t0 = clock::now();
+  for (int s = 0; s < steps; ++s)
+    batch.step();
+  const double many = seconds(t0, clock::now());
+  int failed = 0;
+  for (const Solver &e : batch.environments)
+    failed += std::isfinite(e.bodies.at(1).x.z) ? 0 : 1;
+  std::printf("single env: %.1f steps/s (%.3f ms per step)\n", steps / single,
+              1e3 * single / steps);
+  std::printf("batch of %d: %.1f env-steps/s (%.3f ms per Batch::step), %d non-finite\n", envs,
+              double(envs) * steps / many, 1e3 * many / steps, failed);
+  return failed ? 1 : 0;
+}
+
 // One environment stepped STEPS times with Solver::stepImplicit (dt 5 ms, 10
 // iterations, the file's controls); prints "step body x y z qw qx qy qz" for
 // every body after every step, full precision.
@@ -404,8 +467,12 @@ int main(int argc, char **argv) {
     if (argc >= 6 && std::strcmp(argv[1], "seqtrace") == 0)
       return seqtrace(argv[2], std::atoi(argv[3]), std::atof(argv[4]), std::atoi(argv[5]),
                       argc >= 7 ? argv[6] : nullptr);
+    if (argc >= 8 && std::strcmp(argv[1], "throughput") == 0)
+      return throughput(argv[2], std::atoi(argv[3]), std::atoi(argv[4]), std::atof(argv[5]),
+                        std::atoi(argv[6]), std::atof(argv[7]));
     std::fprintf(stderr, "usage: solver_api_test math | gpu MODEL | batch MODEL | trace MODEL "
-                         "STEPS | seqtrace MODEL STEPS DT ITER [CONTROLS]\n");
+                         "STEPS | seqtrace MODEL STEPS DT ITER [CONTROLS] | throughput MODEL "
+                         "ENVS STEPS DT ITER KP\n");
     return 2;
   } catch (const std::exception &e) {
     std::fprintf(stderr, "FAILED: %s\n", e.what());
