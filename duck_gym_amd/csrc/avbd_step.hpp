@@ -991,13 +991,42 @@ struct Stepper {
     }
     for (int adj = adjNext; adj < adjEnd; adj += nParts)
       hingeRows<true>(H, bi, F.adj[adj], true, implicitDrive, slow);
-    int nth = 0;
+    if constexpr (GW == 1) {
+      // The lane's further contacts (positions p0 + k nParts beyond the
+      // straight-line ones), one per lane per round, the rounds counted by a
+      // ballot: the lanes of a wave stamp their k-th further contact together
+      // (a round without one stamps zeros).  Each lane adds the same contacts
+      // in the same order as a walk over the body's list.
+      uint64_t m = E.gmask[0][bi];
+      if constexpr (Ground) {
+        // the contacts after the lane's second straight-line one, then the
+        // other parts' nParts - 1
+        const int c1 = (sp.w1 >> 8) & 255;
+        m = (sp.w0 >> 26) & 1 ? m & ~((2ull << c1) - 1) : 0ull;
 #pragma unroll
-    for (int w = 0; w < GW; ++w)
-      for (uint64_t g = E.gmask[w][bi]; g; g &= g - 1, ++nth)
-        if ((!Ground || nth >= 2 * nParts) && nth % nParts == p0)
-          groundRows(H, bi, 64 * w + __builtin_ctzll(g), true);
-    nth = 0;
+        for (int k = 0; k < 3; ++k)
+          m = k < nParts - 1 ? m & (m - 1) : m;
+      } else {
+#pragma unroll
+        for (int k = 0; k < 3; ++k)
+          m = k < p0 ? m & (m - 1) : m;
+      }
+      while (__any(m != 0)) {
+        const bool v = m != 0;
+        groundRows(H, bi, v ? __builtin_ctzll(m) : 0, v);
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          m = k < nParts ? m & (m - 1) : m;
+      }
+    } else {
+      int nth = 0;
+#pragma unroll
+      for (int w = 0; w < GW; ++w)
+        for (uint64_t g = E.gmask[w][bi]; g; g &= g - 1, ++nth)
+          if ((!Ground || nth >= 2 * nParts) && nth % nParts == p0)
+            groundRows(H, bi, 64 * w + __builtin_ctzll(g), true);
+    }
+    int nth = 0;
     for (uint32_t g = Pairs ? E.smask[bi] : 0u; g; g &= g - 1, ++nth)
       if (nth % nParts == p0)
         selfRows(H, bi, __builtin_ctz(g));
