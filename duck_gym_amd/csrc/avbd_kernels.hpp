@@ -1526,6 +1526,22 @@ __device__ __forceinline__ void stepBody(const StepArgs &args, const ServoArgs<R
     if (shareEval) {
       dualJoint = active && mine[0] >= 0 && ((plans[0].w0 >> 24) & 1) ? plans[0].w0 & 255 : -1;
       leftover = allJoints & ~uint32_t(groupOr<L>(dualJoint >= 0 ? int(1u << dualJoint) : 0));
+      if constexpr (L == 16) {
+        // The lanes left without a hinge take the leftover ones (the n-th
+        // such lane of the environment the n-th leftover hinge), so that
+        // the straight-line block updates them too; only hinges beyond the
+        // free lanes go round-robin.  A hinge's update does not depend on
+        // the lane that makes it.
+        const uint32_t freeLanes = uint32_t(__ballot(dualJoint < 0) >> (t - lane)) & 0xffffu;
+        const int rank = __popc(freeLanes & ((1u << lane) - 1));
+        uint32_t m = leftover;
+#pragma unroll
+        for (int k = 0; k < L - 1; ++k)
+          m = k < rank ? m & (m - 1) : m;
+        const int take = dualJoint < 0 && m != 0 ? __builtin_ctz(m) : -1;
+        leftover &= ~uint32_t(groupOr<L>(take >= 0 ? int(1u << take) : 0));
+        dualJoint = take >= 0 ? take : dualJoint;
+      }
     }
     // The ends of that hinge and the owner of the lane's first ground
     // contact (the list is fixed until the next detection).
