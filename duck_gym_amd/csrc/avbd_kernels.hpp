@@ -1454,9 +1454,9 @@ __device__ __forceinline__ void stepBody(const StepArgs &args, const ServoArgs<R
       }
     }
     if constexpr (P == 2) {
-      // A colour with a free slot lends it to its body with the most hinges
-      // or ground contacts (three or more: two lanes would need two rounds);
-      // that body's group becomes four lanes (both slots, lane and lane ^ 8).
+      // A colour with a free slot lends it to the body that four lanes
+      // serve best (the most assembly rounds saved, weighed below); that
+      // body's group becomes four lanes (both slots, lane and lane ^ 8).
       if (active && twoColourSlots) {
         // Each slot weighs its own body, and one reduction over the
         // environment's lanes picks the first of the heaviest (the lanes of
@@ -1467,11 +1467,18 @@ __device__ __forceinline__ void stepBody(const StepArgs &args, const ServoArgs<R
           const int cs = E.colorStart[c], n = E.colorStart[c + 1] - cs;
           int key = 0;
           if (slot < n && n < L / P && !(c == 1 && early)) {
+            // What four lanes save over two: the hinge rounds (ceil(h / 2)
+            // against ceil(h / 4)) and the contact rounds beyond the two
+            // straight-line ones per lane, a hinge's rows costing about
+            // three contacts' (instruction counts of the float assembly).
             const int b = E.order[cs + slot];
             const int hinges = F.adjStart[b + 1] - F.adjStart[b];
             const int ground = stp.groundCount(b);
-            const int units = hinges > ground ? hinges : ground;
-            key = units > 2 ? (units << 8 | (255 - slot)) : 0;
+            const int hingeRounds = ((hinges + 1) >> 1) - ((hinges + 3) >> 2);
+            const int extra2 = ((ground + 1) >> 1) - 2, extra4 = ((ground + 3) >> 2) - 2;
+            const int contactRounds = (extra2 > 0 ? extra2 : 0) - (extra4 > 0 ? extra4 : 0);
+            const int saved = 3 * hingeRounds + contactRounds;
+            key = saved > 0 ? (saved << 8 | (255 - slot)) : 0;
           }
           key = groupMax<L>(key);
           bestOf[c] = key != 0 ? 255 - (key & 255) : -1;
