@@ -1354,8 +1354,28 @@ __device__ __forceinline__ void stepBody(const StepArgs &args, const ServoArgs<R
         }
       }
     }
+    // the per-body contact masks, cleared here and filled below by LDS atomic
+    // ors from the contacts' lanes (one per contact instead of a walk over
+    // the list per body)
+    constexpr int GW = (CG + 63) / 64;
+    if (active) {
+      for (int b = lane; b < B; b += L) {
+#pragma unroll
+        for (int k = 0; k < GW; ++k)
+          E.gmask[k][b] = 0;
+        E.smask[b] = 0;
+      }
+    }
     __syncthreads(); // joint warm start reads the poses the predictor overwrites
     if (active) {
+      for (int i = lane; i < E.s.ngc; i += L)
+        atomicOr(reinterpret_cast<unsigned long long *>(&E.gmask[i >> 6][gcBody(E.s.gc[i].id)]),
+                 1ull << (i & 63));
+      for (int i = lane; i < E.s.nsc; i += L) {
+        const int id = E.s.sc[i].id;
+        atomicOr(&E.smask[scBody(id)], 1u << i);
+        atomicOr(&E.smask[scOther(id)], 1u << i);
+      }
       for (int b = lane; b < nb; b += L) {
         V3<R> x = stp.X(b);
         Q4<R> q = stp.Q(b);
@@ -1372,21 +1392,6 @@ __device__ __forceinline__ void stepBody(const StepArgs &args, const ServoArgs<R
           for (int k = 0; k < 6; ++k)
             E.Iw[k][b] = iw[k];
         }
-        constexpr int GW = (CG + 63) / 64;
-        uint64_t gm[GW] = {};
-        for (int i = 0; i < E.s.ngc; ++i)
-          if (gcBody(E.s.gc[i].id) == b)
-            gm[i >> 6] |= uint64_t(1) << (i & 63);
-        uint32_t sm = 0;
-        for (int i = 0; i < E.s.nsc; ++i) {
-          int id = E.s.sc[i].id;
-          if (scBody(id) == b || scOther(id) == b)
-            sm |= 1u << i;
-        }
-#pragma unroll
-        for (int k = 0; k < GW; ++k)
-          E.gmask[k][b] = gm[k];
-        E.smask[b] = sm;
         const R mass = E.s.mass[b];
         if (mass == 0)
           continue;
