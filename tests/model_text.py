@@ -53,18 +53,21 @@ def chain(bodies=4, shapes_per_body=1, version=2, pairs=(), header=None, edit=No
 
 
 def caterpillar(segments=24, pairs=True, length=0.04, width=0.03, height=0.02, mass=0.05,
-                friction=0.8):
+                friction=0.8, shapes_per_segment=1):
     """`segments` boxes lying on the ground in a row along x, each hinged to
     the next about z (yaw: the row curls in the ground plane), every box a
     ground shape resting on its four bottom corners; with `pairs`, body
     contact between segments i and i + 2 (the neighbours a curl brings
-    together).  Segment 1 is the free root."""
+    together).  Segment 1 is the free root.  `shapes_per_segment` > 1 stacks
+    that many identical box shapes on each segment (each brings its own four
+    ground contacts)."""
     hx, hy, hz = length / 2, width / 2, height / 2
     ix = mass * (4 * hy * hy + 4 * hz * hz) / 12
     iy = mass * (4 * hx * hx + 4 * hz * hz) / 12
     iz = mass * (4 * hx * hx + 4 * hy * hy) / 12
     nb, nj = segments + 1, segments - 1
-    lines = [f"DUCK_MODEL {2 if pairs else 1} {nb} {nj} {segments}", "0 0 -9.81 1",
+    lines = [f"DUCK_MODEL {2 if pairs else 1} {nb} {nj} {segments * shapes_per_segment}",
+             "0 0 -9.81 1",
              _body("world", 0, 0)]
     for s in range(segments):
         lines.append(" ".join(str(v) for v in (f"segment{s}", mass, ix, iy, iz,
@@ -76,10 +79,12 @@ def caterpillar(segments=24, pairs=True, length=0.04, width=0.03, height=0.02, m
             f"yaw{j}", j + 1, j + 2, hx + gap, 0, 0, -hx - gap, 0, 0, 0, 0, 1, 0, 0, 1,
             1, 0, 0, 1, 0, 0, 1, -1.2, 1.2, 0.02, 0.001, 0, 0, 8, 0, 0)))
     for s in range(segments):
-        line = f"{s + 1} 1 0 0 0 1 0 0 0 {hx} {hy} {hz} {friction} 0"
-        lines.append(line + (" 1" if pairs else ""))
+        for _ in range(shapes_per_segment):
+            line = f"{s + 1} 1 0 0 0 1 0 0 0 {hx} {hy} {hz} {friction} 0"
+            lines.append(line + (" 1" if pairs else ""))
     if pairs:
-        chosen = [(s, s + 2) for s in range(segments - 2)]
+        k = shapes_per_segment
+        chosen = [(k * s, k * (s + 2)) for s in range(segments - 2)]
         lines.append(str(len(chosen)))
         lines += [f"{a} {b} 0.5" for a, b in chosen]
     return "\n".join(lines) + "\n"
