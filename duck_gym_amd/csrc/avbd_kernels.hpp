@@ -1354,9 +1354,8 @@ __device__ __forceinline__ void stepBody(const StepArgs &args, const ServoArgs<R
         }
       }
     }
-    // the per-body contact masks, cleared here and filled below by LDS atomic
-    // ors from the contacts' lanes (one per contact instead of a walk over
-    // the list per body)
+    // The per-body contact masks, cleared here and filled below by one LDS
+    // atomic or per contact from the contact's lane.
     constexpr int GW = (CG + 63) / 64;
     if (active) {
       for (int b = lane; b < B; b += L) {
