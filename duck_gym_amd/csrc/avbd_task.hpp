@@ -96,15 +96,78 @@ struct TaskBuffers {
   void *diag;                // [E,6] R, may be null
 };
 
+// What the task kernel reads of a blob, staged in LDS: the 16-byte chunks
+// covering the diagnostics through the angular velocities (the targets, force
+// and the body poses and velocities lie between them).  A workgroup of 64
+// lanes copies its environments' ranges with whole-wave loads (each
+// environment's chunks are consecutive, so a load instruction covers a few
+// cache lines instead of one line per lane), then each lane computes one
+// environment from LDS.
+template <class S> constexpr size_t taskStageBegin() { return diagBegin<S>() / 16 * 16; }
+template <class S> constexpr size_t taskStageEnd() { return (offsetof(S, w) + sizeof(S::w) + 15) / 16 * 16; }
+template <class S> constexpr int taskStageChunks() { return int((taskStageEnd<S>() - taskStageBegin<S>()) / 16); }
+// environments per workgroup: as many as 60 KiB of LDS holds, at most 64; the
+// record stride in words is the chunks' plus one (odd: the lanes' records
+// fall on distinct LDS banks) for a float batch, plus two for a double one
+// (whole 8-byte words)
+template <class S> constexpr int taskStageStride() {
+  return 4 * taskStageChunks<S>() + (sizeof(S::diag[0]) == 4 ? 1 : 2);
+}
+template <class S> constexpr int taskEnvsPerBlock() {
+  return 61440 / (4 * taskStageStride<S>()) > 64 ? 64 : 61440 / (4 * taskStageStride<S>());
+}
+
+// The staged fields of one environment (the same values as the blob's).
+template <class R, int B, int J, int CG, int CS> struct TaskStage {
+  using State = EnvState<R, B, J, CG, CS>;
+  const DeviceModel<R> &M;
+  const R *r; // the environment's staged words, from taskStageBegin
+  static constexpr int at(size_t offset) { return int((offset - taskStageBegin<State>()) / sizeof(R)); }
+  DUCK_HD R x(int k, int b) const { return r[at(offsetof(State, x)) + k * B + b]; }
+  DUCK_HD R q(int k, int b) const { return r[at(offsetof(State, q)) + k * B + b]; }
+  DUCK_HD R v(int k, int b) const { return r[at(offsetof(State, v)) + k * B + b]; }
+  DUCK_HD R w(int k, int b) const { return r[at(offsetof(State, w)) + k * B + b]; }
+  DUCK_HD R diag(int k) const { return r[at(offsetof(State, diag)) + k]; }
+  DUCK_HD Q4<R> Q(int b) const { return {q(0, b), q(1, b), q(2, b), q(3, b)}; }
+  DUCK_HD V3<R> W(int b) const { return {w(0, b), w(1, b), w(2, b)}; }
+  DUCK_HD V3<R> mv(const R (&a)[3][kMaxModelJoints], int j) const { return {a[0][j], a[1][j], a[2][j]}; }
+  DUCK_HD R angle(int j) const {
+    return hingeAngle(Q(M.ja[j]), Q(M.jb[j]), mv(M.axisA, j), mv(M.tangentA, j), mv(M.tangentB, j));
+  }
+};
+
 template <class R, int B, int J, int CG, int CS>
-__global__ void taskKernel(DuckTask t, int mode, const DeviceModel<R> *model,
-                           unsigned char *states, long long blobBytes, int count, TaskBuffers io) {
-  int e = blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= count)
+__global__ __launch_bounds__(64) void taskKernel(DuckTask t, int mode, const DeviceModel<R> *model,
+                                                 unsigned char *states, long long blobBytes, int count,
+                                                 TaskBuffers io) {
+  using State = EnvState<R, B, J, CG, CS>;
+  constexpr int CH = taskStageChunks<State>(), STRIDE = taskStageStride<State>(),
+                TE = taskEnvsPerBlock<State>();
+  static_assert(TE >= 1 && (4 * STRIDE) % sizeof(R) == 0 && taskStageBegin<State>() % sizeof(R) == 0,
+                "a staged record holds whole words of the batch dtype");
+  __shared__ unsigned stage[TE * STRIDE];
+  const int e0 = blockIdx.x * TE;
+  for (int i = 0; i < TE; ++i) {
+    const int e = e0 + i;
+    if (e >= count)
+      break;
+    const uint4 *src = reinterpret_cast<const uint4 *>(states + blobBytes * e + taskStageBegin<State>());
+    for (int c = threadIdx.x; c < CH; c += 64) {
+      const uint4 v = src[c];
+      unsigned *dst = stage + i * STRIDE + 4 * c;
+      dst[0] = v.x;
+      dst[1] = v.y;
+      dst[2] = v.z;
+      dst[3] = v.w;
+    }
+  }
+  __syncthreads();
+  const int e = e0 + int(threadIdx.x);
+  if (threadIdx.x >= TE || e >= count)
     return;
   const DeviceModel<R> &M = *model;
-  auto &s = blobAt<EnvState<R, B, J, CG, CS>>(states, blobBytes, e);
-  StateView<R, B, J, CG, CS> view{M, s};
+  const State &s = blobAt<State>(states, blobBytes, e);
+  const TaskStage<R, B, J, CG, CS> view{M, reinterpret_cast<const R *>(stage + threadIdx.x * STRIDE)};
   const int nj = M.nj;
   R *act = static_cast<R *>(io.action) + size_t(e) * nj;
   R *last = static_cast<R *>(io.lastAction) + size_t(e) * nj;
@@ -130,12 +193,12 @@ __global__ void taskKernel(DuckTask t, int mode, const DeviceModel<R> *model,
   Q4<R> iq{R(t.iquat[0]), -R(t.iquat[1]), -R(t.iquat[2]), -R(t.iquat[3])};
   Q4<R> q = qb * iq;
   V3<R> g = rotateInv(q, V3<R>{R(0), R(0), R(-1)});
-  V3<R> vel{s.v[0][root], s.v[1][root], s.v[2][root]};
+  V3<R> vel{view.v(0, root), view.v(1, root), view.v(2, root)};
   V3<R> v = rotateInv(q, vel);
   V3<R> w = rotateInv(q, view.W(root));
   R yawC = R(1) - R(2) * (q.y * q.y + q.z * q.z);
   R yawS = R(2) * (q.w * q.z + q.x * q.y);
-  R height = s.x[2][root] - R(t.root_height);
+  R height = view.x(2, root) - R(t.root_height);
 
   R reward = 0;
   bool failed = false, timeout = false;
@@ -144,16 +207,16 @@ __global__ void taskKernel(DuckTask t, int mode, const DeviceModel<R> *model,
     bool finite = true;
     for (int b = 0; b < M.nb; ++b) {
       for (int k = 0; k < 3; ++k)
-        finite = finite && mfinite(s.x[k][b]) && mfinite(s.v[k][b]) && mfinite(s.w[k][b]);
+        finite = finite && mfinite(view.x(k, b)) && mfinite(view.v(k, b)) && mfinite(view.w(k, b));
       for (int k = 0; k < 4; ++k)
-        finite = finite && mfinite(s.q[k][b]);
+        finite = finite && mfinite(view.q(k, b));
     }
     const R cosHalf = R(cosf(0.5f)); // torch.cos of a float32 0.5
     if (t.kind == DUCK_TASK_ROLLOUT)
-      failed = s.x[2][root] < R(t.fall_height);
+      failed = view.x(2, root) < R(t.fall_height);
     else
-      failed = g.z > -cosHalf || mabs(height) > R(0.04) || s.diag[kJointError] > R(0.005) ||
-               s.diag[kPenetration] > R(0.005);
+      failed = g.z > -cosHalf || mabs(height) > R(0.04) || view.diag(kJointError) > R(0.005) ||
+               view.diag(kPenetration) > R(0.005);
     failed = failed || s.failed > 0 || !finite;
 
     R pose = 0, act2 = 0, dact2 = 0;
@@ -197,7 +260,7 @@ __global__ void taskKernel(DuckTask t, int mode, const DeviceModel<R> *model,
       R penalty = 0;
       for (int f = 0; f < 2; ++f) {
         const int fb = t.feet[f];
-        const V3<R> p{s.x[0][fb], s.x[1][fb], s.x[2][fb]};
+        const V3<R> p{view.x(0, fb), view.x(1, fb), view.x(2, fb)};
         const Q4<R> qf = view.Q(fb);
         // inverse_rotate(q, up) (tensor_env.py:21-23)
         const V3<R> up{R(0), R(0), R(1)}, u{-qf.x, -qf.y, -qf.z};
@@ -247,11 +310,11 @@ __global__ void taskKernel(DuckTask t, int mode, const DeviceModel<R> *model,
       last[j] = act[j];
     if (io.diag) {
       R *d = static_cast<R *>(io.diag) + size_t(e) * 6;
-      d[0] = s.diag[kJointError];
-      d[1] = s.diag[kPenetration];
-      d[2] = s.diag[kContacts];
-      d[3] = s.diag[kConverged];
-      d[4] = s.diag[kAxisError];
+      d[0] = view.diag(kJointError);
+      d[1] = view.diag(kPenetration);
+      d[2] = view.diag(kContacts);
+      d[3] = view.diag(kConverged);
+      d[4] = view.diag(kAxisError);
       d[5] = R(s.failed);
     }
   }

@@ -539,7 +539,8 @@ public:
   void task(const DuckTask &t, int mode, const TaskBuffers &io, hipStream_t s) override {
     DeviceGuard guard(device);
     wait(s);
-    taskKernel<R, B, J, CG, CS><<<blocks64(count), 64, 0, s>>>(t, mode, dModel, dStates, blobBytes,
+    constexpr int TE = taskEnvsPerBlock<State>();
+    taskKernel<R, B, J, CG, CS><<<(count + TE - 1) / TE, 64, 0, s>>>(t, mode, dModel, dStates, blobBytes,
                                                                 count, io);
     launched("taskKernel");
     record(s);
