@@ -147,19 +147,18 @@ __global__ __launch_bounds__(64) void taskKernel(DuckTask t, int mode, const Dev
                 "a staged record holds whole words of the batch dtype");
   __shared__ unsigned stage[TE * STRIDE];
   const int e0 = blockIdx.x * TE;
-  for (int i = 0; i < TE; ++i) {
-    const int e = e0 + i;
-    if (e >= count)
-      break;
-    const uint4 *src = reinterpret_cast<const uint4 *>(states + blobBytes * e + taskStageBegin<State>());
-    for (int c = threadIdx.x; c < CH; c += 64) {
-      const uint4 v = src[c];
-      unsigned *dst = stage + i * STRIDE + 4 * c;
-      dst[0] = v.x;
-      dst[1] = v.y;
-      dst[2] = v.z;
-      dst[3] = v.w;
-    }
+  const int n = count - e0 < TE ? count - e0 : TE;
+  // chunk c of environment i is item i CH + c; the lanes take the items in
+  // turn, so that a lane's loads are independent and in flight together
+#pragma unroll 8
+  for (int item = threadIdx.x; item < n * CH; item += 64) {
+    const int i = item / CH, c = item - i * CH;
+    const uint4 v = reinterpret_cast<const uint4 *>(states + blobBytes * (e0 + i) + taskStageBegin<State>())[c];
+    unsigned *dst = stage + i * STRIDE + 4 * c;
+    dst[0] = v.x;
+    dst[1] = v.y;
+    dst[2] = v.z;
+    dst[3] = v.w;
   }
   __syncthreads();
   const int e = e0 + int(threadIdx.x);
