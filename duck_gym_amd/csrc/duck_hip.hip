@@ -918,10 +918,13 @@ int duck_model_info(const char *model_path, unsigned flags, int *out) {
   });
 }
 
-int duck_create(const char *model_path, int num_envs, double dt, int iterations, int device,
-                int fp_bits, unsigned flags, void **out_handle) {
+namespace {
+// duck_create and duck_create_text: the model from a file or from text, then
+// the batch checks and the batch.
+int createBatch(const char *source, bool text, int num_envs, double dt, int iterations,
+                int device, int fp_bits, unsigned flags, void **out_handle) {
   return guarded([&] {
-    require(out_handle != nullptr && model_path != nullptr, "null argument");
+    require(out_handle != nullptr && source != nullptr, "null argument");
     *out_handle = nullptr;
     // extension.cu:424 checks the shared-memory option before anything else
     require(!(flags & DUCK_FLAG_SHARED_MEMORY) || (flags & DUCK_FLAG_SPECIALIZED),
@@ -932,7 +935,7 @@ int duck_create(const char *model_path, int num_envs, double dt, int iterations,
     int devices = 0;
     hipCheck(hipGetDeviceCount(&devices), "hipGetDeviceCount");
     require(device >= 0 && device < devices, "Invalid device index");
-    HostModel m = loadModel(model_path);
+    HostModel m = text ? loadModelText(source) : loadModel(source);
     checkBackend(m, flags);
     const bool split = flags & DUCK_FLAG_SPLIT;
     BatchBase *b =
@@ -940,6 +943,19 @@ int duck_create(const char *model_path, int num_envs, double dt, int iterations,
                       : makeBatch<float>(std::move(m), num_envs, dt, iterations, device, split);
     *out_handle = b;
   });
+}
+} // namespace
+
+int duck_create(const char *model_path, int num_envs, double dt, int iterations, int device,
+                int fp_bits, unsigned flags, void **out_handle) {
+  return createBatch(model_path, false, num_envs, dt, iterations, device, fp_bits, flags,
+                     out_handle);
+}
+
+int duck_create_text(const char *model_text, int num_envs, double dt, int iterations, int device,
+                     int fp_bits, unsigned flags, void **out_handle) {
+  return createBatch(model_text, true, num_envs, dt, iterations, device, fp_bits, flags,
+                     out_handle);
 }
 
 void duck_destroy(void *handle) { delete static_cast<BatchBase *>(handle); }

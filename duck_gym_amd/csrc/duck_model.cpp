@@ -3,6 +3,7 @@
 #include <algorithm>
 #include <cmath>
 #include <fstream>
+#include <sstream>
 #include <stdexcept>
 
 namespace duckhip {
@@ -61,10 +62,21 @@ HostModel loadModel(const std::string &path) {
   return m;
 }
 
+HostModel loadModelText(const std::string &text) {
+  std::istringstream in(text);
+  HostModel m = parseModelStream(in);
+  flattenModel(m);
+  return m;
+}
+
 HostModel parseModel(const std::string &path) {
   std::ifstream in(path);
   if (!in)
     throw std::runtime_error("Cannot read model: " + path);
+  return parseModelStream(in);
+}
+
+HostModel parseModelStream(std::istream &in) {
   HostModel m;
   std::string header;
   int version = -1, nb = -1, nj = -1, ns = -1;

@@ -5,6 +5,7 @@
 // single-parent tree in topological order, depth-parity colours, bipartite
 // hinge graph, body->joint CSR, shape points and interior points).
 #pragma once
+#include <istream>
 #include <string>
 #include <vector>
 
@@ -53,5 +54,9 @@ HostModel loadModel(const std::string &path);
 // adjacency, shape points, interiors and contact capacities.
 HostModel parseModel(const std::string &path);
 void flattenModel(HostModel &m);
+// loadModel on the text of a `.duck` file held in memory (the same checks
+// and messages); parseModelStream is parseModel on an open stream.
+HostModel loadModelText(const std::string &text);
+HostModel parseModelStream(std::istream &in);
 
 } // namespace duckhip

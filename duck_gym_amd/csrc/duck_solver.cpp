@@ -13,12 +13,10 @@
 #include <algorithm>
 #include <cctype>
 #include <exception>
-#include <cstdio>
 #include <cstring>
 #include <fstream>
 #include <iomanip>
 #include <sstream>
-#include <unistd.h>
 
 namespace duck {
 namespace {
@@ -592,19 +590,11 @@ void Solver::stepImplicit() {
   if (!device || device->signature != sig.str()) {
     device.reset();
     auto d = std::make_unique<Device>();
-    char path[] = "/tmp/duck_solver_XXXXXX";
-    const int fd = mkstemp(path);
-    if (fd < 0)
-      throw std::runtime_error("cannot write a temporary model file");
-    close(fd);
-    {
-      std::ofstream out(path);
-      out << modelText(*this, true);
-    }
     int gpu = 0;
     hip(hipGetDevice(&gpu), "hipGetDevice");
-    const int code = duck_create(path, 1, options.dt, options.iterations, gpu, 64, 0, &d->handle);
-    std::remove(path);
+    const std::string text = modelText(*this, true);
+    const int code =
+        duck_create_text(text.c_str(), 1, options.dt, options.iterations, gpu, 64, 0, &d->handle);
     if (code)
       fail(code);
     if (int c = duck_state_layout(d->handle, d->layout))

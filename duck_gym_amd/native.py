@@ -33,6 +33,7 @@ def library():
         dbl = ctypes.c_double
         sig = {
             "duck_create": (ip, [cp, ip, dbl, ip, ip, ip, ctypes.c_uint, ctypes.POINTER(vp)]),
+            "duck_create_text": (ip, [cp, ip, dbl, ip, ip, ip, ctypes.c_uint, ctypes.POINTER(vp)]),
             "duck_destroy": (None, [vp]),
             "duck_model_info": (ip, [cp, ctypes.c_uint, ctypes.POINTER(ip)]),
             "duck_dims": (ip, [vp, ctypes.POINTER(ip), ctypes.POINTER(ip), ctypes.POINTER(ip)]),
@@ -74,7 +75,7 @@ def library():
 
 
 EXPORTED = (
-    "duck_create", "duck_destroy", "duck_model_info", "duck_dims", "duck_num_envs", "duck_fp_bits",
+    "duck_create", "duck_create_text", "duck_destroy", "duck_model_info", "duck_dims", "duck_num_envs", "duck_fp_bits",
     "duck_state_bytes", "duck_kernel_info", "duck_joint_name", "duck_reset", "duck_step",
     "duck_step_motor", "duck_advance",
     "duck_state", "duck_contact_forces", "duck_self_contact_stats", "duck_contact_counts",
@@ -185,13 +186,25 @@ class CudaBatch:
         # kernel always stages environment state in LDS.  `split_solve` (an
         # extension) runs float64 batches in the float layout: two lanes per
         # body block solve, whose partial systems are summed in another order.
+        self._create(library().duck_create, str(model), num_envs, dt, iterations, device, fp64,
+                     _flags(specialized, shared_memory, split_solve))
+
+    @classmethod
+    def from_text(cls, text, num_envs, dt=0.001, iterations=200, device=0, fp64=False,
+                  specialized=False, shared_memory=False, split_solve=False):
+        """A batch of the model whose `.duck` text is `text` (no file; the
+        same checks and errors as the constructor)."""
+        self = cls.__new__(cls)
+        self._create(library().duck_create_text, str(text), num_envs, dt, iterations, device,
+                     fp64, _flags(specialized, shared_memory, split_solve))
+        return self
+
+    def _create(self, create, source, num_envs, dt, iterations, device, fp64, flags):
         lib = library()
         self._h = None
         handle = ctypes.c_void_p()
-        code = lib.duck_create(str(model).encode(), int(num_envs), float(dt), int(iterations),
-                               int(device), 64 if fp64 else 32,
-                               _flags(specialized, shared_memory, split_solve),
-                               ctypes.byref(handle))
+        code = create(source.encode(), int(num_envs), float(dt), int(iterations), int(device),
+                      64 if fp64 else 32, flags, ctypes.byref(handle))
         if code:
             _raise(code, "CudaBatch")
         self._h = handle

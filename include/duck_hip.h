@@ -41,6 +41,13 @@ enum {
  * (extension.cu:216-265, 423-441).  num_envs in [1, 65536]. */
 int duck_create(const char *model_path, int num_envs, double dt, int iterations, int device,
                 int fp_bits, unsigned flags, void **out_handle);
+/* duck_create on the text of a `.duck` file held in memory (the same checks,
+ * messages and error codes; an unparsable text is DUCK_ERR_RUNTIME).  No
+ * counterpart in the reference, whose CudaBatch and Solver::load read files:
+ * for callers that hold the model in memory, such as duck::Solver, which
+ * builds its device batch from its own members without a temporary file. */
+int duck_create_text(const char *model_text, int num_envs, double dt, int iterations, int device,
+                     int fp_bits, unsigned flags, void **out_handle);
 void duck_destroy(void *handle);
 
 /* Parse and validate a `.duck` model file without a device: the checks of

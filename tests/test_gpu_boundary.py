@@ -75,6 +75,30 @@ def test_model_file_errors_raise_as_the_reference(tmp_path, models):
         CudaBatch(path, 4, DT, ITER, 0, True, True)
 
 
+def test_batch_from_text_equals_batch_from_file(tmp_path, models, home):
+    """`CudaBatch.from_text` (duck_create_text, no file) steps bit for bit as
+    the batch the constructor reads from the same text, and raises what the
+    constructor raises for the same malformed text."""
+    from test_model_errors import RUNTIME, VALUE
+
+    text = models["selfc"].read_text()
+    rng = np.random.default_rng(3)
+    targets = torch.tensor(home + rng.uniform(-0.2, 0.2, (9, 14)), dtype=torch.float32,
+                           device=DEV)
+    forces = torch.zeros(9, 3, device=DEV)
+    a, b = _batch(models["selfc"], 9), CudaBatch.from_text(text, 9, DT, ITER, 0, False)
+    for batch in (a, b):
+        _reset_home(batch, home)
+        for _ in range(12):
+            batch.step(targets, forces, 1, KP, 0.0)
+    assert torch.equal(a.export_state(), b.export_state())
+    for cases, error in ((RUNTIME, RuntimeError), ([c for c in VALUE if c[1]], ValueError)):
+        for name, bad, message in cases:
+            with pytest.raises(error) as caught:
+                CudaBatch.from_text(bad, 4, DT, ITER)
+            assert message in str(caught.value), name
+
+
 def test_nan_isolation_and_reset_recovery(models, home):
     b = _batch(models["standing"], 4)
     _reset_home(b, home)
