@@ -105,6 +105,9 @@ class TensorEnv:
         self.lower = t(self.meta["lower"])
         self.upper = t(self.meta["upper"])
         self.iquat = t(self.meta["root_iquat"]) * torch.tensor([1, -1, -1, -1], device=self.device)
+        # constant tables, uploaded once (not on every reset or state() call)
+        self._directions = t([[1.0, 0], [-1, 0], [0, 1], [0, -1]])
+        self._down = t([0.0, 0, -1])
         self.actions = torch.zeros(num_envs, 14, device=self.device, dtype=self.dtype)
         self.forces = torch.zeros(num_envs, 3, device=self.device, dtype=self.dtype)
         self.commands = torch.zeros(num_envs, 2, device=self.device, dtype=self.dtype)
@@ -204,8 +207,7 @@ class TensorEnv:
         mask = mask.contiguous()
         self.native.reset(mask, q.contiguous(), roots)
         if self.task != "standing":
-            directions = torch.tensor([[1.0, 0], [-1, 0], [0, 1], [0, -1]], device=self.device,
-                                      dtype=self.dtype)
+            directions = self._directions
             if self.command_direction == "all":
                 selected = torch.randint(4, (self.num_envs,), generator=self.generator,
                                          device=self.device)
@@ -226,7 +228,7 @@ class TensorEnv:
         """(bodies, joints, diag, gravity, v, w, yaw) as tensor_env.py:221-236."""
         b, j, d = [v.to(self.dtype) for v in self.native.state()]
         q = multiply(b[:, 1, 3:7], self.iquat.expand(self.num_envs, -1))
-        down = torch.tensor([0.0, 0, -1], device=self.device, dtype=self.dtype)
+        down = self._down
         gravity = inverse_rotate(q, down.expand(self.num_envs, -1))
         v = inverse_rotate(q, b[:, 1, 7:10])
         w = inverse_rotate(q, b[:, 1, 10:13])
