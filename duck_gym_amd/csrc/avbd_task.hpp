@@ -81,6 +81,41 @@ __global__ void taskTargetsKernel(DuckTask t, int count, int nj, const R *action
   target[i] = v;
 }
 
+// TensorEnv.reset's inputs from the caller's random draws (tensor_env.py:
+// 196-217), each value rounded per operation as the torch expressions are:
+// thread i < count * nj writes q[i] = HOME + (u - 0.5) * 0.02 (HOME without
+// draws); thread e < count writes the root offset (0, 0, 0.001, (v - 0.5) *
+// 0.02, (v' - 0.5) * 0.02, 0) (zeros without draws) and, with a command draw
+// (`selected`, or one `direction` for every env), commandsOut = mask ?
+// table[direction] * speed : commands.
+template <class R>
+__global__ void taskResetInputsKernel(DuckTask t, int count, int nj, const unsigned char *mask,
+                                      const R *jointDraws, const R *rootDraws,
+                                      const long long *selected, int direction, R speed,
+                                      const R *commands, R *q, R *roots, R *commandsOut) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < count * nj) {
+    const R home = R(t.home[i % nj]);
+    q[i] = jointDraws ? home + (jointDraws[i] - R(0.5)) * R(0.02) : home;
+  }
+  if (i >= count)
+    return;
+  R *r = roots + size_t(i) * 6;
+  r[0] = r[1] = r[5] = R(0);
+  r[2] = rootDraws ? R(0.001) : R(0);
+  r[3] = rootDraws ? (rootDraws[size_t(i) * 2] - R(0.5)) * R(0.02) : R(0);
+  r[4] = rootDraws ? (rootDraws[size_t(i) * 2 + 1] - R(0.5)) * R(0.02) : R(0);
+  if (selected || direction >= 0) {
+    // the direction table [[1, 0], [-1, 0], [0, 1], [0, -1]]
+    const int d = selected ? int(selected[i]) : direction;
+    const R dx = d == 0 ? R(1) : (d == 1 ? R(-1) : R(0));
+    const R dy = d == 2 ? R(1) : (d == 3 ? R(-1) : R(0));
+    const bool on = mask[i] != 0;
+    commandsOut[size_t(i) * 2] = on ? dx * speed : commands[size_t(i) * 2];
+    commandsOut[size_t(i) * 2 + 1] = on ? dy * speed : commands[size_t(i) * 2 + 1];
+  }
+}
+
 struct TaskBuffers {
   const unsigned char *mask; // reset mode: envs whose bookkeeping restarts
   void *action;              // [E,J] R: this step's clamped action (step) / current actions

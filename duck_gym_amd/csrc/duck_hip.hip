@@ -257,6 +257,9 @@ struct BatchBase {
   virtual void taskTargets(const DuckTask &, const void *, const void *, const long long *,
                            const void *, void *, void *, hipStream_t) = 0;
   virtual void task(const DuckTask &, int, const TaskBuffers &, hipStream_t) = 0;
+  virtual void taskResetInputs(const DuckTask &, const unsigned char *, const void *, const void *,
+                               const long long *, int, double, const void *, void *, void *,
+                               void *, hipStream_t) = 0;
   virtual void servo(const DuckServo &, const ServoBuffers &, hipStream_t) = 0;
   virtual void servoSubstep(const DuckServo &, const DuckServoSubstep &, hipStream_t) = 0;
   virtual void kernelInfo(int which, long long *out) = 0;
@@ -535,6 +538,18 @@ public:
         t, count, nj, static_cast<const R *>(actions), static_cast<const R *>(reference), episode,
         static_cast<const R *>(commands), static_cast<R *>(clamped), static_cast<R *>(target));
     launched("taskTargetsKernel");
+  }
+  void taskResetInputs(const DuckTask &t, const unsigned char *mask, const void *jointDraws,
+                       const void *rootDraws, const long long *selected, int direction,
+                       double speed, const void *commands, void *q, void *roots,
+                       void *commandsOut, hipStream_t s) override {
+    DeviceGuard guard(device);
+    const int nj = host.joints.size();
+    taskResetInputsKernel<R><<<blocks64(count * std::max(nj, 1)), 64, 0, s>>>(
+        t, count, nj, mask, static_cast<const R *>(jointDraws), static_cast<const R *>(rootDraws),
+        selected, direction, R(speed), static_cast<const R *>(commands), static_cast<R *>(q),
+        static_cast<R *>(roots), static_cast<R *>(commandsOut));
+    launched("taskResetInputsKernel");
   }
   void task(const DuckTask &t, int mode, const TaskBuffers &io, hipStream_t s) override {
     DeviceGuard guard(device);
@@ -1093,6 +1108,23 @@ int duck_task_step(void *handle, const DuckTask *task, const void *action, void 
     TaskBuffers io{nullptr, const_cast<void *>(action), last_action, commands, episode,
                    filtered, returns, nullptr, obs, reward, failed, timeout, done, diag};
     b->task(*task, kTaskStep, io, st(hip_stream));
+  });
+}
+int duck_task_reset_inputs(void *handle, const DuckTask *task, const unsigned char *reset_mask,
+                           const void *joint_draws, const void *root_draws,
+                           const long long *selected, int direction, double command_speed,
+                           const void *commands, void *q, void *roots, void *commands_out,
+                           void *hip_stream) {
+  return guarded([&] {
+    auto *b = as(handle);
+    checkTask(b, task);
+    require(q && roots, "task reset inputs: null buffer");
+    require(direction < 4, "task reset inputs: direction outside the table");
+    require(!(selected || direction >= 0) || (reset_mask && commands && commands_out),
+            "task reset inputs: a command draw needs the reset mask and both command buffers");
+    require(std::isfinite(command_speed), "task reset inputs: command speed not finite");
+    b->taskResetInputs(*task, reset_mask, joint_draws, root_draws, selected, direction,
+                       command_speed, commands, q, roots, commands_out, st(hip_stream));
   });
 }
 int duck_task_observe(void *handle, const DuckTask *task, const unsigned char *reset_mask,

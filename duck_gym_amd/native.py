@@ -62,6 +62,8 @@ def library():
             "duck_task_targets": (ip, [vp, ctypes.POINTER(DuckTask)] + [vp] * 7),
             "duck_task_step": (ip, [vp, ctypes.POINTER(DuckTask)] + [vp] * 13),
             "duck_task_observe": (ip, [vp, ctypes.POINTER(DuckTask)] + [vp] * 9),
+            "duck_task_reset_inputs": (ip, [vp, ctypes.POINTER(DuckTask), vp, vp, vp, vp, ip, dbl,
+                                            vp, vp, vp, vp, vp]),
             "duck_servo": (ip, [vp, ctypes.POINTER(DuckServo), vp, vp, ip] + [vp] * 7),
             "duck_servo_substep": (ip, [vp, ctypes.POINTER(DuckServo),
                                         ctypes.POINTER(DuckServoSubstep), vp]),
@@ -82,7 +84,8 @@ EXPORTED = (
     "duck_generalized_loads", "duck_reference", "duck_reference_noalloc", "duck_state_layout",
     "duck_export_state",
     "duck_import_state", "duck_last_error", "duck_task_obs_dim", "duck_task_targets",
-    "duck_task_step", "duck_task_observe", "duck_servo", "duck_servo_substep",
+    "duck_task_step", "duck_task_observe", "duck_task_reset_inputs", "duck_servo",
+    "duck_servo_substep",
     "duck_sequential_step",
 )
 
@@ -497,6 +500,23 @@ class CudaBatch:
             code = library().duck_task_observe(self._h, ctypes.byref(task), *args, self._stream())
         if code:
             _raise(code, "task_observe")
+
+    def task_reset_inputs(self, task, reset_mask, joint_draws, root_draws, selected, direction,
+                          command_speed, commands, q, roots, commands_out):
+        """TensorEnv.reset's q [E,J], root offsets [E,6] and, with a command draw
+        (`selected` [E] int64 or one `direction` >= 0), commands_out [E,2] from
+        the caller's draws, in one launch (duck_task_reset_inputs)."""
+        E, J = self.num_envs, self.num_joints
+        args = [self._ptr(reset_mask, [E], torch.bool), self._ptr(joint_draws, [E, J]),
+                self._ptr(root_draws, [E, 2]), self._ptr(selected, [E], torch.int64),
+                int(direction), float(command_speed), self._ptr(commands, [E, 2]),
+                self._check(q, [E, J]), self._check(roots, [E, 6]),
+                self._ptr(commands_out, [E, 2])]
+        with torch.cuda.device(self.device):
+            code = library().duck_task_reset_inputs(self._h, ctypes.byref(task), *args,
+                                                    self._stream())
+        if code:
+            _raise(code, "task_reset_inputs")
 
     # ------------------------------------------------ state introspection
     def state_layout(self):

@@ -105,8 +105,7 @@ class TensorEnv:
         self.lower = t(self.meta["lower"])
         self.upper = t(self.meta["upper"])
         self.iquat = t(self.meta["root_iquat"]) * torch.tensor([1, -1, -1, -1], device=self.device)
-        # constant tables, uploaded once (not on every reset or state() call)
-        self._directions = t([[1.0, 0], [-1, 0], [0, 1], [0, -1]])
+        # uploaded once, not on every state() call
         self._down = t([0.0, 0, -1])
         self.actions = torch.zeros(num_envs, 14, device=self.device, dtype=self.dtype)
         self.forces = torch.zeros(num_envs, 3, device=self.device, dtype=self.dtype)
@@ -195,28 +194,35 @@ class TensorEnv:
 
     # ------------------------------------------------------------------ reset
     def reset(self, mask):
-        """Masked reset with the reference's random draws (tensor_env.py:178-219)."""
-        q = self.home.expand(self.num_envs, -1).clone()
-        roots = torch.zeros(self.num_envs, 6, device=self.device, dtype=self.dtype)
-        if self.randomize:
-            q += (torch.rand(q.shape, generator=self.generator, device=self.device,
-                             dtype=self.dtype) - 0.5) * 0.02
-            roots[:, 3:5] = (torch.rand((self.num_envs, 2), generator=self.generator,
-                                        device=self.device, dtype=self.dtype) - 0.5) * 0.02
-            roots[:, 2] = 0.001
+        """Masked reset with the reference's random draws (tensor_env.py:178-219).
+        The draws are the reference's, in its order, on `self.generator`; q,
+        the root offsets and the new commands that it computes from them with
+        a dozen torch operations come from one launch
+        (duck_task_reset_inputs), rounded as those operations round."""
+        E, J = self.num_envs, len(self.meta["home"])
         mask = mask.contiguous()
-        self.native.reset(mask, q.contiguous(), roots)
+        joint_draws = root_draws = selected = commands = None
+        direction = -1
+        if self.randomize:
+            joint_draws = torch.rand((E, J), generator=self.generator, device=self.device,
+                                     dtype=self.dtype)
+            root_draws = torch.rand((E, 2), generator=self.generator, device=self.device,
+                                    dtype=self.dtype)
         if self.task != "standing":
-            directions = self._directions
+            commands = torch.empty_like(self.commands)
             if self.command_direction == "all":
-                selected = torch.randint(4, (self.num_envs,), generator=self.generator,
-                                         device=self.device)
+                selected = torch.randint(4, (E,), generator=self.generator, device=self.device)
             else:
-                selected = torch.full((self.num_envs,),
-                                      self.direction_names.index(self.command_direction),
-                                      device=self.device, dtype=torch.long)
-            self.commands = torch.where(mask[:, None], directions[selected] * self.command_speed,
-                                        self.commands).contiguous()
+                direction = self.direction_names.index(self.command_direction)
+        q = torch.empty(E, J, device=self.device, dtype=self.dtype)
+        roots = torch.empty(E, 6, device=self.device, dtype=self.dtype)
+        self.native.task_reset_inputs(self.spec, mask, joint_draws, root_draws, selected,
+                                      direction, self.command_speed,
+                                      self.commands if commands is not None else None, q, roots,
+                                      commands)
+        self.native.reset(mask, q, roots)
+        if commands is not None:
+            self.commands = commands
         obs = torch.empty(self.num_envs, self.obs_dim, device=self.device)
         self.native.task_observe(self.spec, mask, self.actions, self._commands,
                                  self.episode_length_buf, self._filtered, self.returns,
@@ -296,6 +302,7 @@ class TensorEnv:
         self.native.task_step(self.spec, a, self.actions, self._commands,
                               self.episode_length_buf, self._filtered, self.returns, obs, reward,
                               failed, timeout, done, diag)
+        peaks = diag[:, :2].amax(0)  # the two maxima in one reduction
         info = {
             "observations": {},
             "time_outs": timeout,
@@ -306,8 +313,8 @@ class TensorEnv:
             "terminal_mask": done,
             "log": {
                 "physics/failed_fraction": failed.float().mean(),
-                "physics/max_joint_error_m": diag[:, 0].max(),
-                "physics/max_penetration_m": diag[:, 1].max(),
+                "physics/max_joint_error_m": peaks[0],
+                "physics/max_penetration_m": peaks[1],
             },
         }
         if self.task == "locomotion":

@@ -215,6 +215,22 @@ int duck_task_step(void *handle, const DuckTask *task, const void *action, void 
                    float *obs, float *reward, unsigned char *failed, unsigned char *timeout,
                    unsigned char *done, void *diag, void *hip_stream);
 
+/* TensorEnv.reset's inputs (tensor_env.py:196-217) in one launch, from the
+ * random draws the caller made on its generator in the reference's order:
+ * q [E,J] = HOME + (u - 0.5) * 0.02 with u = joint_draws [E,J] (HOME when
+ * NULL); roots [E,6] = (0, 0, 0.001, (v - 0.5) * 0.02, 0) with v = root_draws
+ * [E,2] (zeros when NULL); with a command draw, `selected` [E] int64 or one
+ * `direction` (0-3) for every env (-1 and NULL: none), commands_out [E,2] =
+ * reset_mask ? table[direction] * command_speed : commands, the table
+ * [[1, 0], [-1, 0], [0, 1], [0, -1]].  Each value is rounded per operation, as
+ * the reference's torch expressions are.  Batch dtype.  No counterpart in the
+ * reference, which spends about a dozen torch launches on these. */
+int duck_task_reset_inputs(void *handle, const DuckTask *task, const unsigned char *reset_mask,
+                           const void *joint_draws, const void *root_draws,
+                           const long long *selected, int direction, double command_speed,
+                           const void *commands, void *q, void *roots, void *commands_out,
+                           void *hip_stream);
+
 /* TensorEnv.reset bookkeeping + get_observations (tensor_env.py:199-219, 259):
  * for envs in `reset_mask` (may be NULL) zero the actions, filtered velocity,
  * forces [E,3] (may be NULL), episode counter and return; then write the

@@ -145,6 +145,60 @@ def test_reset_draws_follow_the_reference_generator(model_dir):
     assert obs.shape == (16, 52) and info == {"observations": {}}
 
 
+@pytest.mark.parametrize("fp64", [False, True])
+def test_reset_inputs_equal_the_torch_expressions(model_dir, fp64):
+    """duck_task_reset_inputs against the reference's torch expressions
+    (tensor_env.py:196-217) on the same draws, bit for bit: q, the root
+    offsets, and the commands for drawn directions, one fixed direction and
+    none; a TensorEnv's commands after a reset equal the expression on its
+    generator's draws."""
+    E, J = 64, 14
+    dtype = torch.float64 if fp64 else torch.float32
+    env = TensorEnv(model_dir, E, ITER, DT, 1, seed=5, task="locomotion", fp64=fp64)
+    g = torch.Generator(device=DEV).manual_seed(123)
+    u = torch.rand((E, J), generator=g, device=DEV, dtype=dtype)
+    v = torch.rand((E, 2), generator=g, device=DEV, dtype=dtype)
+    sel = torch.randint(4, (E,), generator=g, device=DEV)
+    mask = torch.rand(E, generator=g, device=DEV) < 0.5
+    old = torch.rand((E, 2), generator=g, device=DEV, dtype=dtype)
+    table = torch.tensor([[1.0, 0], [-1, 0], [0, 1], [0, -1]], device=DEV, dtype=dtype)
+    home = torch.tensor(env.meta["home"], device=DEV, dtype=dtype)
+    speed = env.command_speed
+
+    q_ref = home.expand(E, -1).clone()
+    q_ref += (u - 0.5) * 0.02
+    roots_ref = torch.zeros(E, 6, device=DEV, dtype=dtype)
+    roots_ref[:, 3:5] = (v - 0.5) * 0.02
+    roots_ref[:, 2] = 0.001
+    for selected, direction in ((sel, -1), (None, 2), (None, -1)):
+        q, roots = torch.empty(E, J, device=DEV, dtype=dtype), torch.empty(E, 6, device=DEV, dtype=dtype)
+        commands = torch.full((E, 2), 7.0, device=DEV, dtype=dtype)
+        draw = selected is not None or direction >= 0
+        env.native.task_reset_inputs(env.spec, mask, u, v, selected, direction, speed,
+                                     old if draw else None, q, roots, commands if draw else None)
+        assert torch.equal(q, q_ref) and torch.equal(roots, roots_ref)
+        if draw:
+            chosen = selected if selected is not None else torch.full((E,), direction, device=DEV)
+            expected = torch.where(mask[:, None], table[chosen] * speed, old)
+            assert torch.equal(commands, expected)
+        else:
+            assert bool((commands == 7.0).all())
+    # without draws: HOME and zero offsets
+    q, roots = torch.empty(E, J, device=DEV, dtype=dtype), torch.empty(E, 6, device=DEV, dtype=dtype)
+    env.native.task_reset_inputs(env.spec, mask, None, None, None, -1, speed, None, q, roots, None)
+    assert torch.equal(q, home.expand(E, -1)) and bool((roots == 0).all())
+    # a TensorEnv reset: the generator's draws in the reference's order
+    g = torch.Generator(device=DEV).manual_seed(5)
+    torch.rand((E, J), generator=g, device=DEV, dtype=dtype)
+    torch.rand((E, 2), generator=g, device=DEV, dtype=dtype)
+    first = torch.randint(4, (E,), generator=g, device=DEV)
+    assert torch.equal(env.commands, table[first] * speed)
+    with pytest.raises(RuntimeError, match="reset mask"):
+        env.native.task_reset_inputs(env.spec, None, u, v, sel, -1, speed, old, q, roots, commands)
+    with pytest.raises(RuntimeError, match="direction"):
+        env.native.task_reset_inputs(env.spec, mask, u, v, None, 4, speed, old, q, roots, commands)
+
+
 def test_task_argument_checks(model_dir):
     env = TensorEnv(model_dir, 8, ITER, DT, 1)
     with pytest.raises(RuntimeError):
