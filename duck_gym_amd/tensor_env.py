@@ -312,7 +312,7 @@ class TensorEnv:
             "terminal_observation": obs,
             "terminal_mask": done,
             "log": {
-                "physics/failed_fraction": failed.float().mean(),
+                "physics/failed_fraction": failed.mean(dtype=torch.float32),
                 "physics/max_joint_error_m": peaks[0],
                 "physics/max_penetration_m": peaks[1],
             },
