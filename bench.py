@@ -475,6 +475,9 @@ def main():
     p.add_argument("--envs", type=int, default=None,
                    help="environments (default: 4096; the other workloads' own sizes)")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--device-warmup", type=float, default=0.25, metavar="SECONDS",
+                   help="home workload: seconds of the same step on a second batch before the "
+                        "warm-up steps, so that the timed steps do not run at idle clocks (0: off)")
     p.add_argument("--substeps", type=int, default=1,
                    help="physics steps per kernel launch (default 1, the tensor-env contract; "
                         "K > 1 runs K steps inside one launch, the reference's chunked form)")
@@ -532,6 +535,25 @@ def main():
     if K < 1 or args.steps % K:
         raise SystemExit("--steps must be a positive multiple of --substeps")
     launches = args.steps // K
+    # Device warm-up: the same step on a second batch of the same workload for
+    # --device-warmup seconds, then the warm-up steps of the timed batch, then
+    # the timed steps, with no idle gap between them.  A GPU that was idle runs
+    # its first ~100 launches at lower clocks (the same clocks per wave take
+    # longer), which a short window would time; the reference's own protocol
+    # warms up for at least 10 GPU-seconds (scripts/benchmark_engines.py:485-
+    # 500).  The timed batch is exactly --warmup steps past its reset.
+    warm_launches = 0
+    if args.device_warmup > 0:
+        spare = CudaBatch(model, E, DT, ITERATIONS, 0, False)
+        spare.reset(torch.ones(E, dtype=torch.bool, device=dev), target.clone(),
+                    torch.zeros(E, 6, device=dev))
+        torch.cuda.synchronize()
+        t_warm = time.perf_counter()
+        while time.perf_counter() - t_warm < args.device_warmup:
+            for _ in range(20):
+                spare.step(target, forces, K, KP, 0.0)
+            warm_launches += 20
+            torch.cuda.synchronize()
     for _ in range(max(1, args.warmup // K)):
         batch.step(target, forces, K, KP, 0.0)
     torch.cuda.synchronize()
@@ -582,6 +604,10 @@ def main():
             "launch": "one physics step per kernel launch" if K == 1 else
                       f"{K} physics steps per kernel launch",
             "live_ground_contacts_per_env": contacts,
+            "device_warmup": {"seconds": args.device_warmup, "launches": warm_launches,
+                              "on": "a second batch of the same workload, right before the "
+                                    "timed batch's warm-up steps; the timed batch is exactly "
+                                    "`warmup` steps past its reset"},
         },
         "roofline": roofline(kernel_s, algo, E * K, "home", batch.kernel_info(), traffic),
         "cpu_baseline": None,
